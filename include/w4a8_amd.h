@@ -1,0 +1,127 @@
+/*
+ * w4a8_amd.h -- C ABI of the MI355X (gfx950) W4A8 per-group linear.
+ *
+ * This is the drop-in boundary for the reference's W4A8 dynamic linear
+ * (GongCheng1919/vllm-ascend910).  The reference binds its device kernels
+ * through torch.library C++ host impls; here the kernels sit behind plain
+ * extern "C" entry points (raw device pointers, int64 sizes, a HIP stream
+ * passed as void*), and the Python torch.library layer calls them through
+ * ctypes.  Nothing here allocates device memory: outputs and workspace are
+ * passed in by the caller, and every call is asynchronous on `stream`.
+ *
+ * Numeric contract (reference fakequant_lab/quant.py:89-141,
+ * fakequant_lab/fake_linear.py:155-179):
+ *   a_scale[m] = bf16_rne(max_k |x[m,k]| / 127), or bf16 tiny (2^-126) if 0
+ *   a_q[m,k]   = clamp(round_half_even(x[m,k] / a_scale[m]), -128, 127)
+ *   P_g[m,n]   = sum_{k in group g} a_q[m,k] * w_q[n,k]            (int32, exact)
+ *   y[m,n]     = bf16_rne( a_scale[m] * sum_g P_g[m,n] * w_scale[g,n] )  (fp32)
+ *
+ * Status codes: every entry point returns 0 on success or one of the
+ * W4A8_ERR_* codes; w4a8_last_error() returns a message for the calling
+ * thread's most recent failure.  Invalid arguments are rejected before any
+ * launch.
+ */
+#ifndef W4A8_AMD_H
+#define W4A8_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum w4a8_status {
+    W4A8_OK = 0,
+    W4A8_ERR_NULL = 1,        /* a required pointer is NULL */
+    W4A8_ERR_SHAPE = 2,       /* sizes are inconsistent or out of range */
+    W4A8_ERR_DTYPE = 3,       /* unknown dtype code */
+    W4A8_ERR_ALIGN = 4,       /* pointer / leading dimension alignment */
+    W4A8_ERR_UNSUPPORTED = 5, /* valid per the reference, not built here yet */
+    W4A8_ERR_WORKSPACE = 6,   /* workspace too small */
+    W4A8_ERR_HIP = 7          /* the HIP runtime reported an error */
+};
+
+/* Scale dtype codes. */
+enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
+
+/* Library ABI version (bumped on any signature change). */
+int w4a8_abi_version(void);
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char* w4a8_last_error(void);
+
+/*
+ * Dynamic per-token int8 activation quant.
+ *   x       bf16 [M, ldx]   (first K columns used)
+ *   a_q     int8 [M, lda]   (first K columns written)
+ *   a_scale bf16 [M]
+ * Replaces the reference's activation quantiser, kernel
+ * npu_ops/kernel/midgroup_quant_a.inc:112-410 bound by
+ * npu_ops/host/midgroup_quant_a.cpp:40-78, in its per-token mode
+ * (fakequant_lab/quant.py:153-173 with QuantSpec(8, None)); the reference's
+ * MSD planes and per-group activation scales are not produced here.
+ */
+int w4a8_quant_act(const void* x, int64_t ldx, void* a_q, int64_t lda, void* a_scale,
+                   int64_t M, int64_t K, void* stream);
+
+/*
+ * Sizes of the repacked (gfx950 MFMA operand order) weight and scale buffers.
+ * Weight: ceil(N/16) * ceil(kpad/128) tiles of 1024 bytes.  Scale:
+ * ceil(N/16) * ceil(K/group) * 16 entries of 2 bytes.
+ */
+int64_t w4a8_repacked_weight_bytes(int64_t N, int64_t K, int64_t group);
+int64_t w4a8_repacked_scale_bytes(int64_t N, int64_t K, int64_t group);
+
+/*
+ * Offline repacker.
+ *   w_q      int8 [N, kpad/2]  reference packed layout: two int4 per byte
+ *            along K, even k in the low nibble, each group zero-padded to a
+ *            multiple of 64 elements (npu_ops/python/w4a8_ops.py:142-148,
+ *            :231-239; npu_ops/kernel/mg_kgeom.h:90-102)
+ *   w_scale  fp16/bf16 [G, N] group-major (npu_ops/host/midgroup_w4a8_gemm.cpp:82-85)
+ *   w_tiles  output, w4a8_repacked_weight_bytes() bytes
+ *   s_tiles  output, w4a8_repacked_scale_bytes() bytes, same dtype as w_scale
+ * The reference has no repacker: its kernel reads w_q as stored.
+ */
+int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_tiles,
+                void* s_tiles, int64_t N, int64_t K, int64_t group, void* stream);
+
+/*
+ * Workspace bytes the GEMM needs for (M, N, K, group).  The workspace must be
+ * zero-filled before its first use; each call leaves its counter region at
+ * zero again, so one zeroed buffer can be reused by consecutive calls on one
+ * stream.  Calls that overlap in time must not share a workspace.
+ */
+int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
+
+/*
+ * The grouped W4A8 GEMM with fused scale epilogue.
+ *   a_q      int8 [M, lda]      (from w4a8_quant_act)
+ *   a_scale  bf16 [M]
+ *   w_tiles, s_tiles            (from w4a8_repack; scale_dtype as repacked)
+ *   y        bf16 [M, ldy]      output
+ * Replaces the reference GEMM, kernel npu_ops/kernel/midgroup_w4a8_gemm.inc:491-1169
+ * bound by npu_ops/host/midgroup_w4a8_gemm.cpp:45-140 (run_midgroup_w4a8_gemm),
+ * for symmetric weights and per-token activation scales.
+ */
+int w4a8_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
+              const void* s_tiles, int scale_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+              int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Parity hook: the same GEMM, which also writes every per-group int32 partial
+ *   partials int32 [G, M, N],  partials[g][m][n] = P_g[m,n]
+ * from the production kernel's own accumulators.  The reference computes the
+ * same quantity in fakequant_lab/fake_linear.py:175 (`partial`).
+ */
+int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale,
+                             const void* w_tiles, const void* s_tiles, int scale_dtype, void* y,
+                             int64_t ldy, void* partials, int64_t M, int64_t N, int64_t K,
+                             int64_t group, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A8_AMD_H */

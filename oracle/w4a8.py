@@ -1,0 +1,237 @@
+"""numpy restatement of the reference's CPU W4A8 path (test infrastructure only).
+
+Integer work is exact (int64 or fp32 matmuls of small integer codes whose sums
+stay below 2^24); floating-point steps use IEEE fp32 in the order the
+reference's torch code uses.  Citations are to files under the reference
+repository GongCheng1919/vllm-ascend910.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import numpy as np
+
+QMAX = {4: 7, 8: 127}     # fakequant_lab/quant.py:33
+QMIN = {4: -8, 8: -128}   # fakequant_lab/quant.py:34
+BF16_TINY_BITS = 0x0080   # torch.finfo(torch.bfloat16).tiny = 2^-126, quant.py:83-86
+GROUP_ALIGN = 64          # npu_ops/kernel/mg_kgeom.h:52 (kCubeKElemsInt4)
+
+
+# ------------------------------------------------------------------ bf16
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+
+    int4_cube_lab/host/bf16.h:17-27 (FP32ToBF16); torch's .to(torch.bfloat16).
+    """
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, ((u >> 16) | 0x40) & 0xFFFF, r)
+    return r.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    """bf16 bits -> fp32 (exact).  int4_cube_lab/host/bf16.h:9-15."""
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+def bf16_ulp(x: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 numbers at |x| (for normal x: 2^(floor(log2|x|) - 7))."""
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(x, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+# ------------------------------------------------------------------ geometry
+def num_groups(K: int, group: int) -> int:
+    """npu_ops/kernel/mg_kgeom.h:65-68."""
+    return -(-K // group)
+
+
+def group_real(g: int, K: int, group: int) -> int:
+    """npu_ops/kernel/mg_kgeom.h:77-81."""
+    G = num_groups(K, group)
+    return group if g + 1 < G else K - (G - 1) * group
+
+
+def group_stride(group: int) -> int:
+    """npu_ops/kernel/mg_kgeom.h:71-74."""
+    return -(-group // GROUP_ALIGN) * GROUP_ALIGN
+
+
+def kpad(K: int, group: int) -> int:
+    """npu_ops/kernel/mg_kgeom.h:98-102."""
+    G = num_groups(K, group)
+    return (G - 1) * group_stride(group) + -(-group_real(G - 1, K, group) // GROUP_ALIGN) * GROUP_ALIGN
+
+
+# ------------------------------------------------------------------ quantiser
+def group_params_sym(xg: np.ndarray, bits: int) -> np.ndarray:
+    """Symmetric scale per group along the last axis, as bf16 bits.
+
+    fakequant_lab/quant.py:102-105: scale = bf16(amax / qmax), tiny where zero.
+    """
+    amax = np.abs(xg.astype(np.float32)).max(axis=-1)
+    s = f32_to_bf16_bits(amax / np.float32(QMAX[bits]))
+    return np.where((s & 0x7FFF) == 0, np.uint16(BF16_TINY_BITS), s).astype(np.uint16)
+
+
+def group_params_asym(xg: np.ndarray, bits: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Asymmetric (scale, zero) per group, as bf16 bits.  fakequant_lab/quant.py:106-132."""
+    qmax, qmin = QMAX[bits], QMIN[bits]
+    x = xg.astype(np.float32)
+    mx, mn = x.max(axis=-1), x.min(axis=-1)
+    rng = mx - mn
+    s = f32_to_bf16_bits(rng / np.float32(qmax - qmin))
+    s = np.where(s == 0, np.uint16(BF16_TINY_BITS), s)           # where(scale == 0, tiny)
+    z = f32_to_bf16_bits(np.float32(qmin) - np.round(mn / bf16_bits_to_f32(s)))
+    const = rng == 0
+    sc = f32_to_bf16_bits(np.abs(mx) / np.float32(qmax))
+    sc = np.where(sc == 0, np.uint16(BF16_TINY_BITS), sc)
+    s = np.where(const, sc, s).astype(np.uint16)
+    z = np.where(const, np.uint16(0), z).astype(np.uint16)
+    return s, z
+
+
+def quantize_with(x: np.ndarray, scale_bits: np.ndarray, zero_bits: Optional[np.ndarray], bits: int) -> np.ndarray:
+    """fakequant_lab/quant.py:135-141: round_half_even(x / scale) (+ zero), clamp, int8.
+
+    ``scale_bits``/``zero_bits`` broadcast against x's last axis.
+    """
+    q = np.round(x.astype(np.float32) / bf16_bits_to_f32(scale_bits))   # np.round = half to even
+    if zero_bits is not None:
+        q = q + bf16_bits_to_f32(zero_bits)
+    return np.clip(q, QMIN[bits], QMAX[bits]).astype(np.int8)
+
+
+def quant_act_per_token(x_bits: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """Per-token int8 activation quant of a bf16 [M, K] (given as uint16 bits).
+
+    fakequant_lab/quant.py:153-173 with QuantSpec(8, None) (one group spanning K):
+    returns (a_q int8 [M, K], a_scale bf16 bits [M]).
+    """
+    x = bf16_bits_to_f32(x_bits)
+    s = group_params_sym(x, 8)
+    return quantize_with(x, s[:, None], None, 8), s
+
+
+def quantize_weight_sym(w: np.ndarray, group: int, bits: int = 4) -> Tuple[np.ndarray, np.ndarray]:
+    """Symmetric per-group weight quant of a float [N, K]: (codes int8 [N, K], scale bf16 bits [N, G]).
+
+    fakequant_lab/quant.py:153-173 with QuantSpec(4, group, sym=True); a ragged last
+    group is quantised on its real members (npu_ops/python/w4a8_ops.py:193-219).
+    """
+    N, K = w.shape
+    G = num_groups(K, group)
+    codes = np.empty((N, K), np.int8)
+    scales = np.empty((N, G), np.uint16)
+    for g in range(G):
+        sl = slice(g * group, g * group + group_real(g, K, group))
+        s = group_params_sym(w[:, sl], bits)
+        scales[:, g] = s
+        codes[:, sl] = quantize_with(w[:, sl], s[:, None], None, bits)
+    return codes, scales
+
+
+# ------------------------------------------------------------------ packing
+def pack_int4(v: np.ndarray) -> np.ndarray:
+    """[..., K] codes in [-8,7] -> [..., K/2] bytes, even k in the LOW nibble.
+
+    npu_ops/python/w4a8_ops.py:142-148; int4_cube_lab/host/gemm_ref.cpp:9-24.
+    """
+    v = np.asarray(v, np.int16)
+    lo = v[..., 0::2] & 0xF
+    hi = v[..., 1::2] & 0xF
+    return (lo | (hi << 4)).astype(np.uint8).view(np.int8)
+
+
+def unpack_int4(p: np.ndarray) -> np.ndarray:
+    b = np.asarray(p).view(np.uint8).astype(np.int16)
+    out = np.stack([b & 0xF, b >> 4], axis=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
+    return np.where(out >= 8, out - 16, out).astype(np.int8)
+
+
+def pack_grouped(codes: np.ndarray, group: int) -> np.ndarray:
+    """[N, K] codes -> [N, kpad/2] in the grouped zero-padded layout.
+
+    npu_ops/python/w4a8_ops.py:231-239; int4_cube_lab/host/gemm_ref.cpp:42-60.
+    """
+    N, K = codes.shape
+    padded = np.zeros((N, kpad(K, group)), np.int8)
+    for g in range(num_groups(K, group)):
+        r = group_real(g, K, group)
+        padded[:, g * group_stride(group):g * group_stride(group) + r] = codes[:, g * group:g * group + r]
+    return pack_int4(padded)
+
+
+# ------------------------------------------------------------------ GEMM
+def group_partials(a_q: np.ndarray, w_codes: np.ndarray, group: int, exact_int64: bool = False) -> np.ndarray:
+    """P[g, m, n] = sum_{k in g} a_q[m,k] * w[n,k] as int64 (exact).
+
+    fakequant_lab/fake_linear.py:173-175 (``partial = F.linear(a_g, q_w[:, sl])``, an
+    fp32 matmul of integer codes -- exact because |partial| <= 1024*group < 2^24);
+    ``exact_int64`` computes the same with int64 arithmetic
+    (fakequant_lab/run_selftest.py:115-116).
+    """
+    M, K = a_q.shape
+    N = w_codes.shape[0]
+    G = num_groups(K, group)
+    out = np.empty((G, M, N), np.int64)
+    for g in range(G):
+        sl = slice(g * group, g * group + group_real(g, K, group))
+        if exact_int64:
+            out[g] = a_q[:, sl].astype(np.int64) @ w_codes[:, sl].astype(np.int64).T
+        else:
+            out[g] = (a_q[:, sl].astype(np.float32) @ w_codes[:, sl].astype(np.float32).T).astype(np.int64)
+    return out
+
+
+def gemm_fp32(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray,
+              group: int, partials: Optional[np.ndarray] = None) -> np.ndarray:
+    """The reference's kernel-mode GEMM in fp32, per-token activation scale.
+
+    fakequant_lab/fake_linear.py:166-179: for g in order,
+        acc += partial_g * (a_s[:, g] * w_s[:, g])        (fp32; a_s*w_s is exact)
+    with the per-token a_s broadcast over groups (run_selftest.py:104-120 iterates
+    the groups of the weight spec).  ``w_scale`` is [N, G] fp32 values (bf16 or
+    fp16 scales, both exact in fp32).  Returns fp32 [M, N].
+    """
+    M, K = a_q.shape
+    N = w_codes.shape[0]
+    G = num_groups(K, group)
+    a_s = bf16_bits_to_f32(a_scale_bits).astype(np.float32)
+    if partials is None:
+        partials = group_partials(a_q, w_codes, group)
+    acc = np.zeros((M, N), np.float32)
+    for g in range(G):
+        s = (a_s[:, None] * w_scale[:, g].astype(np.float32)[None, :]).astype(np.float32)
+        acc = (acc + (partials[g].astype(np.float32) * s).astype(np.float32)).astype(np.float32)
+    return acc
+
+
+def gemm_f64(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray,
+             group: int, partials: Optional[np.ndarray] = None) -> np.ndarray:
+    """float64 restatement of fakequant_lab/run_selftest.py:104-120 (_exact_reference)."""
+    G = num_groups(a_q.shape[1], group)
+    a_s = bf16_bits_to_f32(a_scale_bits).astype(np.float64)
+    if partials is None:
+        partials = group_partials(a_q, w_codes, group, exact_int64=True)
+    acc = np.zeros((a_q.shape[0], w_codes.shape[0]), np.float64)
+    for g in range(G):
+        acc += partials[g].astype(np.float64) * (a_s[:, None] * w_scale[:, g].astype(np.float64)[None, :])
+    return acc
+
+
+def linear_bf16(x_bits: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray, group: int):
+    """Whole path: per-token quant -> group GEMM -> bf16 (fakequant_lab/fake_linear.py:142-153).
+
+    Returns (y bf16 bits [M,N], y fp32 [M,N], a_q, a_scale_bits, partials).
+    """
+    a_q, a_s = quant_act_per_token(x_bits)
+    P = group_partials(a_q, w_codes, group)
+    y32 = gemm_fp32(a_q, a_s, w_codes, w_scale, group, P)
+    return f32_to_bf16_bits(y32), y32, a_q, a_s, P

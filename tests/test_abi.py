@@ -1,0 +1,88 @@
+"""C ABI: the library loads, exports every symbol include/w4a8_amd.h declares,
+and rejects bad arguments on the host (before any launch, so these run
+without a GPU)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "w4a8_amd.h"
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(w4a8_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg._abi.lib()
+
+
+def test_header_symbols_are_exported(pkg, lib):
+    syms = declared_symbols()
+    assert len(syms) >= 9
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in {HEADER.name} but not exported"
+        assert s in pkg._abi.SIGNATURES, f"{s} has no ctypes signature"
+
+
+def test_version_and_sizes(lib):
+    assert lib.w4a8_abi_version() == 1
+    # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
+    assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
+    assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
+    assert lib.w4a8_repacked_scale_bytes(100, 512, 64) == 7 * 8 * 16 * 2
+    assert lib.w4a8_repacked_weight_bytes(0, 512, 64) == -1
+    # prefill path needs no workspace; decode split-K does, and is a pure function of shape
+    assert lib.w4a8_gemm_workspace_bytes(4096, 5120, 5120, 128) == 0
+    assert lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128) > 0
+    assert lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128) == lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128)
+
+
+def _gemm(lib, **kw):
+    a = dict(a_q=16, lda=256, a_scale=16, w_tiles=16, s_tiles=16, sd=0, y=16, ldy=64, M=4, N=64, K=256,
+             group=128, ws=None, wsb=0)
+    a.update(kw)
+    return lib.w4a8_gemm(a["a_q"], a["lda"], a["a_scale"], a["w_tiles"], a["s_tiles"], a["sd"], a["y"],
+                         a["ldy"], a["M"], a["N"], a["K"], a["group"], a["ws"], a["wsb"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(N=0), 2, "bad shape"),
+    (dict(M=-1), 2, "bad shape"),
+    (dict(K=300), 5, "ragged"),
+    (dict(group=96, K=960), 5, "group % 64"),
+    (dict(sd=7), 3, "scale_dtype"),
+    (dict(a_q=None), 1, "NULL"),
+    (dict(lda=100), 2, "lda"),
+    (dict(lda=264), 4, "16-byte"),
+    (dict(a_q=24), 4, "16-byte"),
+    (dict(M=16, N=5120, K=5120, ldy=5120, lda=5120), 6, "workspace"),
+])
+def test_gemm_rejects_bad_arguments(lib, kw, code, msg):
+    # Fake, never-dereferenced addresses: validation fails before any launch.
+    assert _gemm(lib, **kw) == code
+    assert msg in lib.w4a8_last_error().decode()
+
+
+def test_m0_is_a_noop(lib):
+    assert _gemm(lib, M=0, a_q=None, y=None) == 0
+
+
+def test_quant_and_repack_reject_bad_arguments(lib):
+    assert lib.w4a8_quant_act(None, 64, None, 64, None, 4, 64, None) == 1
+    assert lib.w4a8_quant_act(16, 32, 16, 64, 16, 4, 64, None) == 2
+    assert lib.w4a8_quant_act(None, 64, None, 64, None, 0, 64, None) == 0
+    assert lib.w4a8_repack(16, 16, 0, 16, 16, 64, 300, 128, None) == 5
+    assert lib.w4a8_repack(16, 16, 2, 16, 16, 64, 256, 128, None) == 3
+    assert lib.w4a8_repack(18, 16, 0, 16, 16, 64, 256, 128, None) == 4
+
+
+def test_errors_raise_runtimeerror_from_python(pkg):
+    with pytest.raises(RuntimeError, match="SHAPE"):
+        pkg._abi.check(_gemm(pkg._abi.lib(), N=0), "w4a8_gemm")

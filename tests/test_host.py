@@ -1,0 +1,67 @@
+"""Host-side logic on the CPU: torch weight preparation against the oracle,
+the Python geometry mirror, op schemas and fake kernels, and the refusal to
+run on CPU tensors (there is no CPU fallback)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w4a8 as ow
+
+
+@pytest.mark.parametrize("K,G", [(5120, 128), (1024, 64), (1057, 128), (100, 33), (33, 64), (777, 96)])
+def test_geometry_mirror(pkg, K, G):
+    g = pkg.geometry
+    assert g.num_groups(K, G) == ow.num_groups(K, G)
+    assert g.kpad(K, G) == ow.kpad(K, G)
+    assert all(g.group_real(i, K, G) == ow.group_real(i, K, G) for i in range(g.num_groups(K, G)))
+
+
+@pytest.mark.parametrize("N,K,G", [(64, 1024, 128), (48, 512, 64), (32, 1057, 128), (16, 100, 33)])
+def test_quantize_weight_matches_oracle(pkg, N, K, G):
+    rng = np.random.default_rng(N + K)
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    w[0, :5] = 0.0
+    w[1, :] = 0.0                                  # an all-zero row -> tiny scales
+    wt = torch.from_numpy(w).to(torch.bfloat16)
+    w_q, w_scale = pkg.packing.quantize_weight(wt, G)
+    codes, scales = ow.quantize_weight_sym(wt.float().numpy(), G)
+    assert np.array_equal(w_q.numpy(), ow.pack_grouped(codes, G))
+    assert np.array_equal(w_scale.view(torch.int16).numpy().view(np.uint16), scales.T)
+    if K % 2 == 0:
+        rt = pkg.packing.unpack_int4(pkg.packing.pack_int4(torch.from_numpy(codes)))
+        assert np.array_equal(rt.numpy(), codes)
+
+
+def test_synthetic_distributions(pkg):
+    s = pkg.synth
+    x = s.bf16_bits_to_f32(s.activations(64, 5120, 0))
+    big = np.abs(x).max(axis=0) > 8
+    assert 3 <= big.sum() <= 8                      # ~5 outlier channels of 5120
+    w = s.weight_codes_uniform(64, 512, 1)
+    assert w.min() == -8 and w.max() == 7
+    sc = s.scale_bits_to_f32(s.group_scales(64, 4, 2, "f16"), "f16")
+    assert sc.min() >= 0.0019 and sc.max() <= 0.0201
+
+
+def test_fake_kernels_give_shapes(pkg):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty((5, 1024), dtype=torch.bfloat16, device="cuda")
+        a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x)
+        assert a_q.shape == (5, 1024) and a_q.dtype == torch.int8 and a_s.shape == (5,)
+        w_q = torch.empty((300, 512), dtype=torch.int8, device="cuda")
+        ws = torch.empty((8, 300), dtype=torch.float16, device="cuda")
+        wt, st = torch.ops.npu.w4a8_repack(w_q, ws, 1024, 128)
+        assert wt.numel() == 19 * 8 * 1024 and tuple(st.shape) == (19, 8, 16)
+        y = torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, 300, 1024, 128)
+        assert y.shape == (5, 300) and y.dtype == torch.bfloat16
+        y2, P = torch.ops.npu.w4a8_gemm_partials(a_q, a_s, wt, st, 300, 1024, 128)
+        assert P.shape == (8, 5, 300) and P.dtype == torch.int32
+
+
+def test_cpu_tensors_are_refused(pkg):
+    x = torch.zeros((2, 64), dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        torch.ops.npu.w4a8_quant_pertoken(x)

@@ -1,0 +1,214 @@
+"""Pins the CPU oracle (oracle/w4a8.py) before it is trusted as the checker.
+
+Each check is independent of the oracle's own formula: exact rational
+arithmetic, brute-force integer sums, torch's conversions, and the reference's
+own C++ CPU reference compiled from its sources (oracle/_ref, skipped when the
+reference checkout was not available to build it).  Negative controls plant a
+plausible mistake in a copy of the oracle's inputs or arithmetic and show
+that the comparison catches it.
+"""
+from __future__ import annotations
+
+import subprocess
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref as oref
+from oracle import w4a8 as ow
+
+needs_ref = pytest.mark.skipif(not oref.available(), reason="oracle/_ref not built (reference checkout absent)")
+
+
+# --------------------------------------------------------------- exact helpers
+def round_to_float(fr: Fraction, mant_bits: int) -> Fraction:
+    """Round a positive rational to the nearest value with `mant_bits` significant bits, ties to even
+    (normal range only)."""
+    if fr == 0:
+        return Fraction(0)
+    e = fr.numerator.bit_length() - fr.denominator.bit_length()
+    while Fraction(2) ** e > fr:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= fr:
+        e += 1
+    ulp = Fraction(2) ** (e - mant_bits + 1)
+    q = fr / ulp
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return n * ulp
+
+
+def round_half_even(fr: Fraction) -> int:
+    n = fr.numerator // fr.denominator  # floor
+    rem = fr - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return n
+
+
+def exact_quant_row(xbits: np.ndarray):
+    """Per-token quant of one bf16 row in exact rational arithmetic."""
+    xs = [Fraction(float(v)) for v in ow.bf16_bits_to_f32(xbits)]
+    amax = max(abs(v) for v in xs)
+    s = round_to_float(round_to_float(amax / 127, 24), 8)     # fp32 divide, then bf16
+    if s == 0:
+        s = Fraction(2) ** -126
+    q = [max(-128, min(127, round_half_even(v / s))) for v in xs]
+    return s, q
+
+
+# --------------------------------------------------------------- bf16
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10,
+        np.array([0.0, -0.0, 1.0, np.inf, -np.inf, 3.4e38, 1e-40, -1e-40, 1.1754944e-38], np.float32),
+        # exact half-way points between bf16 neighbours (both parities)
+        (np.arange(0x3F800000, 0x3F800000 + 64, dtype=np.uint32) * 0 + 0x3F808000).view(np.float32),
+        np.array([0x3F818000, 0x3F828000, 0xBF818000], np.uint32).view(np.float32),
+    ])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ow.f32_to_bf16_bits(x), ref)
+
+
+@needs_ref
+def test_bf16_rounding_matches_reference_cpp():
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.standard_normal(5000).astype(np.float32) * 1e3,
+                        np.array([0x3F808000, 0x3F818000, 0x7FC00001, 0x7F800001], np.uint32).view(np.float32)])
+    assert np.array_equal(ow.f32_to_bf16_bits(x), oref.fp32_to_bf16(x))
+
+
+# --------------------------------------------------------------- quantiser
+def test_quant_per_token_matches_rational_arithmetic():
+    rng = np.random.default_rng(3)
+    M, K = 24, 96
+    x = rng.standard_normal((M, K)).astype(np.float32) * rng.uniform(0.01, 50, size=(M, 1)).astype(np.float32)
+    x[:, 7] *= 20  # an outlier channel
+    xb = ow.f32_to_bf16_bits(x)
+    q, s = ow.quant_act_per_token(xb)
+    for m in range(M):
+        s_exact, q_exact = exact_quant_row(xb[m])
+        assert Fraction(float(ow.bf16_bits_to_f32(s[m]))) == s_exact
+        assert q[m].tolist() == q_exact
+
+
+def test_quant_ties_round_half_to_even():
+    # amax = 127 -> scale exactly 1.0; every x/s below is an exact half-integer.
+    vals = np.array([127.0, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5, 126.5, -126.5], np.float32)
+    q, s = ow.quant_act_per_token(ow.f32_to_bf16_bits(vals)[None, :])
+    assert ow.bf16_bits_to_f32(s)[0] == 1.0
+    assert q[0].tolist() == [127, 2, 4, -2, -4, 0, 0, 2, 126, -126]
+
+
+def test_quant_zero_row_uses_bf16_tiny():
+    q, s = ow.quant_act_per_token(np.zeros((2, 64), np.uint16))
+    assert s.tolist() == [0x0080, 0x0080]
+    assert not q.any()
+
+
+def test_quant_tie_rows_match_rational_and_catch_reciprocal_multiply():
+    """On rows built from exact half-way quotients the oracle agrees with exact
+    rounding, while a reciprocal-multiply quantiser (the mistake the reference
+    warns about, npu_ops/kernel/midgroup_quant_a.inc:55-62) does not."""
+    from conftest import tie_rows
+    xb = tie_rows(48, 128, seed=4)
+    q, s = ow.quant_act_per_token(xb)
+    for m in range(xb.shape[0]):
+        s_exact, q_exact = exact_quant_row(xb[m])
+        assert Fraction(float(ow.bf16_bits_to_f32(s[m]))) == s_exact
+        assert q[m].tolist() == q_exact
+    xf = ow.bf16_bits_to_f32(xb)
+    recip = (np.float32(1.0) / ow.bf16_bits_to_f32(s)).astype(np.float32)
+    q_bad = np.clip(np.round(xf * recip[:, None]), -128, 127).astype(np.int8)
+    assert not np.array_equal(q_bad, q)
+
+
+# --------------------------------------------------------------- packing / geometry
+RAGGED_CASES = [(5120, 128), (27648, 128), (1057, 128), (1279, 256), (1025, 1024), (33, 64), (1, 64), (65, 64),
+                (63, 64), (2049, 512), (1023, 1024), (35, 32), (777, 96), (100, 33), (4096, 64)]
+
+
+def test_pack_roundtrip_exhaustive():
+    v = np.array([[a, b] for a in range(-8, 8) for b in range(-8, 8)], np.int8).reshape(1, -1)
+    p = ow.pack_int4(v)
+    assert np.array_equal(ow.unpack_int4(p), v)
+    assert ow.pack_int4(np.array([[1, -1]], np.int8)).view(np.uint8)[0, 0] == 0xF1
+
+
+@needs_ref
+@pytest.mark.parametrize("K,gk", RAGGED_CASES)
+def test_geometry_and_grouped_pack_match_reference(K, gk):
+    lib = oref.lib()
+    assert ow.num_groups(K, gk) == lib.ref_num_groups(K, gk)
+    assert ow.kpad(K, gk) == lib.ref_kpad(K, gk)
+    for g in range(ow.num_groups(K, gk)):
+        assert ow.group_real(g, K, gk) == lib.ref_group_real(g, K, gk)
+        assert g * ow.group_stride(gk) == lib.ref_group_offset(g, gk)
+    codes = np.random.default_rng(K).integers(-8, 8, size=(3, K)).astype(np.int8)
+    assert np.array_equal(ow.pack_grouped(codes, gk), oref.pack_int4_grouped(codes, gk))
+
+
+@needs_ref
+def test_reference_ragged_layout_binary_passes():
+    out = subprocess.run([str(oref.RAGGED_TEST)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and "ALL PASS" in out.stdout, out.stdout[-2000:]
+
+
+# --------------------------------------------------------------- GEMM
+def test_group_partials_fp32_path_is_exact():
+    rng = np.random.default_rng(5)
+    for M, N, K, G in ((5, 48, 1024, 1024), (17, 33, 640, 128), (3, 16, 192, 64)):
+        a = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+        w = rng.integers(-8, 8, size=(N, K)).astype(np.int8)
+        a[0, :] = -128
+        w[0, :] = -8   # extreme products: |P| reaches 1024*G
+        assert np.array_equal(ow.group_partials(a, w, G), ow.group_partials(a, w, G, exact_int64=True))
+        # brute force one entry
+        g = K // G - 1
+        assert ow.group_partials(a, w, G)[g, 1, 2] == sum(int(a[1, k]) * int(w[2, k]) for k in range(g * G, (g + 1) * G))
+
+
+def _gemm_case(seed, M=8, N=64, K=512, G=128):
+    rng = np.random.default_rng(seed)
+    xb = ow.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    w = rng.integers(-8, 8, size=(N, K)).astype(np.int8)
+    wsb = ow.f32_to_bf16_bits(rng.uniform(0.002, 0.02, size=(N, K // G)).astype(np.float32))
+    return xb, w, wsb
+
+
+def test_gemm_fp32_close_to_float64_definition():
+    xb, w, wsb = _gemm_case(6)
+    a_q, a_s = ow.quant_act_per_token(xb)
+    ws = ow.bf16_bits_to_f32(wsb)
+    y32 = ow.gemm_fp32(a_q, a_s, w, ws, 128)
+    y64 = ow.gemm_f64(a_q, a_s, w, ws, 128)
+    assert np.max(np.abs(y32 - y64)) <= 1e-6 * np.max(np.abs(y64))     # run_selftest.py:137-141 bar
+
+
+@needs_ref
+def test_gemm_bf16_matches_reference_cpp():
+    for seed, (M, N, K, G) in enumerate(((8, 64, 512, 128), (16, 128, 5120 // 4, 256), (4, 32, 1024, 64))):
+        xb, w, wsb = _gemm_case(seed + 10, M, N, K, G)
+        a_q, a_s = ow.quant_act_per_token(xb)
+        y = ow.f32_to_bf16_bits(ow.gemm_fp32(a_q, a_s, w, ow.bf16_bits_to_f32(wsb), G))
+        Gn = K // G
+        yr = oref.midgroup_gemm(a_q, np.repeat(a_s[None, :], Gn, axis=0), w, wsb.T.copy(), G)
+        d = np.abs(ow.bf16_bits_to_f32(y).astype(np.float64) - ow.bf16_bits_to_f32(yr))
+        assert np.all(d <= ow.bf16_ulp(ow.bf16_bits_to_f32(yr)))
+        assert np.mean(y == yr) > 0.99
+
+
+@needs_ref
+def test_gemm_negative_control_transposed_scales():
+    xb, w, wsb = _gemm_case(20, 8, 64, 512, 128)
+    a_q, a_s = ow.quant_act_per_token(xb)
+    G = 4
+    yr = oref.midgroup_gemm(a_q, np.repeat(a_s[None, :], G, axis=0), w, wsb.T.copy(), 128)
+    ws_bad = ow.bf16_bits_to_f32(wsb)[:, ::-1].copy()   # groups in the wrong order
+    y_bad = ow.f32_to_bf16_bits(ow.gemm_fp32(a_q, a_s, w, ws_bad, 128))
+    assert np.mean(y_bad == yr) < 0.5

@@ -1,0 +1,175 @@
+// extern "C" entry points declared in include/w4a8_amd.h.
+//
+// Every entry point validates its arguments on the host before launching and
+// reports failures as a status code plus a per-thread message, the way the
+// reference's host impls reject bad tensors with TORCH_CHECK before the launch
+// (npu_ops/host/midgroup_w4a8_gemm.cpp:51-85, npu_ops/host/midgroup_quant_a.cpp:42-43).
+// Nothing here allocates device memory or synchronises the stream.
+#include <stdint.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <string>
+
+#include "../../include/w4a8_amd.h"
+#include "kgeom.h"
+#include "launch.h"
+
+namespace w4a8 {
+
+// Planning constant: MI355X has 256 CUs.  Kept fixed (not queried) so that
+// workspace sizes are a pure function of the problem shape.
+int device_cu_count() { return 256; }
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, long long a = 0, long long b = 0, long long c = 0) {
+    char buf[512];
+    std::snprintf(buf, sizeof(buf), fmt, a, b, c);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return W4A8_OK;
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return W4A8_ERR_HIP;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_problem(int64_t M, int64_t N, int64_t K, int64_t group) {
+    if (M < 0 || N <= 0 || K <= 0 || group <= 0)
+        return fail(W4A8_ERR_SHAPE, "bad shape: M=%lld N=%lld K=%lld (need M>=0, N>0, K>0)", M, N, K);
+    if (M >= (1ll << 31) || N >= (1ll << 30) || K >= (1ll << 30))
+        return fail(W4A8_ERR_SHAPE, "shape too large: M=%lld N=%lld K=%lld", M, N, K);
+    if (!geom::is_slab_aligned(K, group))
+        return fail(W4A8_ERR_UNSUPPORTED,
+                    "K=%lld group=%lld: this build needs group %% 64 == 0 and K %% group == 0 "
+                    "(ragged-K groups are not implemented yet)", K, group);
+    return W4A8_OK;
+}
+
+int check_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
+               const void* s_tiles, int scale_dtype, const void* y, int64_t ldy, int64_t M,
+               int64_t N, int64_t K, int64_t group, const void* workspace,
+               int64_t workspace_bytes) {
+    if (int rc = check_problem(M, N, K, group)) return rc;
+    if (scale_dtype != W4A8_DT_F16 && scale_dtype != W4A8_DT_BF16)
+        return fail(W4A8_ERR_DTYPE, "scale_dtype %lld is neither F16 (0) nor BF16 (1)", scale_dtype);
+    if (M == 0) return W4A8_OK;
+    if (!a_q || !a_scale || !w_tiles || !s_tiles || !y) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (lda < K || ldy < N) return fail(W4A8_ERR_SHAPE, "lda=%lld must be >= K and ldy=%lld >= N", lda, ldy);
+    if (lda % 16 != 0 || !aligned(a_q, 16))
+        return fail(W4A8_ERR_ALIGN, "a_q must be 16-byte aligned with lda %% 16 == 0 (lda=%lld)", lda);
+    if (!aligned(w_tiles, 16) || !aligned(s_tiles, 2) || !aligned(y, 2) || !aligned(a_scale, 2))
+        return fail(W4A8_ERR_ALIGN, "w_tiles must be 16-byte aligned; s_tiles, y, a_scale 2-byte aligned");
+    const int64_t need = w4a8_gemm_workspace_bytes(M, N, K, group);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)))
+        return fail(W4A8_ERR_WORKSPACE, "workspace needs %lld bytes, 256-byte aligned (got %lld)", need,
+                    workspace ? workspace_bytes : 0);
+    return W4A8_OK;
+}
+
+int run_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
+             const void* s_tiles, int scale_dtype, void* y, int64_t ldy, void* partials,
+             int64_t M, int64_t N, int64_t K, int64_t group, void* workspace,
+             int64_t workspace_bytes, void* stream) {
+    if (int rc = check_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, M, N, K,
+                            group, workspace, workspace_bytes))
+        return rc;
+    if (M == 0) return W4A8_OK;
+    GemmArgs a{};
+    a.a_q = static_cast<const int8_t*>(a_q);
+    a.lda = lda;
+    a.a_scale = static_cast<const uint16_t*>(a_scale);
+    a.w_tiles = static_cast<const uint8_t*>(w_tiles);
+    a.s_tiles = static_cast<const uint16_t*>(s_tiles);
+    a.scale_bf16 = scale_dtype == W4A8_DT_BF16;
+    a.y = static_cast<uint16_t*>(y);
+    a.ldy = ldy;
+    a.partials = static_cast<int32_t*>(partials);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.group = group;
+    a.workspace = workspace;
+    a.workspace_bytes = workspace_bytes;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const hipError_t e = (M <= kDecodeMaxM) ? launch_gemm_decode(a, s) : launch_gemm_prefill(a, s);
+    return hip_status(e, "w4a8_gemm launch");
+}
+
+}  // namespace
+}  // namespace w4a8
+
+using namespace w4a8;
+
+extern "C" {
+
+int w4a8_abi_version(void) { return 1; }
+
+const char* w4a8_last_error(void) { return g_last_error.c_str(); }
+
+int w4a8_quant_act(const void* x, int64_t ldx, void* a_q, int64_t lda, void* a_scale, int64_t M,
+                   int64_t K, void* stream) {
+    if (M < 0 || K <= 0 || M >= (1ll << 31) || K >= (1ll << 31))
+        return fail(W4A8_ERR_SHAPE, "bad shape: M=%lld K=%lld", M, K);
+    if (M == 0) return W4A8_OK;
+    if (!x || !a_q || !a_scale) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (ldx < K || lda < K) return fail(W4A8_ERR_SHAPE, "ldx=%lld and lda=%lld must be >= K=%lld", ldx, lda, K);
+    if (!aligned(x, 2) || !aligned(a_scale, 2)) return fail(W4A8_ERR_ALIGN, "x and a_scale must be 2-byte aligned");
+    return hip_status(launch_quant_act(static_cast<const uint16_t*>(x), ldx, static_cast<int8_t*>(a_q), lda,
+                                       static_cast<uint16_t*>(a_scale), M, K, static_cast<hipStream_t>(stream)),
+                      "w4a8_quant_act launch");
+}
+
+int64_t w4a8_repacked_weight_bytes(int64_t N, int64_t K, int64_t group) {
+    if (N <= 0 || K <= 0 || group <= 0) return -1;
+    return geom::col_blocks(N) * geom::k_tiles(K, group) * geom::kTileBytes;
+}
+
+int64_t w4a8_repacked_scale_bytes(int64_t N, int64_t K, int64_t group) {
+    if (N <= 0 || K <= 0 || group <= 0) return -1;
+    return geom::col_blocks(N) * geom::num_groups(K, group) * 16 * 2;
+}
+
+int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_tiles, void* s_tiles,
+                int64_t N, int64_t K, int64_t group, void* stream) {
+    if (int rc = check_problem(0, N, K, group)) return rc;
+    if (scale_dtype != W4A8_DT_F16 && scale_dtype != W4A8_DT_BF16)
+        return fail(W4A8_ERR_DTYPE, "scale_dtype %lld is neither F16 (0) nor BF16 (1)", scale_dtype);
+    if (!w_q || !w_scale || !w_tiles || !s_tiles) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (!aligned(w_q, 4) || !aligned(w_tiles, 16) || !aligned(w_scale, 2) || !aligned(s_tiles, 2))
+        return fail(W4A8_ERR_ALIGN, "w_q must be 4-byte, w_tiles 16-byte, scales 2-byte aligned");
+    return hip_status(launch_repack(static_cast<const uint8_t*>(w_q), static_cast<const uint16_t*>(w_scale),
+                                    static_cast<uint8_t*>(w_tiles), static_cast<uint16_t*>(s_tiles), N, K,
+                                    group, static_cast<hipStream_t>(stream)),
+                      "w4a8_repack launch");
+}
+
+int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
+    if (M <= 0 || N <= 0 || K <= 0 || group <= 0 || !geom::is_slab_aligned(K, group)) return 0;
+    return (M <= kDecodeMaxM) ? decode_workspace_bytes(M, N, K, group) : prefill_workspace_bytes(M, N, K, group);
+}
+
+int w4a8_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles, const void* s_tiles,
+              int scale_dtype, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t group,
+              void* workspace, int64_t workspace_bytes, void* stream) {
+    return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, nullptr, M, N, K, group,
+                    workspace, workspace_bytes, stream);
+}
+
+int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
+                             const void* s_tiles, int scale_dtype, void* y, int64_t ldy, void* partials,
+                             int64_t M, int64_t N, int64_t K, int64_t group, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+    if (!partials && M > 0) return fail(W4A8_ERR_NULL, "partials is NULL");
+    if (partials && !aligned(partials, 4)) return fail(W4A8_ERR_ALIGN, "partials must be 4-byte aligned");
+    return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, partials, M, N, K, group,
+                    workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

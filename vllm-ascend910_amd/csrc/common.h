@@ -1,0 +1,59 @@
+// Device helpers shared by the W4A8 kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a8 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// bf16 bits -> fp32 (exact).
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp16 bits -> fp32 (exact).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quiet bit set).
+// Same rounding as the reference's host conversion (int4_cube_lab/host/bf16.h:17-27)
+// and torch's .to(torch.bfloat16).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// Scale entry -> fp32, for the two scale dtypes the op accepts.
+template <bool BF16>
+__device__ __forceinline__ float scale_to_f32(uint32_t bits) {
+    if constexpr (BF16) return bf16_bits_to_f32(bits);
+    else return f16_bits_to_f32(bits);
+}
+
+// One packed dword of the repacked weight holds 8 int4 codes: byte j carries
+// code k+j in its low nibble and code k+4+j in its high nibble.  Moving each
+// nibble into the HIGH half of a byte gives int8 lanes equal to 16*code, with
+// no sign handling: lo4 -> codes k..k+3, hi4 -> codes k+4..k+7.  The MFMA then
+// accumulates 16*P exactly; the factor is removed in the fp32 epilogue.
+__device__ __forceinline__ int unpack_lo4(uint32_t w) { return static_cast<int>((w << 4) & 0xf0f0f0f0u); }
+__device__ __forceinline__ int unpack_hi4(uint32_t w) { return static_cast<int>(w & 0xf0f0f0f0u); }
+
+// 16 packed bytes (32 codes, two 64-K slabs of 16 codes each for one lane) ->
+// the two MFMA B operands.
+__device__ __forceinline__ void unpack_tile_lane(const uint4 w, v4i& slab0, v4i& slab1) {
+    slab0 = v4i{unpack_lo4(w.x), unpack_hi4(w.x), unpack_lo4(w.y), unpack_hi4(w.y)};
+    slab1 = v4i{unpack_lo4(w.z), unpack_hi4(w.z), unpack_lo4(w.w), unpack_hi4(w.w)};
+}
+
+__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+}  // namespace w4a8

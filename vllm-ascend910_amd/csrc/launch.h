@@ -1,0 +1,45 @@
+// Internal launchers behind the C ABI.  Arguments are already validated by the
+// entry points in abi.hip; each launcher only picks a kernel variant and grid.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a8 {
+
+hipError_t launch_quant_act(const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t lda,
+                            uint16_t* a_scale, int64_t M, int64_t K, hipStream_t stream);
+
+hipError_t launch_repack(const uint8_t* w_q, const uint16_t* w_scale, uint8_t* w_tiles,
+                         uint16_t* s_tiles, int64_t N, int64_t K, int64_t group,
+                         hipStream_t stream);
+
+// Problem description shared by the GEMM paths.
+struct GemmArgs {
+    const int8_t* a_q;
+    int64_t lda;
+    const uint16_t* a_scale;   // bf16 [M]
+    const uint8_t* w_tiles;
+    const uint16_t* s_tiles;
+    bool scale_bf16;
+    uint16_t* y;               // bf16 [M, ldy]
+    int64_t ldy;
+    int32_t* partials;         // optional int32 [G, M, N]
+    int64_t M, N, K, group;
+    void* workspace;
+    int64_t workspace_bytes;
+};
+
+// Decode path (M <= kDecodeMaxM): weight-stream bound, split-K.
+constexpr int64_t kDecodeMaxM = 64;
+
+int64_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
+hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
+
+// Prefill path (M > kDecodeMaxM): MFMA bound, LDS-tiled.
+int64_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
+hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
+
+int device_cu_count();
+
+}  // namespace w4a8

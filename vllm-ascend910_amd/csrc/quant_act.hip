@@ -1,0 +1,143 @@
+// Dynamic per-token int8 activation quant (gfx950).
+//
+// Semantics follow the reference quantiser with a per-token spec
+// (fakequant_lab/quant.py:89-105 group_params, :135-141 quantize_with):
+//   s = bf16_rne(max|x| / 127)   -- fp32 divide, then rounded to bf16 BEFORE use
+//   s = bf16 tiny (2^-126)       -- when that bf16 value is zero
+//   q = clamp(rint(x / s), -128, 127), rint = round half to even, true fp32 divide
+// The divide is the IEEE one (the reference kernel insists on it,
+// npu_ops/kernel/midgroup_quant_a.inc:55-62): a reciprocal multiply would flip
+// half-way cases relative to torch.
+//
+// Layout: one 256-thread workgroup per row.  The row is read once with 16-byte
+// loads into registers, |x| is reduced as integers (for finite bf16 the
+// magnitude order equals the order of the 15 low bits), then the same
+// registers are quantised and written back as 8-byte int8 stores.
+#include "common.h"
+#include "launch.h"
+
+namespace w4a8 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint32_t kBf16Tiny = 0x0080u;  // 2^-126, torch.finfo(torch.bfloat16).tiny
+
+__device__ __forceinline__ uint32_t abs_bits_max2(uint32_t u) {
+    return max(u & 0x7fffu, (u >> 16) & 0x7fffu);
+}
+
+// Block-wide max of a uint32 over 256 threads.
+__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64)));
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    v = max(max(red[0], red[1]), max(red[2], red[3]));
+    return v;
+}
+
+// Scale from the absmax bits; returns bf16 bits of the stored scale.
+__device__ __forceinline__ uint32_t scale_from_amax(uint32_t amax_bits) {
+    const float amax = bf16_bits_to_f32(amax_bits);
+    uint32_t s = f32_to_bf16_bits(amax / 127.0f);
+    if ((s & 0x7fffu) == 0u) s = kBf16Tiny;
+    return s;
+}
+
+__device__ __forceinline__ int quant1(float x, float s) {
+    float q = rintf(x / s);
+    q = fminf(127.0f, fmaxf(-128.0f, q));
+    return static_cast<int>(q);
+}
+
+// Two bf16 in one dword -> two int8 codes in the low 16 bits.
+__device__ __forceinline__ uint32_t quant2(uint32_t u, float s) {
+    const int q0 = quant1(__uint_as_float(u << 16), s);
+    const int q1 = quant1(__uint_as_float(u & 0xffff0000u), s);
+    return (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8);
+}
+
+// Vector path: K % 8 == 0, rows 16-byte aligned, K <= VPT * 8 * 256.
+template <int VPT>
+__global__ __launch_bounds__(kThreads) void quant_act_vec_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ aq, int64_t lda,
+    uint16_t* __restrict__ ascale, int K) {
+    __shared__ uint32_t red[4];
+    const int64_t row = blockIdx.x;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    const int nvec = K >> 3;
+    uint4 v[VPT];
+    uint32_t amax = 0u;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+        v[i] = (idx < nvec) ? xr[idx] : make_uint4(0u, 0u, 0u, 0u);
+        amax = max(amax, max(max(abs_bits_max2(v[i].x), abs_bits_max2(v[i].y)),
+                             max(abs_bits_max2(v[i].z), abs_bits_max2(v[i].w))));
+    }
+    amax = block_max(amax, red);
+    const uint32_t sbits = scale_from_amax(amax);
+    const float s = bf16_bits_to_f32(sbits);
+    if (threadIdx.x == 0) ascale[row] = static_cast<uint16_t>(sbits);
+    uint2* qr = reinterpret_cast<uint2*>(aq + row * lda);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+        if (idx < nvec) {
+            uint2 o;
+            o.x = quant2(v[i].x, s) | (quant2(v[i].y, s) << 16);
+            o.y = quant2(v[i].z, s) | (quant2(v[i].w, s) << 16);
+            qr[idx] = o;
+        }
+    }
+}
+
+// General path: any K and strides; two passes over the row (the second one
+// hits cache).
+__global__ __launch_bounds__(kThreads) void quant_act_scalar_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ aq, int64_t lda,
+    uint16_t* __restrict__ ascale, int K) {
+    __shared__ uint32_t red[4];
+    const int64_t row = blockIdx.x;
+    const uint16_t* xr = x + row * ldx;
+    uint32_t amax = 0u;
+    for (int k = threadIdx.x; k < K; k += kThreads) amax = max(amax, static_cast<uint32_t>(xr[k]) & 0x7fffu);
+    amax = block_max(amax, red);
+    const uint32_t sbits = scale_from_amax(amax);
+    const float s = bf16_bits_to_f32(sbits);
+    if (threadIdx.x == 0) ascale[row] = static_cast<uint16_t>(sbits);
+    int8_t* qr = aq + row * lda;
+    for (int k = threadIdx.x; k < K; k += kThreads)
+        qr[k] = static_cast<int8_t>(quant1(bf16_bits_to_f32(xr[k]), s));
+}
+
+}  // namespace
+
+hipError_t launch_quant_act(const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t lda,
+                            uint16_t* a_scale, int64_t M, int64_t K, hipStream_t stream) {
+    if (M == 0) return hipSuccess;
+    const dim3 grid(static_cast<unsigned>(M));
+    const dim3 block(kThreads);
+    const bool aligned = (K % 8 == 0) && (ldx % 8 == 0) && (lda % 8 == 0) &&
+                         (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(a_q) % 8 == 0);
+    const int64_t nvec = K / 8;
+    const int iK = static_cast<int>(K);
+    if (aligned && nvec <= 1 * kThreads) {
+        quant_act_vec_kernel<1><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
+    } else if (aligned && nvec <= 2 * kThreads) {
+        quant_act_vec_kernel<2><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
+    } else if (aligned && nvec <= 4 * kThreads) {
+        quant_act_vec_kernel<4><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
+    } else if (aligned && nvec <= 8 * kThreads) {
+        quant_act_vec_kernel<8><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
+    } else if (aligned && nvec <= 16 * kThreads) {
+        quant_act_vec_kernel<16><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
+    } else {
+        quant_act_scalar_kernel<<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace w4a8

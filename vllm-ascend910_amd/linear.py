@@ -1,0 +1,84 @@
+"""W4A8 linear layer: the caller side of the op surface.
+
+``W4A8Linear`` reproduces the reference's vLLM linear method
+(npu_ops/python/midgroup_quant.py:102-178): parameters are created in the
+checkpoint layout (``weight_packed [N, kpad/2]`` int8, ``weight_scale [N, G]``,
+output_dim 0 so fused q/k/v and gate/up loaders can concatenate along N),
+``process_weights_after_loading`` converts them once into the kernel's layout
+(here: the gfx950 MFMA repack, instead of the reference's [N,G]->[G,N]
+transpose), and ``forward`` is the reference ``apply``: reshape to 2-D bf16,
+quantise, GEMM, add bias, reshape -- straight-line, no shape-dependent Python,
+so it can be captured in a HIP graph.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from . import geometry as geo
+from . import ops  # noqa: F401  (registers torch.ops.npu.*)
+from .packing import quantize_weight
+
+
+def linear(x: torch.Tensor, w_tiles: torch.Tensor, s_tiles: torch.Tensor, N: int, group: int,
+           bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x @ W.T with per-token int8 activations and per-group int4 weights.
+
+    The reference's ``w4a8_ops.linear`` (npu_ops/python/w4a8_ops.py:243-252).
+    """
+    lead, K = x.shape[:-1], x.shape[-1]
+    x2 = x.reshape(-1, K).to(torch.bfloat16).contiguous()
+    a_q, a_scale = torch.ops.npu.w4a8_quant_pertoken(x2)
+    y = torch.ops.npu.w4a8_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group)
+    if bias is not None:
+        y = y + bias
+    return y.reshape(*lead, N)
+
+
+class W4A8Linear(nn.Module):
+    """Drop-in W4A8 linear (symmetric int4 per-group weights, per-token int8 activations)."""
+
+    def __init__(self, in_features: int, out_features: int, group: int = 128, bias: bool = False,
+                 scale_dtype: torch.dtype = torch.bfloat16, device=None):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.group = group
+        K, N = in_features, out_features
+        G = geo.num_groups(K, group)
+        self.register_buffer("weight_packed", torch.zeros((N, geo.kpad(K, group) // 2), dtype=torch.int8,
+                                                          device=device))
+        self.register_buffer("weight_scale", torch.zeros((N, G), dtype=scale_dtype, device=device))
+        self.bias = nn.Parameter(torch.zeros(N, dtype=torch.bfloat16, device=device),
+                                 requires_grad=False) if bias else None
+        self.w_tiles: Optional[torch.Tensor] = None
+        self.s_tiles: Optional[torch.Tensor] = None
+
+    @classmethod
+    def from_float(cls, lin: nn.Linear, group: int = 128, scale_dtype: torch.dtype = torch.bfloat16
+                   ) -> "W4A8Linear":
+        """Quantise an nn.Linear's weight (symmetric RTN per group) and prepare it."""
+        N, K = lin.weight.shape
+        m = cls(K, N, group, lin.bias is not None, scale_dtype, device=lin.weight.device)
+        w_q, w_scale = quantize_weight(lin.weight.data, group, scale_dtype)
+        m.weight_packed.copy_(w_q)
+        m.weight_scale.copy_(w_scale.T)
+        if lin.bias is not None:
+            m.bias.data.copy_(lin.bias.data.to(torch.bfloat16))
+        m.process_weights_after_loading()
+        return m
+
+    def process_weights_after_loading(self) -> None:
+        """One-time conversion to the kernel layout (the reference transposes
+        scales to [G, N] here, npu_ops/python/midgroup_quant.py:148-161; this
+        build repacks weight and scales into MFMA operand order)."""
+        w_scale_gn = self.weight_scale.t().contiguous()
+        self.w_tiles, self.s_tiles = torch.ops.npu.w4a8_repack(self.weight_packed, w_scale_gn,
+                                                               self.in_features, self.group)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.w_tiles is None:
+            raise RuntimeError("W4A8Linear: call process_weights_after_loading() after loading weights")
+        return linear(x, self.w_tiles, self.s_tiles, self.out_features, self.group, self.bias)

@@ -1,0 +1,182 @@
+"""torch.ops.npu.* -- the W4A8 op surface on PyTorch-ROCm.
+
+Keeps the reference's registration namespace ``npu`` (the reference defines
+its ops with TORCH_LIBRARY_FRAGMENT(npu, ...), npu_ops/host/midgroup_quant_a.cpp:87-91
+and npu_ops/host/midgroup_w4a8_gemm.cpp:149-153) and adds the per-token /
+group-size-parameterised ops of this build:
+
+    torch.ops.npu.w4a8_quant_pertoken(x) -> (a_q, a_scale)
+    torch.ops.npu.w4a8_repack(w_q, w_scale, K, group) -> (w_tiles, s_tiles)
+    torch.ops.npu.w4a8_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> y
+    torch.ops.npu.w4a8_gemm_partials(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> (y, partials)
+
+Only the CUDA (= HIP on ROCm) dispatch key and fake (meta) kernels are
+registered: CPU tensors raise, there is no fallback path.  Each impl checks
+dtypes and shapes like the reference's host impls (TORCH_CHECK ->
+RuntimeError, npu_ops/host/midgroup_w4a8_gemm.cpp:51-85), allocates outputs
+with torch, and calls the C ABI on the current stream without synchronising.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, Tuple
+
+import torch
+
+from . import _abi
+from . import geometry as geo
+
+_LIB = torch.library.Library("npu", "FRAGMENT")
+_LIB.define("w4a8_quant_pertoken(Tensor x) -> (Tensor, Tensor)")
+_LIB.define("w4a8_repack(Tensor w_q, Tensor w_scale, int K, int group) -> (Tensor, Tensor)")
+_LIB.define("w4a8_gemm(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
+            "int N, int K, int group) -> Tensor")
+_LIB.define("w4a8_gemm_partials(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
+            "int N, int K, int group) -> (Tensor, Tensor)")
+
+_SCALE_DT = {torch.float16: _abi.W4A8_DT_F16, torch.bfloat16: _abi.W4A8_DT_BF16}
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+# One zero-filled workspace per (device, stream).  The library leaves its
+# counter region at zero after every call, so the buffer is reused as is; it
+# only grows.  Concurrent calls on one stream are stream-ordered, so sharing
+# per stream is safe.
+_WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(dev: torch.device, need: int) -> torch.Tensor:
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------- quant
+@torch.library.impl(_LIB, "w4a8_quant_pertoken", "CUDA")
+def _quant_pertoken_cuda(x: torch.Tensor):
+    _require(x.dim() == 2, "w4a8_quant_pertoken: x must be [M, K]")
+    _require(x.dtype == torch.bfloat16, "w4a8_quant_pertoken: x must be bfloat16")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    a_q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    a_scale = torch.empty((M,), dtype=torch.bfloat16, device=x.device)
+    if M:
+        _abi.check(_abi.lib().w4a8_quant_act(x.data_ptr(), x.stride(0), a_q.data_ptr(), K,
+                                             a_scale.data_ptr(), M, K, _stream(x.device)),
+                   "w4a8_quant_pertoken")
+    return a_q, a_scale
+
+
+@torch.library.register_fake("npu::w4a8_quant_pertoken")
+def _quant_pertoken_fake(x):
+    M, K = x.shape
+    return x.new_empty((M, K), dtype=torch.int8), x.new_empty((M,), dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------- repack
+def _check_ref_weight(w_q, w_scale, K, group):
+    _require(w_q.dim() == 2 and w_q.dtype in (torch.int8, torch.uint8),
+             "w4a8_repack: w_q must be a 2-D int8 [N, kpad/2] packed-int4 tensor")
+    _require(w_scale.dtype in _SCALE_DT, "w4a8_repack: w_scale must be float16 or bfloat16")
+    N = w_q.shape[0]
+    G = geo.num_groups(K, group)
+    _require(w_q.shape[1] == geo.kpad(K, group) // 2,
+             f"w4a8_repack: packed row length must be kpad/2 = {geo.kpad(K, group) // 2} "
+             f"for K={K}, group={group}; got {w_q.shape[1]}")
+    _require(tuple(w_scale.shape) == (G, N), f"w4a8_repack: w_scale must be group-major [{G}, {N}]")
+    return N, G
+
+
+@torch.library.impl(_LIB, "w4a8_repack", "CUDA")
+def _repack_cuda(w_q: torch.Tensor, w_scale: torch.Tensor, K: int, group: int):
+    N, G = _check_ref_weight(w_q, w_scale, K, group)
+    w_q = w_q.contiguous()
+    w_scale = w_scale.contiguous()
+    w_tiles = torch.empty((geo.repacked_weight_bytes(N, K, group),), dtype=torch.uint8, device=w_q.device)
+    s_tiles = torch.empty(geo.repacked_scale_shape(N, K, group), dtype=w_scale.dtype, device=w_q.device)
+    _abi.check(_abi.lib().w4a8_repack(w_q.data_ptr(), w_scale.data_ptr(), _SCALE_DT[w_scale.dtype],
+                                      w_tiles.data_ptr(), s_tiles.data_ptr(), N, K, group,
+                                      _stream(w_q.device)), "w4a8_repack")
+    return w_tiles, s_tiles
+
+
+@torch.library.register_fake("npu::w4a8_repack")
+def _repack_fake(w_q, w_scale, K, group):
+    N = w_q.shape[0]
+    return (w_q.new_empty((geo.repacked_weight_bytes(N, K, group),), dtype=torch.uint8),
+            w_scale.new_empty(geo.repacked_scale_shape(N, K, group)))
+
+
+# ---------------------------------------------------------------- gemm
+def _check_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group):
+    _require(a_q.dim() == 2 and a_q.dtype == torch.int8, "w4a8_gemm: a_q must be int8 [M, K]")
+    _require(a_q.shape[1] == K, f"w4a8_gemm: a_q has {a_q.shape[1]} columns, K={K}")
+    _require(a_scale.dtype == torch.bfloat16 and a_scale.dim() == 1 and a_scale.shape[0] == a_q.shape[0],
+             "w4a8_gemm: a_scale must be bfloat16 [M]")
+    _require(w_tiles.dtype == torch.uint8 and w_tiles.numel() == geo.repacked_weight_bytes(N, K, group),
+             "w4a8_gemm: w_tiles must be the uint8 output of w4a8_repack for (N, K, group)")
+    _require(s_tiles.dtype in _SCALE_DT and tuple(s_tiles.shape) == geo.repacked_scale_shape(N, K, group),
+             "w4a8_gemm: s_tiles must be the scale output of w4a8_repack for (N, K, group)")
+
+
+def _run_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group, partials):
+    _check_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group)
+    if a_q.stride(1) != 1 or a_q.stride(0) % 16:
+        a_q = a_q.contiguous()
+    a_scale = a_scale.contiguous()
+    M = a_q.shape[0]
+    dev = a_q.device
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    if M == 0:
+        return y
+    lib = _abi.lib()
+    need = lib.w4a8_gemm_workspace_bytes(M, N, K, group)
+    ws = _workspace(dev, need) if need > 0 else None
+    ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+    args_head = (a_q.data_ptr(), a_q.stride(0), a_scale.data_ptr(), w_tiles.data_ptr(), s_tiles.data_ptr(),
+                 _SCALE_DT[s_tiles.dtype], y.data_ptr(), N)
+    if partials is None:
+        st = lib.w4a8_gemm(*args_head, M, N, K, group, ws_ptr, ws_bytes, _stream(dev))
+    else:
+        st = lib.w4a8_gemm_debug_partials(*args_head, partials.data_ptr(), M, N, K, group, ws_ptr, ws_bytes,
+                                          _stream(dev))
+    _abi.check(st, "w4a8_gemm")
+    return y
+
+
+@torch.library.impl(_LIB, "w4a8_gemm", "CUDA")
+def _gemm_cuda(a_q, a_scale, w_tiles, s_tiles, N: int, K: int, group: int):
+    return _run_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group, None)
+
+
+@torch.library.register_fake("npu::w4a8_gemm")
+def _gemm_fake(a_q, a_scale, w_tiles, s_tiles, N, K, group):
+    return a_q.new_empty((a_q.shape[0], N), dtype=torch.bfloat16)
+
+
+@torch.library.impl(_LIB, "w4a8_gemm_partials", "CUDA")
+def _gemm_partials_cuda(a_q, a_scale, w_tiles, s_tiles, N: int, K: int, group: int):
+    M = a_q.shape[0]
+    partials = torch.empty((geo.num_groups(K, group), M, N), dtype=torch.int32, device=a_q.device)
+    y = _run_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group, partials)
+    return y, partials
+
+
+@torch.library.register_fake("npu::w4a8_gemm_partials")
+def _gemm_partials_fake(a_q, a_scale, w_tiles, s_tiles, N, K, group):
+    M = a_q.shape[0]
+    return (a_q.new_empty((M, N), dtype=torch.bfloat16),
+            a_q.new_empty((geo.num_groups(K, group), M, N), dtype=torch.int32))
