@@ -87,9 +87,10 @@ int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_t
                 void* s_tiles, int64_t N, int64_t K, int64_t group, void* stream);
 
 /*
- * Workspace bytes the GEMM needs for (M, N, K, group).  The workspace must be
- * zero-filled before its first use; each call leaves its counter region at
- * zero again, so one zeroed buffer can be reused by consecutive calls on one
+ * Workspace bytes the GEMM needs for (M, N, K, group); 0 when none.  A
+ * non-empty workspace starts with a fixed 256 KiB counter region that must be
+ * zero before the buffer's first use; every call leaves it zero again (whatever
+ * its shape), so one zeroed buffer can be reused by consecutive calls on one
  * stream.  Calls that overlap in time must not share a workspace.
  */
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);

@@ -191,26 +191,43 @@ def group_partials(a_q: np.ndarray, w_codes: np.ndarray, group: int, exact_int64
 
 
 def gemm_fp32(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray,
-              group: int, partials: Optional[np.ndarray] = None) -> np.ndarray:
+              group: int, partials: Optional[np.ndarray] = None, return_abs: bool = False):
     """The reference's kernel-mode GEMM in fp32, per-token activation scale.
 
     fakequant_lab/fake_linear.py:166-179: for g in order,
         acc += partial_g * (a_s[:, g] * w_s[:, g])        (fp32; a_s*w_s is exact)
     with the per-token a_s broadcast over groups (run_selftest.py:104-120 iterates
     the groups of the weight spec).  ``w_scale`` is [N, G] fp32 values (bf16 or
-    fp16 scales, both exact in fp32).  Returns fp32 [M, N].
+    fp16 scales, both exact in fp32).  Returns fp32 [M, N]; with ``return_abs``
+    also the float64 sum of |partial_g * a_s * w_s| over groups, the magnitude
+    that bounds any fp32 summation error (see ``fp32_sum_error_bound``).
+    Partials are computed group by group unless given.
     """
     M, K = a_q.shape
     N = w_codes.shape[0]
     G = num_groups(K, group)
     a_s = bf16_bits_to_f32(a_scale_bits).astype(np.float32)
-    if partials is None:
-        partials = group_partials(a_q, w_codes, group)
     acc = np.zeros((M, N), np.float32)
+    mag = np.zeros((M, N), np.float64) if return_abs else None
     for g in range(G):
+        if partials is not None:
+            pg = partials[g]
+        else:
+            sl = slice(g * group, g * group + group_real(g, K, group))
+            pg = a_q[:, sl].astype(np.float32) @ w_codes[:, sl].astype(np.float32).T
         s = (a_s[:, None] * w_scale[:, g].astype(np.float32)[None, :]).astype(np.float32)
-        acc = (acc + (partials[g].astype(np.float32) * s).astype(np.float32)).astype(np.float32)
-    return acc
+        term = (pg.astype(np.float32) * s).astype(np.float32)
+        acc = (acc + term).astype(np.float32)
+        if return_abs:
+            mag += np.abs(term.astype(np.float64))
+    return (acc, mag) if return_abs else acc
+
+
+def fp32_sum_error_bound(mag: np.ndarray, n_groups: int) -> np.ndarray:
+    """Worst-case |fp32 result - exact| for a sequential fp32 sum of n_groups
+    rounded products plus a final scaling: (n_groups + 2) * 2^-24 * sum|terms|
+    (the textbook recursive-summation bound, gamma_n = n*u)."""
+    return (n_groups + 2) * 2.0 ** -24 * mag
 
 
 def gemm_f64(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray,

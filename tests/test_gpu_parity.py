@@ -3,8 +3,9 @@
 Bars (stated per test):
   * activation quant: int8 codes and bf16 scales byte-exact
   * per-group int32 partials (dumped by the production kernel): bit-exact
-  * bf16 output: |y - y32| <= 1 bf16 ulp of the oracle's fp32 result y32 for every
-    element, and rel-L2(y, y32) <= 1e-3
+  * bf16 output: |y - y32| <= 1 bf16 ulp of the oracle's fp32 result y32 (plus the
+    fp32 summation bound where groups cancel, see check_output) for every element,
+    rel-L2 against the oracle's bf16 output <= 1e-3, and >= 99% of outputs equal
 """
 from __future__ import annotations
 
@@ -49,15 +50,26 @@ def run_hip(dev, xb, w, w_scale, N, K, G, partials=True):
     return y, P, a_q, a_s
 
 
-def check_output(y_bits: np.ndarray, y32: np.ndarray, tag: str) -> None:
+def check_output(y_bits: np.ndarray, y32: np.ndarray, mag: np.ndarray, n_groups: int, tag: str) -> None:
+    """Output bars.
+
+    max-abs: |y - y32| <= 1 bf16 ulp of the oracle's fp32 result y32, widened by
+    the fp32 summation error both sides may carry, 2 * (G+2) * 2^-24 * sum_g|term_g|.
+    The widening only matters where the groups cancel (|y32| far below the
+    terms); there the fp32 oracle is itself that inexact.
+    rel-L2: between the bf16 outputs (ours vs the oracle's bf16(y32), which is
+    what the reference's path returns, fakequant_lab/fake_linear.py:149) <= 1e-3.
+    """
     y = ow.bf16_bits_to_f32(y_bits).astype(np.float64)
     r = y32.astype(np.float64)
     err = np.abs(y - r)
-    ulp = ow.bf16_ulp(r)
-    bad = err > ulp
-    assert not bad.any(), f"{tag}: {bad.sum()} outputs off by more than 1 bf16 ulp (max err {err.max()})"
-    rel = np.linalg.norm(y - r) / max(np.linalg.norm(r), 1e-30)
+    tol = ow.bf16_ulp(r) + 2 * ow.fp32_sum_error_bound(mag, n_groups)
+    bad = err > tol
+    assert not bad.any(), f"{tag}: {bad.sum()} outputs outside 1 bf16 ulp + fp32 sum bound (max err {err.max()})"
+    rb = ow.round_bf16(y32).astype(np.float64)
+    rel = np.linalg.norm(y - rb) / max(np.linalg.norm(rb), 1e-30)
     assert rel <= 1e-3, f"{tag}: rel-L2 {rel}"
+    assert np.mean(y == rb) > 0.99, f"{tag}: only {np.mean(y == rb):.4f} of outputs equal bf16(oracle)"
     assert np.linalg.norm(r) > 0, f"{tag}: vacuous reference"
 
 
@@ -164,8 +176,8 @@ def test_gemm_partials_bit_exact_and_output(pkg, dev, M, N, K, G, sd):
     assert np.array_equal(a_q.cpu().numpy(), q_ref)
     P_ref = ow.group_partials(q_ref, w, G)
     assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
-    y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref)
-    check_output(tensor_bf16_bits(y), y32, f"M{M} N{N} K{K} G{G}")
+    y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref, return_abs=True)
+    check_output(tensor_bf16_bits(y), y32, mag, K // G, f"M{M} N{N} K{K} G{G}")
 
 
 @pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
@@ -176,8 +188,8 @@ def test_gemm_qwq_decode_shapes(pkg, dev, proj, M):
     xb, w, ws32, w_scale = make_problem(pkg, M, N, K, 128, seed=M)
     y, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, 128, partials=False)
     q_ref, s_ref = ow.quant_act_per_token(xb)
-    y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, 128)
-    check_output(tensor_bf16_bits(y), y32, f"{proj} M{M}")
+    y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, 128, return_abs=True)
+    check_output(tensor_bf16_bits(y), y32, mag, K // 128, f"{proj} M{M}")
 
 
 @pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
@@ -191,8 +203,8 @@ def test_gemm_qwq_prefill_column_sample(pkg, dev, proj):
     y, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, 128, partials=False)
     cols = np.sort(np.random.default_rng(0).choice(N, 192, replace=False))
     q_ref, s_ref = ow.quant_act_per_token(xb)
-    y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], 128)
-    check_output(tensor_bf16_bits(y)[:, cols], y32, f"{proj} M{M}")
+    y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], 128, return_abs=True)
+    check_output(tensor_bf16_bits(y)[:, cols], y32, mag, K // 128, f"{proj} M{M}")
 
 
 def test_gemm_deterministic_and_stress(pkg, dev):
@@ -247,3 +259,17 @@ def test_w4a8_linear_module(pkg, dev):
              + lin.bias.detach().cpu()).float().numpy()
     got = y.reshape(-1, N).float().cpu().numpy()
     assert np.max(np.abs(got - y_ref) - 2 * ow.bf16_ulp(y_ref)) <= 0
+
+
+def test_workspace_reuse_across_shapes(pkg, dev):
+    """Regression: consecutive split-K calls of different shapes share one
+    workspace; a small-N call's partials must not leave non-zero counters for a
+    later wide-N call."""
+    cases = [(16, 256, 4096, 128), (1, 32768, 1024, 128), (8, 1024, 8192, 256), (1, 32768, 1024, 128)]
+    for i, (M, N, K, G) in enumerate(cases):
+        say(f"workspace reuse step {i}: M={M} N={N} K={K} G={G}")
+        xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=40 + i)
+        y, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, G, partials=False)
+        q_ref, s_ref = ow.quant_act_per_token(xb)
+        y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, return_abs=True)
+        check_output(tensor_bf16_bits(y), y32, mag, K // G, f"reuse step {i}")

@@ -36,6 +36,11 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kPF = 8;             // tiles in flight per wave (register ring depth)
 constexpr int kLdsBudget = 40960;  // bytes of A staging per workgroup
+// Split-K arrival counters live in a FIXED region at the start of the
+// workspace, one uint32 per column group, so that no call's partials ever
+// overlap another call's counters: the region stays zero between calls.
+constexpr int64_t kCounterBytes = 256 * 1024;
+constexpr int64_t kMaxCounters = kCounterBytes / 4;
 
 template <int MT>
 struct DecodeCfg {
@@ -280,6 +285,7 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int64_t target = 4 * static_cast<int64_t>(device_cu_count());
     int ks = static_cast<int>(std::max<int64_t>(1, (target + pl.ncg - 1) / pl.ncg));
     ks = std::min(ks, units);
+    if (pl.ncg > kMaxCounters) ks = 1;  // wide N has enough column groups without split-K
     const int ups = (units + ks - 1) / ks;
     pl.tps = ups * unit;
     pl.ksplit = (KT + pl.tps - 1) / pl.tps;
@@ -303,14 +309,12 @@ hipError_t launch_sd(const DecodeParams& p, const DecodePlan& pl, hipStream_t st
     }
 }
 
-constexpr int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
-
 }  // namespace
 
 int64_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
     const DecodePlan pl = plan_decode(M, N, K, group);
     if (pl.ksplit <= 1) return 0;
-    return align256(pl.ncg * 4) + static_cast<int64_t>(pl.ksplit) * M * N * 4;
+    return kCounterBytes + static_cast<int64_t>(pl.ksplit) * M * N * 4;
 }
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
@@ -335,7 +339,7 @@ hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
     p.ksplit = pl.ksplit;
     if (pl.ksplit > 1) {
         p.cnt = reinterpret_cast<uint32_t*>(a.workspace);
-        p.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + align256(pl.ncg * 4));
+        p.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes);
     }
     const bool dump = a.partials != nullptr;
     if (a.scale_bf16) return dump ? launch_sd<true, true>(p, pl, stream) : launch_sd<true, false>(p, pl, stream);
