@@ -38,10 +38,9 @@ def test_version_and_sizes(lib):
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
     assert lib.w4a8_repacked_scale_bytes(100, 512, 64) == 7 * 8 * 16 * 2
     assert lib.w4a8_repacked_weight_bytes(0, 512, 64) == -1
-    # prefill path needs no workspace; decode split-K does, and is a pure function of shape
+    # neither path needs a workspace (decode reduces its K split inside a workgroup)
     assert lib.w4a8_gemm_workspace_bytes(4096, 5120, 5120, 128) == 0
-    assert lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128) > 0
-    assert lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128) == lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128)
+    assert lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128) == 0
 
 
 def _gemm(lib, **kw):
@@ -62,7 +61,6 @@ def _gemm(lib, **kw):
     (dict(lda=100), 2, "lda"),
     (dict(lda=264), 4, "16-byte"),
     (dict(a_q=24), 4, "16-byte"),
-    (dict(M=16, N=5120, K=5120, ldy=5120, lda=5120), 6, "workspace"),
 ])
 def test_gemm_rejects_bad_arguments(lib, kw, code, msg):
     # Fake, never-dereferenced addresses: validation fails before any launch.

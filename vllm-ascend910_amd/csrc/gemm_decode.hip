@@ -7,22 +7,19 @@
 // CPU definition fakequant_lab/fake_linear.py:155-179) in its per-token,
 // symmetric special case.
 //
-// Work split.  Each 256-thread workgroup owns 4*CPW column blocks of 16 and a
-// contiguous, group-aligned range of 128-K weight tiles (split-K over
-// blockIdx.y).  Each wave streams its own column block(s): one 16-byte load
-// per lane per tile (1 KB per wave), kept PF tiles ahead in a register ring so
-// that many loads are in flight per CU.  The activations for the workgroup's
-// K range are staged through LDS in chunks of TC tiles and shared by the four
-// waves.  Per 64-K slab each wave issues MT*CPW v_mfma_i32_16x16x64_i8 (16 rows
-// of A by 16 columns of B); at each group end the int32 accumulators are folded
-// into fp32: acc += float(16*P) * w_scale.  The token scale and the 1/16 of the
-// nibble unpack are applied once at the end (both exact power-of-two / single
-// multiplies, see common.h).
-//
-// Split-K reduction is deterministic: every split writes its fp32 partial to
-// the workspace, and the last workgroup to arrive at a column group (counted
-// with a device-scope atomic) sums the partials in split order and writes bf16.
-// It then resets the counter, so the workspace counters stay zero between calls.
+// Work split.  A workgroup owns CPW column blocks of 16 (16*CPW output
+// columns) and ALL of K; its KW waves split K into contiguous, group-aligned
+// ranges.  Each wave streams its range: per 128-K tile one 16-byte load per
+// lane per column block (the repacked tile, 1 KB) plus MT*2 16-byte loads of
+// activations (L2-resident; rows >= M are masked), held D tiles ahead in a
+// register ring.  Every load is unconditional -- addresses are clamped into
+// the buffers and the values masked afterwards -- so the compiler can count
+// loads in flight exactly and the ring really overlaps.  Per 64-K slab each
+// wave issues MT*CPW v_mfma_i32_16x16x64_i8; at each group end the int32
+// accumulators fold into fp32 (acc += float(16*P) * w_scale).  The KW partial
+// sums are reduced through LDS in a fixed order, and the token scale and the
+// 1/16 of the nibble unpack are applied once at the end.  No workspace, no
+// inter-workgroup communication, deterministic results.
 #include <algorithm>
 
 #include "common.h"
@@ -31,25 +28,6 @@
 
 namespace w4a8 {
 namespace {
-
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kPF = 8;             // tiles in flight per wave (register ring depth)
-constexpr int kLdsBudget = 40960;  // bytes of A staging per workgroup
-// Split-K arrival counters live in a FIXED region at the start of the
-// workspace, one uint32 per column group, so that no call's partials ever
-// overlap another call's counters: the region stays zero between calls.
-constexpr int64_t kCounterBytes = 256 * 1024;
-constexpr int64_t kMaxCounters = kCounterBytes / 4;
-
-template <int MT>
-struct DecodeCfg {
-    static constexpr int kRows = 16 * MT;
-    // Tiles per A chunk, so that rows * (TC*128 + 16) <= kLdsBudget.
-    static constexpr int kTC = ((kLdsBudget / kRows) - 16) / 128;
-    static constexpr int kLStride = kTC * 128 + 16;  // +16 B per row against bank conflicts
-    static constexpr int kLdsBytes = kRows * kLStride;
-};
 
 struct DecodeParams {
     const int8_t* A;
@@ -60,61 +38,69 @@ struct DecodeParams {
     uint16_t* Y;
     int64_t ldy;
     int32_t* P;        // optional partial dump [NG, M, N]
-    float* part;       // split-K partials [ksplit, M, N]
-    uint32_t* cnt;     // split-K arrival counters [ncg]
     int M, N, K;
     int KT, NG, NB;
     int spg;           // 64-K slabs per group
-    int tps;           // tiles per split
-    int ksplit;
+    int unit;          // tiles per K-split unit (group and tile aligned)
+    int units;         // ceil(KT / unit)
 };
 
-template <int MT, int CPW, bool SBF16, bool DUMP>
-__global__ __launch_bounds__(kThreads) void gemm_decode_kernel(const DecodeParams p) {
-    using Cfg = DecodeCfg<MT>;
-    __shared__ __attribute__((aligned(16))) int8_t lds[Cfg::kLdsBytes];
-    __shared__ uint32_t s_last;
+template <int MT, int CPW, int KW, int D, bool SBF16, bool DUMP>
+__global__ __launch_bounds__(64 * KW) void gemm_decode_kernel(const DecodeParams p) {
+    constexpr int R = 16 * MT;
+    constexpr int C = 16 * CPW;
+    __shared__ float red[KW * R * C];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int t0 = blockIdx.y * p.tps;
-    const int t1 = min(p.KT, t0 + p.tps);
-    const int nbw = (blockIdx.x * kWaves + wave) * CPW;
+    // Wave-uniform by construction; readfirstlane tells the compiler so, which
+    // keeps the tile loop and fold conditions scalar branches.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb0 = blockIdx.x * CPW;
+    const int rowq = 4 * (lane >> 4);  // first output row of this lane in a 16-row tile
+    const int colq = lane & 15;        // A row / output column of this lane in a 16-block
+
+    // This wave's tile range [ta, tb).
+    const int ua = (wave * p.units) / KW;
+    const int ub = ((wave + 1) * p.units) / KW;
+    const int ta = ua * p.unit;
+    const int tb = min(p.KT, ub * p.unit);
 
     const uint4* wp[CPW];
     const uint16_t* sp[CPW];
-    bool cval[CPW];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
-        cval[c] = (nbw + c) < p.NB;
-        const int nb = cval[c] ? (nbw + c) : 0;
+        const int nb = min(nb0 + c, p.NB - 1);
         wp[c] = p.W + static_cast<int64_t>(nb) * p.KT * 64 + lane;
-        sp[c] = p.S + static_cast<int64_t>(nb) * p.NG * 16 + (lane & 15);
+        sp[c] = p.S + static_cast<int64_t>(nb) * p.NG * 16 + colq;
+    }
+    const int8_t* ap[MT];
+    bool arow_ok[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int row = mt * 16 + colq;
+        arow_ok[mt] = row < p.M;
+        ap[mt] = p.A + static_cast<int64_t>(min(row, p.M - 1)) * p.lda + (lane >> 4) * 16;
     }
 
-    // Scale prefetch for the (at most two) groups that end inside tile t.
-    auto load_scales = [&](int t, uint32_t (&sv)[CPW][2]) {
+    uint4 wb[D][CPW];
+    uint4 ab[D][MT][2];
+    uint32_t sb[D][CPW][2];
+    auto load_slot = [&](int s, int t) {
+        const int tc = max(ta, min(t, tb - 1));   // clamp into this wave's range
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) wb[s][c] = wp[c][static_cast<int64_t>(tc) * 64];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)   // a slab past K has zero weights; clamp its read into the row
+                ab[s][mt][h] = *reinterpret_cast<const uint4*>(ap[mt] + min(tc * 128 + h * 64, p.K - 64));
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int sg = 2 * t + h;
-            const int g = sg / p.spg;
-            const bool ends = ((sg + 1) % p.spg == 0) && g < p.NG;
+            const int g = min((2 * tc + h) / p.spg, p.NG - 1);
 #pragma unroll
-            for (int c = 0; c < CPW; ++c)
-                sv[c][h] = (ends && cval[c]) ? static_cast<uint32_t>(sp[c][g * 16]) : 0u;
+            for (int c = 0; c < CPW; ++c) sb[s][c][h] = sp[c][g * 16];
         }
     };
-
-    uint4 wb[kPF][CPW];
-    uint32_t sb[kPF][CPW][2];
-#pragma unroll
-    for (int s = 0; s < kPF; ++s) {
-        const int t = t0 + s;
-#pragma unroll
-        for (int c = 0; c < CPW; ++c)
-            wb[s][c] = (t < t1 && cval[c]) ? wp[c][static_cast<int64_t>(t) * 64] : make_uint4(0, 0, 0, 0);
-        if (t < t1) load_scales(t, sb[s]);
-    }
 
     float acc[MT][CPW][4];
     v4i P[MT][CPW];
@@ -127,78 +113,67 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(const DecodeParam
             for (int i = 0; i < 4; ++i) acc[mt][c][i] = 0.0f;
         }
 
-    int chunk_t0 = t0;
-    const int rowq = 4 * (lane >> 4);  // first output row of this lane inside a 16-row tile
-    const int colq = lane & 15;
-
-    for (int tb = t0; tb < t1; tb += kPF) {
+    if (tb > ta) {
 #pragma unroll
-        for (int s = 0; s < kPF; ++s) {
-            const int t = tb + s;
-            if (t >= t1) break;
-            if (((t - t0) % Cfg::kTC) == 0) {
-                // Stage A[:, t*128 : (t+tc)*128) into LDS; rows >= M and K >= K are zero.
-                chunk_t0 = t;
-                const int tc = min(Cfg::kTC, t1 - t);
-                const int upr = tc * 8;  // 16-byte units per row
-                __syncthreads();
-                for (int u = threadIdx.x; u < Cfg::kRows * upr; u += kThreads) {
-                    const int r = u / upr;
-                    const int cu = u - r * upr;
-                    const int64_t k = static_cast<int64_t>(t) * 128 + cu * 16;
-                    uint4 v = make_uint4(0, 0, 0, 0);
-                    if (r < p.M && k < p.K) v = *reinterpret_cast<const uint4*>(p.A + r * p.lda + k);
-                    *reinterpret_cast<uint4*>(lds + r * Cfg::kLStride + cu * 16) = v;
+        for (int s = 0; s < D; ++s) load_slot(s, ta + s);
+        const int iters = (tb - ta + D - 1) / D;
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int s = 0; s < D; ++s) {
+                const int t = ta + it * D + s;
+                const bool tvalid = t < tb;
+                uint4 wc[CPW];
+                v4i a[MT][2];
+                uint32_t sc[CPW][2];
+#pragma unroll
+                for (int c = 0; c < CPW; ++c) {
+                    wc[c] = wb[s][c];
+                    sc[c][0] = sb[s][c][0];
+                    sc[c][1] = sb[s][c][1];
                 }
-                __syncthreads();
-            }
-            uint4 wc[CPW];
-            uint32_t sc[CPW][2];
 #pragma unroll
-            for (int c = 0; c < CPW; ++c) {
-                wc[c] = wb[s][c];
-                sc[c][0] = sb[s][c][0];
-                sc[c][1] = sb[s][c][1];
-            }
-            const int tn = t + kPF;
-            if (tn < t1) {
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int c = 0; c < CPW; ++c)
-                    wb[s][c] = cval[c] ? wp[c][static_cast<int64_t>(tn) * 64] : make_uint4(0, 0, 0, 0);
-                load_scales(tn, sb[s]);
-            }
-            v4i b[CPW][2];
+                    for (int h = 0; h < 2; ++h) {
+                        const uint4 v = ab[s][mt][h];
+                        const bool ok = arow_ok[mt];
+                        a[mt][h] = v4i{ok ? static_cast<int>(v.x) : 0, ok ? static_cast<int>(v.y) : 0,
+                                       ok ? static_cast<int>(v.z) : 0, ok ? static_cast<int>(v.w) : 0};
+                    }
+                load_slot(s, t + D);
+                v4i b[CPW][2];
 #pragma unroll
-            for (int c = 0; c < CPW; ++c) unpack_tile_lane(wc[c], b[c][0], b[c][1]);
-            const int8_t* arow = lds + colq * Cfg::kLStride + (t - chunk_t0) * 128 + (lane >> 4) * 16;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const v4i a = *reinterpret_cast<const v4i*>(arow + mt * 16 * Cfg::kLStride + h * 64);
-#pragma unroll
-                    for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(a, b[c][h], P[mt][c]);
+                for (int c = 0; c < CPW; ++c) {
+                    unpack_tile_lane(wc[c], b[c][0], b[c][1]);
+                    if (!tvalid) b[c][0] = b[c][1] = v4i{0, 0, 0, 0};
                 }
-                const int sg = 2 * t + h;
-                const int g = sg / p.spg;
-                if (((sg + 1) % p.spg) == 0 && g < p.NG) {
 #pragma unroll
-                    for (int c = 0; c < CPW; ++c) {
-                        const float ws = scale_to_f32<SBF16>(sc[c][h]);
+                for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) {
-                            if constexpr (DUMP) {
-                                const int col = (nbw + c) * 16 + colq;
+                    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                                for (int i = 0; i < 4; ++i) {
-                                    const int row = mt * 16 + rowq + i;
-                                    if (row < p.M && col < p.N)
-                                        p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[mt][c][i] >> 4;
+                        for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(a[mt][h], b[c][h], P[mt][c]);
+                    const int sg = 2 * t + h;
+                    const int g = sg / p.spg;
+                    if (tvalid && ((sg + 1) % p.spg) == 0 && g < p.NG) {
+#pragma unroll
+                        for (int c = 0; c < CPW; ++c) {
+                            const float ws = scale_to_f32<SBF16>(sc[c][h]);
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) {
+                                if constexpr (DUMP) {
+                                    const int col = (nb0 + c) * 16 + colq;
+#pragma unroll
+                                    for (int i = 0; i < 4; ++i) {
+                                        const int row = mt * 16 + rowq + i;
+                                        if (row < p.M && col < p.N)
+                                            p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[mt][c][i] >> 4;
+                                    }
                                 }
-                            }
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) acc[mt][c][i] += static_cast<float>(P[mt][c][i]) * ws;
-                            P[mt][c] = v4i{0, 0, 0, 0};
+                                for (int i = 0; i < 4; ++i) acc[mt][c][i] += static_cast<float>(P[mt][c][i]) * ws;
+                                P[mt][c] = v4i{0, 0, 0, 0};
+                            }
                         }
                     }
                 }
@@ -206,119 +181,58 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(const DecodeParam
         }
     }
 
-    if (p.ksplit == 1) {
+    // Fixed-order reduction of the KW wave partials, then the epilogue.
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = mt * 16 + rowq + i;
-                if (row >= p.M) continue;
-                const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
+        for (int c = 0; c < CPW; ++c)
 #pragma unroll
-                for (int c = 0; c < CPW; ++c) {
-                    const int col = (nbw + c) * 16 + colq;
-                    if (col < p.N) p.Y[row * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][c][i] * ts));
-                }
-            }
-        }
-        return;
-    }
-
-    // Split-K: publish this split's partial, last arrival reduces in split order.
-    float* mypart = p.part + static_cast<int64_t>(blockIdx.y) * p.M * p.N;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = mt * 16 + rowq + i;
-            if (row >= p.M) continue;
-#pragma unroll
-            for (int c = 0; c < CPW; ++c) {
-                const int col = (nbw + c) * 16 + colq;
-                if (col < p.N) mypart[static_cast<int64_t>(row) * p.N + col] = acc[mt][c][i];
-            }
-        }
-    }
-    __threadfence();
+            for (int i = 0; i < 4; ++i) red[wave * R * C + (mt * 16 + rowq + i) * C + c * 16 + colq] = acc[mt][c][i];
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(p.cnt + blockIdx.x, 1u);
-        s_last = (prev == static_cast<uint32_t>(p.ksplit - 1)) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (s_last == 0u) return;
-    __threadfence();
-    constexpr int kCols = kWaves * CPW * 16;
-    const int col0 = blockIdx.x * kCols;
-    for (int idx = threadIdx.x; idx < p.M * kCols; idx += kThreads) {
-        const int row = idx / kCols;
-        const int col = col0 + (idx - row * kCols);
-        if (col >= p.N) continue;
-        const int64_t off = static_cast<int64_t>(row) * p.N + col;
-        float sum = 0.0f;
-        for (int ks = 0; ks < p.ksplit; ++ks) sum += __builtin_nontemporal_load(p.part + static_cast<int64_t>(ks) * p.M * p.N + off);
+    for (int e = threadIdx.x; e < R * C; e += 64 * KW) {
+        const int row = e / C;
+        const int col = nb0 * 16 + (e - row * C);
+        if (row >= p.M || col >= p.N) continue;
+        float sum = red[e];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) sum += red[w * R * C + e];
         const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
-        p.Y[row * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
+        p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
     }
-    if (threadIdx.x == 0) p.cnt[blockIdx.x] = 0u;
 }
 
-struct DecodePlan {
-    int MT, CPW, ksplit, tps;
-    int64_t ncg;
-};
-
-int gcd_i(int a, int b) { while (b) { int t = a % b; a = b; b = t; } return a; }
-
-DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t group) {
-    DecodePlan pl{};
-    pl.MT = static_cast<int>(geom::ceil_div(M, 16));
-    pl.CPW = 1;
-    const int64_t NB = geom::col_blocks(N);
-    pl.ncg = geom::ceil_div(NB, kWaves * pl.CPW);
-    const int KT = static_cast<int>(geom::k_tiles(K, group));
-    const int spg = static_cast<int>(group / 64);
-    // Split boundaries must fall on both tile (2 slabs) and group boundaries.
-    const int unit_slabs = 2 * spg / gcd_i(2, spg);
-    const int unit = unit_slabs / 2;
-    const int units = (KT + unit - 1) / unit;
-    const int64_t target = 4 * static_cast<int64_t>(device_cu_count());
-    int ks = static_cast<int>(std::max<int64_t>(1, (target + pl.ncg - 1) / pl.ncg));
-    ks = std::min(ks, units);
-    if (pl.ncg > kMaxCounters) ks = 1;  // wide N has enough column groups without split-K
-    const int ups = (units + ks - 1) / ks;
-    pl.tps = ups * unit;
-    pl.ksplit = (KT + pl.tps - 1) / pl.tps;
-    return pl;
+int gcd_i(int a, int b) {
+    while (b) {
+        const int t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
 }
 
-template <int MT, bool SBF16, bool DUMP>
-hipError_t launch_mt(const DecodeParams& p, const DecodePlan& pl, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(pl.ncg), static_cast<unsigned>(pl.ksplit));
-    gemm_decode_kernel<MT, 1, SBF16, DUMP><<<grid, dim3(kThreads), 0, stream>>>(p);
+template <int MT, int CPW, int KW, int D, bool SBF16, bool DUMP>
+hipError_t launch_cfg(const DecodeParams& p, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW));
+    gemm_decode_kernel<MT, CPW, KW, D, SBF16, DUMP><<<grid, dim3(64 * KW), 0, stream>>>(p);
     return hipGetLastError();
 }
 
 template <bool SBF16, bool DUMP>
-hipError_t launch_sd(const DecodeParams& p, const DecodePlan& pl, hipStream_t stream) {
-    switch (pl.MT) {
-        case 1: return launch_mt<1, SBF16, DUMP>(p, pl, stream);
-        case 2: return launch_mt<2, SBF16, DUMP>(p, pl, stream);
-        case 3: return launch_mt<3, SBF16, DUMP>(p, pl, stream);
-        default: return launch_mt<4, SBF16, DUMP>(p, pl, stream);
+hipError_t launch_sd(const DecodeParams& p, hipStream_t stream) {
+    const int mt = (p.M + 15) / 16;
+    switch (mt) {
+        case 1: return launch_cfg<1, 1, 8, 8, SBF16, DUMP>(p, stream);
+        case 2: return launch_cfg<2, 2, 4, 4, SBF16, DUMP>(p, stream);
+        case 3: return launch_cfg<3, 2, 4, 4, SBF16, DUMP>(p, stream);
+        default: return launch_cfg<4, 2, 4, 4, SBF16, DUMP>(p, stream);
     }
 }
 
 }  // namespace
 
-int64_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
-    const DecodePlan pl = plan_decode(M, N, K, group);
-    if (pl.ksplit <= 1) return 0;
-    return kCounterBytes + static_cast<int64_t>(pl.ksplit) * M * N * 4;
-}
+int64_t decode_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
-    const DecodePlan pl = plan_decode(a.M, a.N, a.K, a.group);
     DecodeParams p{};
     p.A = a.a_q;
     p.lda = a.lda;
@@ -335,15 +249,12 @@ hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
     p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
     p.NB = static_cast<int>(geom::col_blocks(a.N));
     p.spg = static_cast<int>(a.group / 64);
-    p.tps = pl.tps;
-    p.ksplit = pl.ksplit;
-    if (pl.ksplit > 1) {
-        p.cnt = reinterpret_cast<uint32_t*>(a.workspace);
-        p.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes);
-    }
+    // K-split boundaries fall on both tile (2 slabs) and group boundaries.
+    p.unit = (2 * p.spg / gcd_i(2, p.spg)) / 2;
+    p.units = (p.KT + p.unit - 1) / p.unit;
     const bool dump = a.partials != nullptr;
-    if (a.scale_bf16) return dump ? launch_sd<true, true>(p, pl, stream) : launch_sd<true, false>(p, pl, stream);
-    return dump ? launch_sd<false, true>(p, pl, stream) : launch_sd<false, false>(p, pl, stream);
+    if (a.scale_bf16) return dump ? launch_sd<true, true>(p, stream) : launch_sd<true, false>(p, stream);
+    return dump ? launch_sd<false, true>(p, stream) : launch_sd<false, false>(p, stream);
 }
 
 }  // namespace w4a8
