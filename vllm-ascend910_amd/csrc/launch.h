@@ -36,6 +36,19 @@ constexpr int64_t kDecodeMaxM = 64;
 int64_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
 
+// Decode launch configuration: register-ring depth D (tiles in flight per
+// wave), columns blocks per workgroup CPW, waves per workgroup KW (the K
+// split).  ``decode_config`` is the shape heuristic launch_gemm_decode uses;
+// launch_gemm_decode_cfg takes an explicit one (cfg.D/CPW must name a built
+// variant, otherwise hipErrorInvalidValue).
+struct DecodeConfig {
+    int D;
+    int CPW;
+    int KW;
+};
+DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group);
+hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream);
+
 // Prefill path (M > kDecodeMaxM): MFMA bound, LDS-tiled.
 int64_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
