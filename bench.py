@@ -13,7 +13,8 @@ that every step streams them from HBM, not from the 256 MB Infinity Cache
 Each step is replayed as a HIP graph (one per weight copy).
 
 ``value`` = algorithmic bytes of the 16 linears per step / step time, in
-GB/s: GEMM bytes N*K/2 + (K/G)*N*2 + M*K + 4*M + 2*M*N
+GB/s: GEMM bytes N*K/2 + (K/G)*N*2 + M*K + 4*M + 2*M*N (weights, group scales, int8
+activations, token scales, bf16 output)
 plus quant bytes 2*M*K + M*K + 2*M.  Inputs are resident in HBM before the
 timed region.  Per-shape kernel times (graph replays of back-to-back
 launches between HIP events), prefill TOPS and a CPU baseline
@@ -65,10 +66,13 @@ def main():
     ap.add_argument("--no-detail", action="store_true", help="only the timed steps (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: each decode linear once (eager) on cold weights, then a "
+                         "256 MiB device copy of known size for calibrating the byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the W4A8 linear is "
-              f"a per-GPU kernel and its sharding is described in DESIGN.md", file=sys.stderr)
+              f"a per-GPU kernel (tensor-parallel shards run the same kernel on their slice)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -115,6 +119,20 @@ def main():
                 a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(xs[(M, p)])
                 outs.append(torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP))
         return outs
+
+    if args.pmc_probe:
+        for i, M in enumerate(DECODE_MS):
+            for j, p in enumerate(PROJS):
+                K, N = synth.QWQ_SHAPES[p]
+                wt, st = weights[p][(i * len(PROJS) + j) % copies]
+                a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(xs[(M, p)])
+                torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP)
+        src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("bench: pmc probe done (16 decode linears, then one 268435456-byte device copy)")
+        return
 
     # ---------------------------------------------------------------- graphs
     cap = torch.cuda.Stream(device=dev)
@@ -223,11 +241,18 @@ def main():
             log(f"  {p:13s} M={M:3d}: gemm {us:8.2f} us {b / us / 1e3:7.1f} GB/s ({b / us / 1e3 / HBM_PEAK_GBS:.1%})"
                 f"  quant {qus:6.2f} us")
     achieved = tot_bytes / tot_us / 1e3
+    # HBM bytes per launch from the two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) recorded in
+    # profiles/ (the command is in the summary), each scaled by a 256 MiB copy's reading.
+    traffic, traffic_src = None, ROOT / "profiles" / "gemm_decode_kernel_traffic.json"
+    if traffic_src.exists():
+        traffic = round(json.loads(traffic_src.read_text())["avg_traffic_bytes"])
     result["roofline"] = {
         "kernel": "gemm_decode_kernel (decode W4A8 GEMM, all 16 configs[1] shapes, cold)",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
         "per_launch_bytes_avg": round(tot_bytes / len(shapes)), "launch_us_avg": round(tot_us / len(shapes), 3),
+        "timing": "HIP events around graph replays of back-to-back launches on the launch stream",
+        "traffic_source": str(traffic_src.relative_to(ROOT)) if traffic is not None else None,
     }
     result["decode_shapes"] = shapes
 
