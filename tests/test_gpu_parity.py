@@ -164,6 +164,10 @@ GEMM_CASES = [
     (65, 384, 1024, 128, "bf16"),    # first prefill-path M
     (128, 256, 1024, 1024, "f16"),
     (300, 1000, 2048, 128, "bf16"),  # ragged M and N tiles
+    (130, 512, 1024, 64, "f16"),     # prefill, two groups per 128-K step
+    (200, 300, 768, 192, "bf16"),    # prefill, groups ending mid-step, K % 128 == 64
+    (96, 520, 2048, 256, "f16"),     # prefill, a group spans two steps
+    (257, 264, 1024, 512, "bf16"),
 ]
 
 

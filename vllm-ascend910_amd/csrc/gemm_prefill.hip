@@ -1,16 +1,27 @@
 // Prefill-shaped W4A8 GEMM (M > 64): int8 MFMA bound.
 //
-// Same arithmetic as the decode path (see gemm_decode.hip): exact int32 per
-// group, fp32 fold with the group scale, token scale at the end.
+// Same arithmetic as the decode path (gemm_decode.hip): exact int32 per group,
+// fp32 fold with the group scale, token scale at the end.
 //
-// Tiling: a 256-thread workgroup computes a BM x BN = 128 x 128 output tile;
-// its four waves form a 2 x 2 grid of 64 x 64 wave tiles, each 2 x 2
-// v_mfma_i32_32x32x32_i8 blocks.  The K loop walks 128-K steps (one repacked
-// weight tile row).  Each step the workgroup stages 128 x 128 int8
-// activations and 128 columns x 128 K of weights in LDS; the weights arrive as
-// packed int4 (8 KB) and are unpacked once on the way into LDS, so the four
-// waves share the unpack.  The next step's global loads are issued into
-// registers before the current step's MFMAs (register double buffering).
+// Tiling.  A 512-thread workgroup (8 waves, two per SIMD) computes a
+// BM x BN = 128 x 256 output tile; wave (wm, wn) owns rows wm*64..+64 and
+// columns wn*64..+64 as 2 x 2 blocks of v_mfma_i32_32x32x32_i8.  The K loop
+// walks 128-K steps (one repacked weight tile row):
+//   * activations: the workgroup stages A[128 rows][128 K] int8 in LDS,
+//     double-buffered (the next step's rows are loaded into registers at the
+//     start of a step and written to the other buffer at its end), so there
+//     is one barrier per step;
+//   * weights: every wave loads its own 64 columns straight from the repacked
+//     tiles into registers, DW steps ahead.  For a 32x32x32 B operand lane
+//     (column c, half hh) and slab s the natural K order k = 32s + 16hh + [0,16)
+//     is held by repacked lane (c%16) + 16*(2*(s%2) + hh), bytes 8*(s/2)..+8,
+//     so each lane needs exactly two 16-byte chunks per step and unpacks them
+//     with two AND/shift operations per 8 codes -- no shuffles.
+// All global reads are raw buffer loads (SGPR descriptor + 32-bit offset):
+// rows past M and column blocks past N read as zero, and per-lane addresses
+// cost one VGPR.  The per-group fold (acc += float(16*P) * w_scale) is VALU
+// work of the same size as the MFMA work at group 128; two waves per SIMD let
+// the hardware run one wave's fold under the other's MFMAs.
 #include "common.h"
 #include "kgeom.h"
 #include "launch.h"
@@ -18,9 +29,10 @@
 namespace w4a8 {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 128;
-constexpr int kBN = 128;
+constexpr int kBN = 256;
 constexpr int kLS = 128 + 16;  // LDS row stride in bytes (+16 against bank conflicts)
 
 struct PrefillParams {
@@ -35,79 +47,85 @@ struct PrefillParams {
     int M, N, K;
     int KT, NG, NB;
     int group;
+    int tiles_m, tiles_n;
+    uint32_t a_bytes, w_bytes, s_bytes;
 };
 
-template <bool SBF16, bool DUMP>
-__global__ __launch_bounds__(kThreads) void gemm_prefill_kernel(const PrefillParams p) {
-    __shared__ __attribute__((aligned(16))) int8_t la[kBM * kLS];
-    __shared__ __attribute__((aligned(16))) int8_t lb[kBN * kLS];
+// GMODE: 0 = group 64 (two groups per step), 1 = group 128 (one per step),
+// 2 = any other multiple of 64 (groups may start and end on either 64-K half).
+template <int GMODE, int DW, bool SBF16, bool DUMP>
+__global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const PrefillParams p) {
+    __shared__ __attribute__((aligned(16))) int8_t la[2][kBM * kLS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1;  // wave row (0..1)
-    const int wn = wave & 1;   // wave col (0..1)
-    const int m0 = blockIdx.y * kBM;
-    const int n0 = blockIdx.x * kBN;
-    const int nb0 = n0 / 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2;  // 0..1
+    const int wn = wave & 3;   // 0..3
+    const int tile_n = blockIdx.x % p.tiles_n;
+    const int tile_m = blockIdx.x / p.tiles_n;
+    const int m0 = tile_m * kBM;
+    const int n0 = tile_n * kBN;
+    const int c32 = lane & 31;   // column (B) / row (A) inside a 32-block
+    const int hh = lane >> 5;    // K half of the 32-K slab
 
-    // Global -> register staging of one K step.
-    uint4 ra[4];
-    uint4 rb[2];
-    auto load_step = [&](int kt) {
+    const auto ra_rsrc = make_rsrc(p.A, p.a_bytes);
+    const auto rw_rsrc = make_rsrc(p.W, p.w_bytes);
+    const auto rs_rsrc = make_rsrc(p.S, p.s_bytes);
+
+    // ---- weights: byte offsets of this lane's two 16-byte chunks per step,
+    // for the wave's 32-column blocks j = 0, 1 (column blocks past N read 0).
+    uint32_t woff[2][2];
+    uint32_t soff[2];
+    int colj[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = i * kThreads + tid;
-            const int r = c >> 3;
-            const int cu = c & 7;
-            const int row = m0 + r;
-            const int64_t k = static_cast<int64_t>(kt) * 128 + cu * 16;
-            ra[i] = (row < p.M && k < p.K) ? *reinterpret_cast<const uint4*>(p.A + row * p.lda + k)
-                                           : make_uint4(0, 0, 0, 0);
-        }
+    for (int j = 0; j < 2; ++j) {
+        const int col = n0 + wn * 64 + j * 32 + c32;
+        colj[j] = col;
+        const uint32_t tile0 = static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u;
+        woff[j][0] = tile0 + static_cast<uint32_t>((col & 15) + 16 * hh) * 16u;        // slabs 0, 2
+        woff[j][1] = tile0 + static_cast<uint32_t>((col & 15) + 16 * (2 + hh)) * 16u;  // slabs 1, 3
+        soff[j] = (static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.NG) * 16u + (col & 15)) * 2u;
+    }
+
+    // ---- activation staging: 128 rows x 8 units of 16 B = 1024 units, 2 per thread
+    uint32_t aoffg[2];
+    int aoff[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = i * kThreads + tid;
-            const int j = c >> 6;
-            const int ll = c & 63;
-            const int nb = nb0 + j;
-            rb[i] = (nb < p.NB) ? p.W[(static_cast<int64_t>(nb) * p.KT + kt) * 64 + ll] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+        const int c = i * kThreads + tid;
+        const int r = c >> 3;
+        const int cu = (c & 7) * 16;
+        // rows >= M lie past the buffer and read zero; they are never stored
+        aoffg[i] = static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(p.lda) + cu;
+        aoff[i] = r * kLS + cu;
+    }
+    auto load_a = [&](int kt, uint4 (&ra)[2]) {
+        // a half-empty last step reads past K: those bytes meet zero weights
+        const uint32_t k = static_cast<uint32_t>(min(kt, p.KT - 1)) * 128u;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) ra[i] = buf_load16(ra_rsrc, aoffg[i] + k);
+    };
+
+    uint4 wr[DW][2][2];
+    auto load_w = [&](int slot, int kt) {
+        const uint32_t t = static_cast<uint32_t>(min(kt, p.KT - 1)) * 1024u;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            wr[slot][j][0] = buf_load16(rw_rsrc, woff[j][0] + t);
+            wr[slot][j][1] = buf_load16(rw_rsrc, woff[j][1] + t);
         }
     };
-    auto store_step = [&]() {
+    // Scales of the groups that may end in step kt: at its 64-K halves h=0,1
+    // (group 128 only ends on the step's last slab, so one scale suffices).
+    constexpr int NSC = GMODE == 1 ? 1 : 2;
+    auto load_s = [&](int kt, uint32_t (&sv)[2][NSC]) {
+        const int ktc = min(kt, p.KT - 1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = i * kThreads + tid;
-            *reinterpret_cast<uint4*>(la + (c >> 3) * kLS + (c & 7) * 16) = ra[i];
-        }
+        for (int h = 0; h < NSC; ++h) {
+            const int g = min((ktc * 128 + (GMODE == 1 ? 127 : h * 64 + 63)) / p.group, p.NG - 1);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = i * kThreads + tid;
-            const int j = c >> 6;
-            const int ll = c & 63;
-            v4i s0, s1;
-            unpack_tile_lane(rb[i], s0, s1);
-            int8_t* dst = lb + (j * 16 + (ll & 15)) * kLS + (ll >> 4) * 16;
-            *reinterpret_cast<v4i*>(dst) = s0;
-            *reinterpret_cast<v4i*>(dst + 64) = s1;
-        }
-    };
-
-    // Scales of this lane's two columns for the groups ending in step kt.
-    const int colw = n0 + wn * 64 + (lane & 31);
-    uint32_t sc[2][2];
-    auto load_scales = [&](int kt, uint32_t (&s)[2][2]) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int kend = kt * 128 + (h + 1) * 64;
-            const int g = (kend - 1) / p.group;
-            const bool ends = (kend % p.group) == 0 && g < p.NG;
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const int col = colw + cb * 32;
-                const int nb = col >> 4;
-                s[cb][h] = (ends && nb < p.NB) ? static_cast<uint32_t>(p.S[(static_cast<int64_t>(nb) * p.NG + g) * 16 + (col & 15)]) : 0u;
-            }
+            for (int j = 0; j < 2; ++j) sv[j][h] = buf_load_u16(rs_rsrc, soff[j] + static_cast<uint32_t>(g) * 32u);
         }
     };
 
@@ -123,94 +141,139 @@ __global__ __launch_bounds__(kThreads) void gemm_prefill_kernel(const PrefillPar
                 acc[a][b][i] = 0.0f;
             }
         }
+    const v16i zero16 = {};
 
-    load_step(0);
-    load_scales(0, sc);
-    store_step();
-    __syncthreads();
-
-    const int8_t* abase = la + (wm * 64 + (lane & 31)) * kLS + (lane >> 5) * 16;
-    const int8_t* bbase = lb + (wn * 64 + (lane & 31)) * kLS + (lane >> 5) * 16;
-
-    for (int kt = 0; kt < p.KT; ++kt) {
-        uint32_t scn[2][2];
-        const bool more = (kt + 1) < p.KT;
-        if (more) {
-            load_step(kt + 1);
-            load_scales(kt + 1, scn);
-        }
+    auto fold = [&](int g, const uint32_t (&sv)[2][NSC], int h) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            v4i av[2], bv[2];
+        for (int j = 0; j < 2; ++j) {
+            const float ws = scale_to_f32<SBF16>(sv[j][h]);
 #pragma unroll
-            for (int r = 0; r < 2; ++r) av[r] = *reinterpret_cast<const v4i*>(abase + r * 32 * kLS + s * 32);
+            for (int rb = 0; rb < 2; ++rb) {
+                if constexpr (DUMP) {
+                    const int col = colj[j];
 #pragma unroll
-            for (int c = 0; c < 2; ++c) bv[c] = *reinterpret_cast<const v4i*>(bbase + c * 32 * kLS + s * 32);
-#pragma unroll
-            for (int r = 0; r < 2; ++r)
-#pragma unroll
-                for (int c = 0; c < 2; ++c) P[r][c] = mfma32(av[r], bv[c], P[r][c]);
-            if (s & 1) {
-                const int h = s >> 1;
-                const int kend = kt * 128 + (h + 1) * 64;
-                const int g = (kend - 1) / p.group;
-                if ((kend % p.group) == 0 && g < p.NG) {
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const float ws = scale_to_f32<SBF16>(sc[c][h]);
-#pragma unroll
-                        for (int r = 0; r < 2; ++r) {
-                            if constexpr (DUMP) {
-                                const int col = colw + c * 32;
-#pragma unroll
-                                for (int i = 0; i < 16; ++i) {
-                                    const int row = m0 + wm * 64 + r * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                                    if (row < p.M && col < p.N)
-                                        p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[r][c][i] >> 4;
-                                }
-                            }
-#pragma unroll
-                            for (int i = 0; i < 16; ++i) {
-                                acc[r][c][i] += static_cast<float>(P[r][c][i]) * ws;
-                                P[r][c][i] = 0;
-                            }
-                        }
+                    for (int i = 0; i < 16; ++i) {
+                        const int row = m0 + wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
+                        if (row < p.M && col < p.N)
+                            p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[rb][j][i] >> 4;
                     }
                 }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[rb][j][i] += static_cast<float>(P[rb][j][i]) * ws;
             }
         }
-        if (more) {
-            __syncthreads();
-            store_step();
+    };
+
+    // ---- prologue: A(0) into LDS, A(1) in registers, W(0..DW-1) in flight
+    uint4 ra[2][2];
+    load_a(0, ra[0]);
+    load_a(1, ra[1]);
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
+    for (int s = 0; s < DW; ++s) load_w(s, s);
+    uint32_t sc[2][NSC];
+    load_s(0, sc);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) sc[c][h] = scn[c][h];
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(&la[0][aoff[i]]) = ra[0][i];
+    __syncthreads();
+
+    const int8_t* abase = &la[0][0] + (wm * 64 + c32) * kLS + hh * 16;
+
+    // DW is even, so the A register buffer of step kt is ra[u & 1] with a
+    // compile-time index.
+    static_assert(DW % 2 == 0, "DW must be even");
+    for (int kt0 = 0; kt0 < p.KT; kt0 += DW) {
+#pragma unroll
+        for (int u = 0; u < DW; ++u) {
+            const int kt = kt0 + u;
+            if (kt >= p.KT) break;
+            const int buf = kt & 1;
+            // ra[(u+1)&1] holds A(kt+1) (written to LDS at the end of this step);
+            // refill ra[u&1] with A(kt+2).
+            load_a(kt + 2, ra[u & 1]);
+            uint32_t scn[2][NSC];
+            load_s(kt + 1, scn);
+            uint4 wc[2][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                wc[j][0] = wr[u][j][0];
+                wc[j][1] = wr[u][j][1];
+            }
+            load_w(u, kt + DW);
+            const int8_t* ab = abase + buf * (kBM * kLS);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                v4i av[2], bv[2];
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) av[rb] = *reinterpret_cast<const v4i*>(ab + rb * 32 * kLS + s * 32);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint4 w = wc[j][s & 1];
+                    const uint32_t d0 = (s >> 1) ? w.z : w.x;
+                    const uint32_t d1 = (s >> 1) ? w.w : w.y;
+                    bv[j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
+                }
+                // A group starts on this slab: accumulate from zero (static for
+                // groups 64/128, a uniform runtime test otherwise).
+                if constexpr (GMODE == 2) {
+                    if ((s == 0 || s == 2) && ((kt * 128 + s * 32) % p.group) == 0) {
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j) P[rb][j] = zero16;
+                    }
+                }
+                const bool fresh = (GMODE == 0) ? (s == 0 || s == 2) : (GMODE == 1 && s == 0);
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) P[rb][j] = mfma32(av[rb], bv[j], fresh ? zero16 : P[rb][j]);
+                if (s == 1 || s == 3) {
+                    const int kend = kt * 128 + (s + 1) * 32;   // K position after this slab
+                    const int g = (kend - 1) / p.group;
+                    const bool ends = GMODE == 0 || (GMODE == 1 ? s == 3 : (kend % p.group) == 0);
+                    if (ends && g < p.NG) fold(g, sc, GMODE == 1 ? 0 : (s >> 1));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int h = 0; h < NSC; ++h) sc[j][h] = scn[j][h];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(&la[buf ^ 1][aoff[i]]) = ra[(u + 1) & 1][i];
             __syncthreads();
         }
     }
 
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int row = m0 + wm * 64 + r * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            const int row = m0 + wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
             if (row >= p.M) continue;
             const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const int col = colw + c * 32;
-                if (col < p.N) p.Y[row * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[r][c][i] * ts));
+            for (int j = 0; j < 2; ++j) {
+                const int col = colj[j];
+                if (col < p.N) p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][j][i] * ts));
             }
         }
     }
 }
 
+constexpr int kDW = 2;   // weight prefetch depth in K steps
+
+template <int GMODE, bool SBF16, bool DUMP>
+hipError_t launch_g(const PrefillParams& p, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+    gemm_prefill_kernel<GMODE, kDW, SBF16, DUMP><<<grid, dim3(kThreads), 0, stream>>>(p);
+    return hipGetLastError();
+}
+
 template <bool SBF16, bool DUMP>
 hipError_t launch(const PrefillParams& p, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(geom::ceil_div(p.N, kBN)), static_cast<unsigned>(geom::ceil_div(p.M, kBM)));
-    gemm_prefill_kernel<SBF16, DUMP><<<grid, dim3(kThreads), 0, stream>>>(p);
-    return hipGetLastError();
+    if (p.group == 64) return launch_g<0, SBF16, DUMP>(p, stream);
+    if (p.group == 128) return launch_g<1, SBF16, DUMP>(p, stream);
+    return launch_g<2, SBF16, DUMP>(p, stream);
 }
 
 }  // namespace
@@ -234,6 +297,11 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
     p.NB = static_cast<int>(geom::col_blocks(a.N));
     p.group = static_cast<int>(a.group);
+    p.tiles_m = static_cast<int>(geom::ceil_div(a.M, kBM));
+    p.tiles_n = static_cast<int>(geom::ceil_div(a.N, kBN));
+    p.a_bytes = static_cast<uint32_t>(a.M * a.lda);
+    p.w_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::k_tiles(a.K, a.group) * geom::kTileBytes);
+    p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
     const bool dump = a.partials != nullptr;
     if (a.scale_bf16) return dump ? launch<true, true>(p, stream) : launch<true, false>(p, stream);
     return dump ? launch<false, true>(p, stream) : launch<false, false>(p, stream);
