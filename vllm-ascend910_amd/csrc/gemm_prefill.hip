@@ -192,26 +192,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const Prefill
             load_a(kt + 2, ra[u & 1]);
             uint32_t scn[2][NSC];
             load_s(kt + 1, scn);
-            uint4 wc[2][2];
+            // Unpack this step's weights into all four slabs' B operands first,
+            // so the ring slot is dead and its refill needs no register copies.
+            v4i bvs[4][2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                wc[j][0] = wr[u][j][0];
-                wc[j][1] = wr[u][j][1];
-            }
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint4 w = wr[u][j][s & 1];
+                    const uint32_t d0 = (s >> 1) ? w.z : w.x;
+                    const uint32_t d1 = (s >> 1) ? w.w : w.y;
+                    bvs[s][j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
+                }
             load_w(u, kt + DW);
             const int8_t* ab = abase + buf * (kBM * kLS);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                v4i av[2], bv[2];
+                v4i av[2];
+                const v4i* bv = bvs[s];
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb) av[rb] = *reinterpret_cast<const v4i*>(ab + rb * 32 * kLS + s * 32);
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint4 w = wc[j][s & 1];
-                    const uint32_t d0 = (s >> 1) ? w.z : w.x;
-                    const uint32_t d1 = (s >> 1) ? w.w : w.y;
-                    bv[j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
-                }
                 // A group starts on this slab: accumulate from zero (static for
                 // groups 64/128, a uniform runtime test otherwise).
                 if constexpr (GMODE == 2) {
