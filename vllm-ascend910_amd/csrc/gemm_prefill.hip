@@ -3,14 +3,15 @@
 // Same arithmetic as the decode path (gemm_decode.hip): exact int32 per group,
 // fp32 fold with the group scale, token scale at the end.
 //
-// Tiling.  A 512-thread workgroup (8 waves, two per SIMD) computes a
-// BM x BN = 128 x 256 output tile; wave (wm, wn) owns rows wm*64..+64 and
+// Tiling.  A 256-thread workgroup (4 waves, one per SIMD; two workgroups
+// share a CU, so every SIMD runs two independent waves) computes a
+// BM x BN = 128 x 128 output tile; wave (wm, wn) owns rows wm*64..+64 and
 // columns wn*64..+64 as 2 x 2 blocks of v_mfma_i32_32x32x32_i8.  The K loop
 // walks 128-K steps (one repacked weight tile row):
 //   * activations: the workgroup stages A[128 rows][128 K] int8 in LDS,
-//     double-buffered (the next step's rows are loaded into registers at the
-//     start of a step and written to the other buffer at its end), so there
-//     is one barrier per step;
+//     double-buffered (the next step's rows are loaded into registers two
+//     steps ahead and written to the other buffer at the end of a step), so
+//     there is one barrier per step;
 //   * weights: every wave loads its own 64 columns straight from the repacked
 //     tiles into registers, DW steps ahead.  For a 32x32x32 B operand lane
 //     (column c, half hh) and slab s the natural K order k = 32s + 16hh + [0,16)
@@ -19,9 +20,10 @@
 //     with two AND/shift operations per 8 codes -- no shuffles.
 // All global reads are raw buffer loads (SGPR descriptor + 32-bit offset):
 // rows past M and column blocks past N read as zero, and per-lane addresses
-// cost one VGPR.  The per-group fold (acc += float(16*P) * w_scale) is VALU
-// work of the same size as the MFMA work at group 128; two waves per SIMD let
-// the hardware run one wave's fold under the other's MFMAs.
+// cost one VGPR.  The per-group fold (acc += float(16*P) * w_scale, a convert
+// and an FMA per output element and group) is VALU work of the same duration
+// as the MFMA work at group 128, so this kernel is bound by VALU issue and
+// MFMA/VALU overlap rather than by the matrix cores.
 #include "common.h"
 #include "kgeom.h"
 #include "launch.h"
@@ -29,10 +31,12 @@
 namespace w4a8 {
 namespace {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;   // 2 x kWN waves of 64 x 64
+constexpr int kWN = kWaves / 2;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 128;
-constexpr int kBN = 256;
+constexpr int kBN = 64 * kWN;
+constexpr int kNA = kBM * 8 / kThreads;   // 16-byte A units per thread per step
 constexpr int kLS = 128 + 16;  // LDS row stride in bytes (+16 against bank conflicts)
 
 struct PrefillParams {
@@ -47,23 +51,38 @@ struct PrefillParams {
     int M, N, K;
     int KT, NG, NB;
     int group;
-    int tiles_m, tiles_n;
+    int tiles_m, tiles_n, band;
     uint32_t a_bytes, w_bytes, s_bytes;
 };
 
 // GMODE: 0 = group 64 (two groups per step), 1 = group 128 (one per step),
 // 2 = any other multiple of 64 (groups may start and end on either 64-K half).
 template <int GMODE, int DW, bool SBF16, bool DUMP>
-__global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const PrefillParams p) {
     __shared__ __attribute__((aligned(16))) int8_t la[2][kBM * kLS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2;  // 0..1
-    const int wn = wave & 3;   // 0..3
-    const int tile_n = blockIdx.x % p.tiles_n;
-    const int tile_m = blockIdx.x / p.tiles_n;
+    const int wm = wave / kWN;  // 0..1
+    const int wn = wave % kWN;
+    // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+    // L2.  Renumber them so that every XCD walks one contiguous run of tiles,
+    // and order the tiles in bands of p.band tile rows, so the workgroups
+    // resident on one XCD at a time cover a compact block of the output and
+    // share A rows and weight columns in that XCD's L2.
+    int tile_m, tile_n;
+    {
+        const int nwg = static_cast<int>(gridDim.x);
+        const int bid = static_cast<int>(blockIdx.x);
+        const int xcd = bid & 7, q = nwg >> 3, r = nwg & 7;
+        const int lin = xcd * q + min(xcd, r) + (bid >> 3);
+        const int band = lin / (p.band * p.tiles_n);
+        const int inband = lin - band * p.band * p.tiles_n;
+        const int rows = min(p.band, p.tiles_m - band * p.band);
+        tile_m = band * p.band + inband % rows;
+        tile_n = inband / rows;
+    }
     const int m0 = tile_m * kBM;
     const int n0 = tile_n * kBN;
     const int c32 = lane & 31;   // column (B) / row (A) inside a 32-block
@@ -89,10 +108,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const Prefill
     }
 
     // ---- activation staging: 128 rows x 8 units of 16 B = 1024 units, 2 per thread
-    uint32_t aoffg[2];
-    int aoff[2];
+    uint32_t aoffg[kNA];
+    int aoff[kNA];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kNA; ++i) {
         const int c = i * kThreads + tid;
         const int r = c >> 3;
         const int cu = (c & 7) * 16;
@@ -100,11 +119,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const Prefill
         aoffg[i] = static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(p.lda) + cu;
         aoff[i] = r * kLS + cu;
     }
-    auto load_a = [&](int kt, uint4 (&ra)[2]) {
+    auto load_a = [&](int kt, uint4 (&ra)[kNA]) {
         // a half-empty last step reads past K: those bytes meet zero weights
         const uint32_t k = static_cast<uint32_t>(min(kt, p.KT - 1)) * 128u;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) ra[i] = buf_load16(ra_rsrc, aoffg[i] + k);
+        for (int i = 0; i < kNA; ++i) ra[i] = buf_load16(ra_rsrc, aoffg[i] + k);
     };
 
     uint4 wr[DW][2][2];
@@ -143,14 +162,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const Prefill
         }
     const v16i zero16 = {};
 
-    auto fold = [&](int g, const uint32_t (&sv)[2][NSC], int h) {
+    // acc[rb] += float(P[rb]) * w_scale for row block rb of group g;
+    // ws2[j] are the scale bits of the wave's column blocks j = 0, 1.
+    auto fold_rb = [&](int rb, int g, const uint32_t (&ws2)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const float ws = scale_to_f32<SBF16>(sv[j][h]);
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                if constexpr (DUMP) {
-                    const int col = colj[j];
+            const float ws = scale_to_f32<SBF16>(ws2[j]);
+            if constexpr (DUMP) {
+                const int col = colj[j];
+                if (g >= 0 && g < p.NG) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int row = m0 + wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
@@ -158,14 +178,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const Prefill
                             p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[rb][j][i] >> 4;
                     }
                 }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[rb][j][i] += static_cast<float>(P[rb][j][i]) * ws;
             }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rb][j][i] += static_cast<float>(P[rb][j][i]) * ws;
         }
     };
 
     // ---- prologue: A(0) into LDS, A(1) in registers, W(0..DW-1) in flight
-    uint4 ra[2][2];
+    uint4 ra[2][kNA];
     load_a(0, ra[0]);
     load_a(1, ra[1]);
 #pragma unroll
@@ -173,76 +193,89 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_prefill_kernel(const Prefill
     uint32_t sc[2][NSC];
     load_s(0, sc);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(&la[0][aoff[i]]) = ra[0][i];
+    for (int i = 0; i < kNA; ++i) *reinterpret_cast<uint4*>(&la[0][aoff[i]]) = ra[0][i];
     __syncthreads();
 
     const int8_t* abase = &la[0][0] + (wm * 64 + c32) * kLS + hh * 16;
 
+    // Per step: issue the loads for later steps, unpack this step's weights
+    // into all four slabs' B operands (so the ring slot is dead and its refill
+    // needs no register copies), then the MFMAs.
+    auto step = [&](int kt, int u, int buf) __attribute__((always_inline)) {
+        // ra[(u+1)&1] holds A(kt+1) (written to LDS at the end of this step);
+        // refill ra[u&1] with A(kt+2).
+        load_a(kt + 2, ra[u & 1]);
+        uint32_t scn[2][NSC];
+        load_s(kt + 1, scn);
+        v4i bvs[4][2];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint4 w = wr[u][j][s & 1];
+                const uint32_t d0 = (s >> 1) ? w.z : w.x;
+                const uint32_t d1 = (s >> 1) ? w.w : w.y;
+                bvs[s][j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
+            }
+        load_w(u, kt + DW);
+        const int8_t* ab = abase + buf * (kBM * kLS);
+        auto lds_a = [&](int rb, int s) { return *reinterpret_cast<const v4i*>(ab + rb * 32 * kLS + s * 32); };
+
+        // Slab-major: the four blocks' MFMA chains interleave, so no MFMA waits
+        // on its predecessor's result.  A group ends after slab 1 or 3 (fixed
+        // for groups 64/128, a uniform runtime test otherwise); both row blocks
+        // are folded then.  Groups past NG (the half-empty last step of an odd
+        // number of 64-groups) hold zero partials and fold nothing.
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            bool fresh = GMODE == 0 ? (s == 0 || s == 2) : (GMODE == 1 && s == 0);
+            if constexpr (GMODE == 2) fresh = (s == 0 || s == 2) && ((kt * 128 + s * 32) % p.group) == 0;
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                const v4i av = lds_a(rb, s);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) P[rb][j] = mfma32(av, bvs[s][j], fresh ? zero16 : P[rb][j]);
+            }
+            if (s == 1 || s == 3) {
+                const int kend = kt * 128 + (s + 1) * 32;   // K position after this slab
+                const int g = (kend - 1) / p.group;
+                const bool ends = GMODE == 0 || (GMODE == 1 ? s == 3 : (kend % p.group) == 0);
+                if (ends) {
+                    const int h = GMODE == 1 ? 0 : (s >> 1);
+                    const uint32_t ws2[2] = {sc[0][h], sc[1][h]};
+                    fold_rb(0, g, ws2);
+                    fold_rb(1, g, ws2);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int h = 0; h < NSC; ++h) sc[j][h] = scn[j][h];
+    };
+
     // DW is even, so the A register buffer of step kt is ra[u & 1] with a
     // compile-time index.
     static_assert(DW % 2 == 0, "DW must be even");
-    for (int kt0 = 0; kt0 < p.KT; kt0 += DW) {
+    auto one = [&](int kt, int u) __attribute__((always_inline)) {
+        const int buf = kt & 1;
+        step(kt, u, buf);
 #pragma unroll
-        for (int u = 0; u < DW; ++u) {
-            const int kt = kt0 + u;
-            if (kt >= p.KT) break;
-            const int buf = kt & 1;
-            // ra[(u+1)&1] holds A(kt+1) (written to LDS at the end of this step);
-            // refill ra[u&1] with A(kt+2).
-            load_a(kt + 2, ra[u & 1]);
-            uint32_t scn[2][NSC];
-            load_s(kt + 1, scn);
-            // Unpack this step's weights into all four slabs' B operands first,
-            // so the ring slot is dead and its refill needs no register copies.
-            v4i bvs[4][2];
+        for (int i = 0; i < kNA; ++i) *reinterpret_cast<uint4*>(&la[buf ^ 1][aoff[i]]) = ra[(u + 1) & 1][i];
+        __syncthreads();
+    };
+    // Whole groups of DW steps, then the remaining steps after the loop: an
+    // early exit inside the unrolled group would give the loop header a path
+    // whose newest loads are this group's weight refills, and the wait counts
+    // at the top of every iteration would have to cover it.
+    int kt = 0;
+    for (; kt + DW <= p.KT; kt += DW) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint4 w = wr[u][j][s & 1];
-                    const uint32_t d0 = (s >> 1) ? w.z : w.x;
-                    const uint32_t d1 = (s >> 1) ? w.w : w.y;
-                    bvs[s][j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
-                }
-            load_w(u, kt + DW);
-            const int8_t* ab = abase + buf * (kBM * kLS);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                v4i av[2];
-                const v4i* bv = bvs[s];
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb) av[rb] = *reinterpret_cast<const v4i*>(ab + rb * 32 * kLS + s * 32);
-                // A group starts on this slab: accumulate from zero (static for
-                // groups 64/128, a uniform runtime test otherwise).
-                if constexpr (GMODE == 2) {
-                    if ((s == 0 || s == 2) && ((kt * 128 + s * 32) % p.group) == 0) {
-#pragma unroll
-                        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                            for (int j = 0; j < 2; ++j) P[rb][j] = zero16;
-                    }
-                }
-                const bool fresh = (GMODE == 0) ? (s == 0 || s == 2) : (GMODE == 1 && s == 0);
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) P[rb][j] = mfma32(av[rb], bv[j], fresh ? zero16 : P[rb][j]);
-                if (s == 1 || s == 3) {
-                    const int kend = kt * 128 + (s + 1) * 32;   // K position after this slab
-                    const int g = (kend - 1) / p.group;
-                    const bool ends = GMODE == 0 || (GMODE == 1 ? s == 3 : (kend % p.group) == 0);
-                    if (ends && g < p.NG) fold(g, sc, GMODE == 1 ? 0 : (s >> 1));
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int h = 0; h < NSC; ++h) sc[j][h] = scn[j][h];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(&la[buf ^ 1][aoff[i]]) = ra[(u + 1) & 1][i];
-            __syncthreads();
-        }
+        for (int u = 0; u < DW; ++u) one(kt + u, u);
     }
+#pragma unroll
+    for (int u = 0; u < DW - 1; ++u)
+        if (kt + u < p.KT) one(kt + u, u);
 
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
@@ -299,6 +332,7 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     p.group = static_cast<int>(a.group);
     p.tiles_m = static_cast<int>(geom::ceil_div(a.M, kBM));
     p.tiles_n = static_cast<int>(geom::ceil_div(a.N, kBN));
+    p.band = 4;
     p.a_bytes = static_cast<uint32_t>(a.M * a.lda);
     p.w_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::k_tiles(a.K, a.group) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
