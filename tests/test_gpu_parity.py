@@ -160,6 +160,10 @@ GEMM_CASES = [
     (7, 100, 512, 256, "f16"),       # N not a multiple of 16
     (16, 5120, 5120, 128, "f16"),    # o_proj decode, C1
     (33, 1024, 4096, 512, "bf16"),
+    (3, 200, 1536, 192, "bf16"),     # decode, groups ending on a tile's lower slab
+    (9, 300, 1920, 320, "f16"),      # decode, 5 slabs per group: ends on either slab
+    (2, 160, 2560, 640, "bf16"),     # decode, 10 slabs per group (not a power-of-two multiple of 128)
+    (5, 96, 3072, 256, "f16"),       # decode, two tiles per group
     (64, 7168, 5120, 128, "f16"),    # qkv decode, M=64
     (65, 384, 1024, 128, "bf16"),    # first prefill-path M
     (128, 256, 1024, 1024, "f16"),

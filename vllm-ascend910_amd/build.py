@@ -24,7 +24,11 @@ ARCH = "gfx950"
 
 # Packed-FP32 VALU forms are disabled for all device code on this platform;
 # hipcc's host pass warns that it does not know the feature, which is harmless.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# MFMA results stay in ordinary VGPRs: the folds read every accumulator with
+# VALU instructions, which cannot address AGPRs (each element would first need
+# a v_accvgpr_read).
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall",
                 "-Wno-unused-function", "-Wno-unused-variable"]
 

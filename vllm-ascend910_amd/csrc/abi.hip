@@ -98,13 +98,14 @@ int run_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_ti
     a.workspace = workspace;
     a.workspace_bytes = workspace_bytes;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (M > kDecodeMaxM) {
-        // The prefill kernel addresses A and the weight tiles with 32-bit buffer
-        // offsets, including up to one tile past the end of each.
+    {
+        // Both kernels address A and the weight tiles with 32-bit buffer
+        // offsets, including up to one tile past the end of each, and mark
+        // out-of-range reads with an offset of 2^31 added on top.
         const int64_t a_span = (M + 128) * lda;
         const int64_t w_span = (geom::col_blocks(N) + 16) * geom::k_tiles(K, group) * geom::kTileBytes;
         if (a_span >= (1ll << 31) || w_span >= (1ll << 31))
-            return fail(W4A8_ERR_UNSUPPORTED, "prefill operands too large for 32-bit offsets (A %lld B, weights %lld B)",
+            return fail(W4A8_ERR_UNSUPPORTED, "operands too large for 32-bit offsets (A %lld B, weights %lld B)",
                         a_span, w_span);
     }
     const hipError_t e = (M <= kDecodeMaxM) ? launch_gemm_decode(a, s) : launch_gemm_prefill(a, s);

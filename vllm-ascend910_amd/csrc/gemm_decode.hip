@@ -11,15 +11,18 @@
 // columns) and ALL of K; its KW waves split K into contiguous, group-aligned
 // ranges.  Each wave streams its range: per 128-K tile one 16-byte load per
 // lane per column block (the repacked tile, 1 KB) plus MT*2 16-byte loads of
-// activations (L2-resident; rows >= M are masked), held D tiles ahead in a
-// register ring.  Every load is unconditional -- addresses are clamped into
-// the buffers and the values masked afterwards -- so the compiler can count
-// loads in flight exactly and the ring really overlaps.  Per 64-K slab each
-// wave issues MT*CPW v_mfma_i32_16x16x64_i8; at each group end the int32
+// activations (L2-resident), held D tiles ahead in a register ring.  All loads
+// are raw buffer loads (SGPR descriptor + 32-bit offset) and unconditional:
+// rows past M and tiles past the wave's range are addressed beyond the buffer
+// ends and read as zero, so nothing is masked
+// and the compiler can count loads in flight exactly.  Per 64-K slab each wave
+// issues MT*CPW v_mfma_i32_16x16x64_i8; at each group end the int32
 // accumulators fold into fp32 (acc += float(16*P) * w_scale).  The KW partial
 // sums are reduced through LDS in a fixed order, and the token scale and the
 // 1/16 of the nibble unpack are applied once at the end.  No workspace, no
-// inter-workgroup communication, deterministic results.
+// inter-workgroup communication (an agent-scope release/acquire pair costs
+// about 10 us per call on MI355X, more than a K split across workgroups
+// gains), deterministic results.
 #include <algorithm>
 #include <type_traits>
 
@@ -42,11 +45,19 @@ struct DecodeParams {
     int M, N, K;
     int KT, NG, NB;
     int spg;           // 64-K slabs per group
+    int gshift;        // GM 1: log2(tiles per group)
     int unit;          // tiles per K-split unit (group and tile aligned)
     int units;         // ceil(KT / unit)
+    uint32_t a_bytes, w_bytes, s_bytes;
 };
 
-template <int MT, int CPW, int KWMAX, int D, bool G64, bool SBF16, bool DUMP>
+// Offset that every buffer here treats as out of range (reads return zero).
+constexpr uint32_t kOOB = 0x80000000u;
+
+// GM: 0 = group 64 (a group per slab), 1 = group 128 * 2^gshift (groups end on
+// a tile's upper slab), 2 = any other multiple of 64 (a group ends on either
+// slab; at most one per tile).
+template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP>
 __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodeParams p) {
     constexpr int R = 16 * MT;
     constexpr int C = 16 * CPW;
@@ -55,7 +66,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
 
     const int lane = threadIdx.x & 63;
     // Wave-uniform by construction; readfirstlane tells the compiler so, which
-    // keeps the tile loop and fold conditions scalar branches.
+    // keeps the tile loop and fold conditions scalar.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kw = blockDim.x >> 6;
     const int nb0 = blockIdx.x * CPW;
@@ -68,44 +79,62 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     const int ta = ua * p.unit;
     const int tb = min(p.KT, ub * p.unit);
 
-    const uint4* wp[CPW];
-    const uint16_t* sp[CPW];
+    const auto rw = make_rsrc(p.W, p.w_bytes);
+    const auto ra = make_rsrc(p.A, p.a_bytes);
+    const auto rs = make_rsrc(p.S, p.s_bytes);
+    uint32_t wo[CPW], so[CPW], ao[MT];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
-        const int nb = min(nb0 + c, p.NB - 1);
-        wp[c] = p.W + static_cast<int64_t>(nb) * p.KT * 64 + lane;
-        sp[c] = p.S + static_cast<int64_t>(nb) * p.NG * 16 + colq;
+        // a column block past NB (odd NB, last workgroup) re-reads the last
+        // block; its columns are past N and never stored
+        const uint32_t nb = static_cast<uint32_t>(min(nb0 + c, p.NB - 1));
+        wo[c] = nb * static_cast<uint32_t>(p.KT) * 1024u + lane * 16u;
+        so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + colq) * 2u;
     }
-    const int8_t* ap[MT];
-    bool arow_ok[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const int row = mt * 16 + colq;
-        arow_ok[mt] = row < p.M;
-        ap[mt] = p.A + static_cast<int64_t>(min(row, p.M - 1)) * p.lda + (lane >> 4) * 16;
+        // rows past M start past the buffer end; a slab past K meets zero weights
+        const uint32_t row = static_cast<uint32_t>(mt * 16 + colq);
+        ao[mt] = row < static_cast<uint32_t>(p.M) ? row * static_cast<uint32_t>(p.lda) + (lane >> 4) * 16u : kOOB;
     }
 
-    // Register ring: D tiles of weights, activations and the scales of the
-    // groups ending in them (two per tile for group 64, one otherwise: a group
-    // of >= 128 can only end on a tile's upper slab).
-    constexpr int NS = G64 ? 2 : 1;
+    // Group bookkeeping.  end_slab(t): -1, 0 or 1 = which slab of tile t ends
+    // a group; gend(t): that group (clamped, for the scale load).
+    auto gend = [&](int t, int h) -> int {
+        int g;
+        if constexpr (GM == 0) g = 2 * t + h;
+        else if constexpr (GM == 1) g = t >> p.gshift;
+        else g = ((2 * t + 1) % p.spg == 0) ? (2 * t) / p.spg : (2 * t + 1) / p.spg;
+        return min(g, p.NG - 1);
+    };
+
+    // Register rings: D tiles of weights and of the scales of the groups
+    // ending in them (two per tile for group 64, one otherwise), and DA tiles
+    // of activations (L2-resident, so a shallower ring keeps the registers of
+    // the 32- to 64-row tiles in budget).
+    constexpr int NS = GM == 0 ? 2 : 1;
+    constexpr int DA = MT >= 3 ? 2 : D;
+    static_assert(D % DA == 0, "activation ring depth must divide D");
     uint4 wb[D][CPW];
-    uint4 ab[D][MT][2];
+    uint4 ab[DA][MT][2];
     uint32_t sb[D][CPW][NS];
-    auto load_slot = [&](int s, int t) {
-        const int tc = max(ta, min(t, tb - 1));   // clamp into this wave's range
-#pragma unroll
-        for (int c = 0; c < CPW; ++c) wb[s][c] = load_stream(wp[c] + static_cast<int64_t>(tc) * 64);
+    auto load_a = [&](int sa, int t) {
+        const uint32_t ka = static_cast<uint32_t>(min(t, p.KT - 1)) * 128u;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)   // a slab past K has zero weights; clamp its read into the row
-                ab[s][mt][h] = *reinterpret_cast<const uint4*>(ap[mt] + min(tc * 128 + h * 64, p.K - 64));
+            for (int h = 0; h < 2; ++h) ab[sa][mt][h] = buf_load16(ra, ao[mt] + ka + h * 64u);
+    };
+    auto load_slot = [&](int s, int t) {
+        // tiles past this wave's range read zero weights
+        const uint32_t tw = t < tb ? static_cast<uint32_t>(t) * 1024u : kOOB;
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, wo[c] + tw);
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-            const int g = min((2 * tc + (G64 ? j : 1)) / p.spg, p.NG - 1);
+            const uint32_t g = static_cast<uint32_t>(gend(min(t, p.KT - 1), j)) * 32u;
 #pragma unroll
-            for (int c = 0; c < CPW; ++c) sb[s][c][j] = sp[c][g * 16];
+            for (int c = 0; c < CPW; ++c) sb[s][c][j] = buf_load_u16(rs, so[c] + g);
         }
     };
 
@@ -120,68 +149,68 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
             for (int i = 0; i < 4; ++i) acc[mt][c][i] = 0.0f;
         }
 
-    // One pass over the D ring slots; PREFETCH refills each slot with the tile
-    // D ahead (the last pass is peeled without it, so nothing past the range
-    // is requested).
+    // `own`: the group lies in this wave's range (folds in the zero tiles past
+    // the range add nothing and must not overwrite another wave's partials).
+    auto fold = [&](int g, bool own, const uint32_t (&sc)[CPW][NS], int j) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const float ws = scale_to_f32<SBF16>(sc[c][j]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                if constexpr (DUMP) {
+                    const int col = (nb0 + c) * 16 + colq;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int row = mt * 16 + rowq + i;
+                        if (own && row < p.M && col < p.N && g < p.NG)
+                            p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[mt][c][i] >> 4;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mt][c][i] += static_cast<float>(P[mt][c][i]) * ws;
+                P[mt][c] = v4i{0, 0, 0, 0};
+            }
+        }
+    };
+
+    // One pass over the D ring slots; PREFETCH refills each weight slot with
+    // the tile D ahead (the last pass is peeled without it, so no weights past
+    // the range are requested).  The activation ring is refilled DA ahead in
+    // every pass.  Tiles of the last pass past tb hold zero weights: their
+    // MFMAs add nothing and a fold there adds zero.
     auto pass = [&](int it, auto prefetch) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int t = ta + it * D + s;
-            const bool tvalid = t < tb;
-            uint4 wc[CPW];
-            v4i a[MT][2];
             uint32_t sc[CPW][NS];
 #pragma unroll
-            for (int c = 0; c < CPW; ++c) {
-                wc[c] = wb[s][c];
+            for (int c = 0; c < CPW; ++c)
 #pragma unroll
                 for (int j = 0; j < NS; ++j) sc[c][j] = sb[s][c][j];
-            }
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint4 v = ab[s][mt][h];
-                    const bool ok = arow_ok[mt];
-                    a[mt][h] = v4i{ok ? static_cast<int>(v.x) : 0, ok ? static_cast<int>(v.y) : 0,
-                                   ok ? static_cast<int>(v.z) : 0, ok ? static_cast<int>(v.w) : 0};
-                }
-            if constexpr (decltype(prefetch)::value) load_slot(s, t + D);
+            // Unpack the weight slot, then refill it; the activation slot is
+            // used in place and refilled after its last MFMA (no copies).
             v4i b[CPW][2];
 #pragma unroll
-            for (int c = 0; c < CPW; ++c) {
-                unpack_tile_lane(wc[c], b[c][0], b[c][1]);
-                if (!tvalid) b[c][0] = b[c][1] = v4i{0, 0, 0, 0};
-            }
+            for (int c = 0; c < CPW; ++c) unpack_tile_lane(wb[s][c], b[c][0], b[c][1]);
+            if constexpr (decltype(prefetch)::value) load_slot(s, t + D);
+            const auto& av = ab[s % DA];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+                for (int mt = 0; mt < MT; ++mt) {
+                    const uint4 v = av[mt][h];
+                    const v4i a = {static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
 #pragma unroll
-                    for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(a[mt][h], b[c][h], P[mt][c]);
-                if (!G64 && h == 0) continue;
-                const int sg = 2 * t + h;
-                const int g = sg / p.spg;
-                if (tvalid && ((sg + 1) % p.spg) == 0 && g < p.NG) {
-#pragma unroll
-                    for (int c = 0; c < CPW; ++c) {
-                        const float ws = scale_to_f32<SBF16>(sc[c][G64 ? h : 0]);
-#pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) {
-                            if constexpr (DUMP) {
-                                const int col = (nb0 + c) * 16 + colq;
-#pragma unroll
-                                for (int i = 0; i < 4; ++i) {
-                                    const int row = mt * 16 + rowq + i;
-                                    if (row < p.M && col < p.N)
-                                        p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[mt][c][i] >> 4;
-                                }
-                            }
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) acc[mt][c][i] += static_cast<float>(P[mt][c][i]) * ws;
-                            P[mt][c] = v4i{0, 0, 0, 0};
-                        }
-                    }
+                    for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(a, b[c][h], P[mt][c]);
+                }
+                if (h == 1) load_a(s % DA, t + DA);
+                if constexpr (GM == 0) {
+                    fold(2 * t + h, t < tb, sc, h);
+                } else if constexpr (GM == 1) {
+                    if (h == 1 && ((t + 1) & ((1 << p.gshift) - 1)) == 0) fold(t >> p.gshift, t < tb, sc, 0);
+                } else {
+                    const int sg = 2 * t + h;
+                    if (((sg + 1) % p.spg) == 0) fold(sg / p.spg, t < tb, sc, 0);
                 }
             }
         }
@@ -190,6 +219,8 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     if (tb > ta) {
 #pragma unroll
         for (int s = 0; s < D; ++s) load_slot(s, ta + s);
+#pragma unroll
+        for (int s = 0; s < DA; ++s) load_a(s, ta + s);
         const int iters = (tb - ta + D - 1) / D;
         for (int it = 0; it + 1 < iters; ++it) pass(it, std::true_type{});
         pass(iters - 1, std::false_type{});
@@ -223,36 +254,47 @@ int gcd_i(int a, int b) {
     return a;
 }
 
-constexpr int kwmax_for(int mt) { return mt == 1 ? 16 : (mt == 2 ? 8 : 4); }
+constexpr int kwmax_for(int mt) { return mt == 1 ? 12 : (mt == 2 ? 8 : 4); }
 
-template <int MT, int CPW, int D, bool DUMP>
-hipError_t launch_v(const DecodeParams& p, int kw, bool g64, bool sbf16, hipStream_t stream) {
+template <int MT, int CPW, int D, int GM, bool DUMP>
+hipError_t launch_g(const DecodeParams& p, int kw, bool sbf16, hipStream_t stream) {
     constexpr int KWM = kwmax_for(MT);
     const int w = std::max(1, std::min(kw, KWM));
     const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW)), block(64 * w);
     const size_t lds = static_cast<size_t>(w) * 16 * MT * 16 * CPW * sizeof(float);
-    if (g64) {
-        if (sbf16) gemm_decode_kernel<MT, CPW, KWM, D, true, true, DUMP><<<grid, block, lds, stream>>>(p);
-        else gemm_decode_kernel<MT, CPW, KWM, D, true, false, DUMP><<<grid, block, lds, stream>>>(p);
-    } else {
-        if (sbf16) gemm_decode_kernel<MT, CPW, KWM, D, false, true, DUMP><<<grid, block, lds, stream>>>(p);
-        else gemm_decode_kernel<MT, CPW, KWM, D, false, false, DUMP><<<grid, block, lds, stream>>>(p);
-    }
+    if (sbf16) gemm_decode_kernel<MT, CPW, KWM, D, GM, true, DUMP><<<grid, block, lds, stream>>>(p);
+    else gemm_decode_kernel<MT, CPW, KWM, D, GM, false, DUMP><<<grid, block, lds, stream>>>(p);
     return hipGetLastError();
+}
+
+// Group mode: 64 -> 0; 128 * 2^s -> 1; anything else -> 2.
+int group_mode(int spg) {
+    if (spg == 1) return 0;
+    if (spg % 2 == 0 && ((spg / 2) & (spg / 2 - 1)) == 0) return 1;
+    return 2;
+}
+
+template <int MT, int CPW, int D, bool DUMP>
+hipError_t launch_v(const DecodeParams& p, int kw, bool sbf16, hipStream_t stream) {
+    switch (group_mode(p.spg)) {
+        case 0: return launch_g<MT, CPW, D, 0, DUMP>(p, kw, sbf16, stream);
+        case 1: return launch_g<MT, CPW, D, 1, DUMP>(p, kw, sbf16, stream);
+        default: return launch_g<MT, CPW, D, 2, DUMP>(p, kw, sbf16, stream);
+    }
 }
 
 // The variants that are built: (MT, D, CPW).
 template <bool DUMP>
-hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool g64, bool sbf16, hipStream_t s) {
+hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool sbf16, hipStream_t s) {
     const int mt = (p.M + 15) / 16;
-    if (mt == 1 && c.D == 8 && c.CPW == 1) return launch_v<1, 1, 8, DUMP>(p, c.KW, g64, sbf16, s);
-    if (mt == 1 && c.D == 4 && c.CPW == 1) return launch_v<1, 1, 4, DUMP>(p, c.KW, g64, sbf16, s);
-    if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, DUMP>(p, c.KW, g64, sbf16, s);
-    if (mt == 2 && c.D == 4 && c.CPW == 1) return launch_v<2, 1, 4, DUMP>(p, c.KW, g64, sbf16, s);
-    if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, DUMP>(p, c.KW, g64, sbf16, s);
-    if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, DUMP>(p, c.KW, g64, sbf16, s);
-    if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, DUMP>(p, c.KW, g64, sbf16, s);
-    if (mt == 4 && c.D == 2 && c.CPW == 4) return launch_v<4, 4, 2, DUMP>(p, c.KW, g64, sbf16, s);
+    if (mt == 1 && c.D == 8 && c.CPW == 1) return launch_v<1, 1, 8, DUMP>(p, c.KW, sbf16, s);
+    if (mt == 1 && c.D == 4 && c.CPW == 1) return launch_v<1, 1, 4, DUMP>(p, c.KW, sbf16, s);
+    if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, DUMP>(p, c.KW, sbf16, s);
+    if (mt == 2 && c.D == 4 && c.CPW == 1) return launch_v<2, 1, 4, DUMP>(p, c.KW, sbf16, s);
+    if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, DUMP>(p, c.KW, sbf16, s);
+    if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, DUMP>(p, c.KW, sbf16, s);
+    if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, DUMP>(p, c.KW, sbf16, s);
+    if (mt == 4 && c.D == 2 && c.CPW == 4) return launch_v<4, 4, 2, DUMP>(p, c.KW, sbf16, s);
     return hipErrorInvalidValue;
 }
 
@@ -273,6 +315,11 @@ DecodeParams make_params(const GemmArgs& a) {
     p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
     p.NB = static_cast<int>(geom::col_blocks(a.N));
     p.spg = static_cast<int>(a.group / 64);
+    p.gshift = 0;
+    while ((2 << p.gshift) < p.spg) ++p.gshift;
+    p.a_bytes = static_cast<uint32_t>(a.M * a.lda);
+    p.w_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.KT) * geom::kTileBytes);
+    p.s_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.NG) * 16 * 2);
     // K-split boundaries fall on both tile (2 slabs) and group boundaries.
     p.unit = (2 * p.spg / gcd_i(2, p.spg)) / 2;
     p.units = (p.KT + p.unit - 1) / p.unit;
@@ -290,23 +337,30 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int KT = static_cast<int>(geom::k_tiles(K, group));
     const int64_t NB = geom::col_blocks(N);
     DecodeConfig c{4, 2, 4};
+    const int64_t wgs = (NB + 1) / 2;
     if (mt <= 2) {
         // Wide N already gives >= 1024 workgroups; otherwise split K so that
-        // each wave holds about one ring (4 tiles) of its range.
-        const int64_t wgs = (NB + 1) / 2;
-        if (wgs >= 1024) c.KW = M <= 8 ? 2 : 1;
-        else c.KW = std::max(1, std::min(mt == 1 ? 12 : 8, (KT + 3) / 4));
-    } else if ((NB + 1) / 2 >= 1024) {
+        // each wave holds about one ring (4 tiles) of its range -- but long K
+        // (>= 128 tiles) streams better with fewer, longer waves the more
+        // activation rows ride along.
+        if (wgs >= 1024) {
+            c.KW = M <= 2 ? 2 : 1;
+        } else {
+            const int cap = KT >= 128 ? (M <= 1 ? 8 : (M <= 4 ? 6 : 4)) : (mt == 1 ? 12 : 8);
+            c.KW = std::max(1, std::min(cap, (KT + 3) / 4));
+        }
+    } else if (wgs >= 1024) {
         c = DecodeConfig{2, 4, 1};
+    } else {
+        c.KW = KT >= 128 ? 3 : 2;
     }
     return c;
 }
 
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream) {
     const DecodeParams p = make_params(a);
-    const bool g64 = p.spg == 1;
-    return a.partials ? dispatch<true>(p, cfg, g64, a.scale_bf16, stream)
-                      : dispatch<false>(p, cfg, g64, a.scale_bf16, stream);
+    return a.partials ? dispatch<true>(p, cfg, a.scale_bf16, stream)
+                      : dispatch<false>(p, cfg, a.scale_bf16, stream);
 }
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
