@@ -69,7 +69,19 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: each decode linear once (eager) on cold weights, then a "
                          "256 MiB device copy of known size for calibrating the byte counters")
+    ap.add_argument("--trace-summary", metavar="DB",
+                    help="summarize a rocprofv3 --kernel-trace database (rocpd SQLite) as markdown and exit")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
+                    help="turn two rocprofv3 --pmc databases of a --pmc-probe run (FETCH_SIZE, WRITE_SIZE) into "
+                         "the per-shape HBM traffic table (markdown on stdout) and exit")
+    ap.add_argument("--pmc-json", metavar="OUT", help="with --pmc-summary: also write the table as JSON")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary, args.pmc_json)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the W4A8 linear is "
               f"a per-GPU kernel (tensor-parallel shards run the same kernel on their slice)", file=sys.stderr)
@@ -282,6 +294,72 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(pkg, dev, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def trace_summary(db):
+    """Per-kernel and per-dispatch-shape duration table of a rocprofv3
+    --kernel-trace database (the rocpd ``kernels`` view)."""
+    import collections
+    import sqlite3
+    rows = sqlite3.connect(db).execute(
+        "select name, duration, grid_x, grid_y, workgroup_x from kernels order by start").fetchall()
+    by_name, by_shape = collections.defaultdict(list), collections.defaultdict(list)
+    for name, dur, gx, gy, wx in rows:
+        short = name.split("(")[0].split("<")[0].split("::")[-1]
+        by_name[short].append(dur)
+        by_shape[(short, gx, gy, wx)].append(dur)
+    print("| kernel | calls | avg us | min us | max us | total ms |\n|---|---:|---:|---:|---:|---:|")
+    for k, d in sorted(by_name.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| {k} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} | {min(d) / 1e3:.3f} | {max(d) / 1e3:.3f} | "
+              f"{sum(d) / 1e6:.3f} |")
+    print("\n| kernel | grid x (threads) | grid y | workgroup | calls | avg us |\n|---|---:|---:|---:|---:|---:|")
+    for (k, gx, gy, wx), d in sorted(by_shape.items()):
+        if k.startswith(("gemm_", "quant_")):
+            print(f"| {k} | {gx} | {gy} | {wx} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
+
+
+def pmc_summary(fetch_db, write_db, out_json=None):
+    """HBM bytes per decode GEMM launch from a --pmc-probe run's FETCH_SIZE and
+    WRITE_SIZE counters (KiB per dispatch), each scaled by what it reads for the
+    probe's closing 256 MiB device copy."""
+    import sqlite3
+
+    def load(db, counter):
+        return sqlite3.connect(db).execute(
+            "select name, counter_value from pmc_events where counter_name=? order by dispatch_id",
+            (counter,)).fetchall()
+
+    fetch, write = load(fetch_db, "FETCH_SIZE"), load(write_db, "WRITE_SIZE")
+    is_copy = lambda n: "copy" in n.lower()
+    cal_kib = 256 * 1024
+    ff = cal_kib / [v for n, v in fetch if is_copy(n)][-1]
+    fw = cal_kib / [v for n, v in write if is_copy(n)][-1]
+    gf = [v for n, v in fetch if "gemm_decode_kernel" in n][-16:]
+    gw = [v for n, v in write if "gemm_decode_kernel" in n][-16:]
+    shapes = [(M, p) for M in DECODE_MS for p in PROJS]
+    import __graft_entry__ as ge
+    synth = ge.package().synth
+    print(f"Calibration: the probe's 256 MiB copy reads FETCH_SIZE {cal_kib / ff:.0f} KiB (factor {ff:.4f}) and "
+          f"WRITE_SIZE {cal_kib / fw:.0f} KiB (factor {fw:.4f}).\n")
+    print("| M | proj | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB | algorithmic MB | ratio |\n"
+          "|---:|---|---:|---:|---:|---:|---:|")
+    out, tot_alg, tot_tr = [], 0.0, 0.0
+    for (M, p), f, w in zip(shapes, gf, gw):
+        K, N = synth.QWQ_SHAPES[p]
+        alg = gemm_bytes(M, N, K)
+        tr = f * 1024 * ff + w * 1024 * fw
+        tot_alg += alg
+        tot_tr += tr
+        out.append(dict(M=M, proj=p, fetch_kib=f, write_kib=w, hbm_bytes=round(tr), alg_bytes=alg,
+                        ratio=round(tr / alg, 4)))
+        print(f"| {M} | {p} | {f:.1f} | {w:.1f} | {tr / 1e6:.3f} | {alg / 1e6:.3f} | {tr / alg:.3f} |")
+    n = len(out)
+    print(f"\nAverage per launch: {tot_tr / n / 1e6:.3f} MB HBM vs {tot_alg / n / 1e6:.3f} MB algorithmic "
+          f"({tot_tr / tot_alg:.3f}x).")
+    if out_json:
+        with open(out_json, "w") as fh:
+            json.dump(dict(factor_fetch=ff, factor_write=fw, per_shape=out, avg_traffic_bytes=tot_tr / n,
+                           avg_alg_bytes=tot_alg / n), fh, indent=1)
 
 
 def cpu_baseline(pkg, dev, seconds):
