@@ -87,11 +87,11 @@ int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_t
                 void* s_tiles, int64_t N, int64_t K, int64_t group, void* stream);
 
 /*
- * Workspace bytes the GEMM needs for (M, N, K, group); 0 when none.  A
- * non-empty workspace starts with a fixed 256 KiB counter region that must be
- * zero before the buffer's first use; every call leaves it zero again (whatever
- * its shape), so one zeroed buffer can be reused by consecutive calls on one
- * stream.  Calls that overlap in time must not share a workspace.
+ * Workspace bytes the GEMM needs for (M, N, K, group); 0 when none, which is
+ * every shape in this build (decode reduces its K split inside a workgroup,
+ * prefill does not split K).  The workspace arguments of w4a8_gemm stay so
+ * that a kernel needing scratch can be added without changing the ABI; a
+ * caller passes the size this function returns (NULL/0 for 0).
  */
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 

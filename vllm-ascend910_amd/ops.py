@@ -46,10 +46,9 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
-# One zero-filled workspace per (device, stream).  The library leaves its
-# counter region at zero after every call, so the buffer is reused as is; it
-# only grows.  Concurrent calls on one stream are stream-ordered, so sharing
-# per stream is safe.
+# One workspace per (device, stream), allocated only when the library asks
+# for one (no shape does at present); it only grows.  Concurrent calls on one
+# stream are stream-ordered, so sharing per stream is safe.
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
 
 
