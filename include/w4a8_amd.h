@@ -53,16 +53,22 @@ const char* w4a8_last_error(void);
 /*
  * Dynamic per-token int8 activation quant.
  *   x       bf16 [M, ldx]   (first K columns used)
- *   a_q     int8 [M, lda]   (first K columns written)
+ *   a_q     int8 [M, lda]   output: with group == 0 (or a geometry without
+ *                           padding, kpad(K, group) == K) the first K columns
+ *                           hold a_q[m, k]; otherwise the first kpad columns
+ *                           hold the padded group layout the GEMM reads --
+ *                           code k at (k / group) * ceil_to(group, 64) + k % group,
+ *                           padding slots zero (npu_ops/kernel/mg_kgeom.h:47-129)
  *   a_scale bf16 [M]
  * Replaces the reference's activation quantiser, kernel
  * npu_ops/kernel/midgroup_quant_a.inc:112-410 bound by
  * npu_ops/host/midgroup_quant_a.cpp:40-78, in its per-token mode
- * (fakequant_lab/quant.py:153-173 with QuantSpec(8, None)); the reference's
- * MSD planes and per-group activation scales are not produced here.
+ * (fakequant_lab/quant.py:153-173 with QuantSpec(8, None)); like it, the
+ * output follows the padded K layout of the weight.  The reference's MSD planes
+ * and per-group activation scales are not produced here.
  */
 int w4a8_quant_act(const void* x, int64_t ldx, void* a_q, int64_t lda, void* a_scale,
-                   int64_t M, int64_t K, void* stream);
+                   int64_t M, int64_t K, int64_t group, void* stream);
 
 /*
  * Sizes of the repacked (gfx950 MFMA operand order) weight and scale buffers.
@@ -97,7 +103,10 @@ int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
 
 /*
  * The grouped W4A8 GEMM with fused scale epilogue.
- *   a_q      int8 [M, lda]      (from w4a8_quant_act)
+ *   a_q      int8 [M, lda]      the padded group layout of w4a8_quant_act with
+ *                               the same group (lda >= kpad, lda % 16 == 0);
+ *                               padding slots may hold any value (they meet
+ *                               zero weight codes)
  *   a_scale  bf16 [M]
  *   w_tiles, s_tiles            (from w4a8_repack; scale_dtype as repacked)
  *   y        bf16 [M, ldy]      output

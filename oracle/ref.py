@@ -70,6 +70,18 @@ def pack_int4_grouped(codes: np.ndarray, group: int) -> np.ndarray:
     return out
 
 
+def split_planes_grouped(a_q: np.ndarray, group: int):
+    """SplitInt8ToInt4PlanesGrouped (gemm_ref.cpp:62-90): packed (hi, lo) int4
+    planes [rows, kpad/2] with a = 16*hi + lo + 8 in the padded K layout."""
+    a_q = np.ascontiguousarray(a_q, np.int8)
+    rows, K = a_q.shape
+    kp = lib().ref_kpad(K, group)
+    hi = np.empty((rows, kp // 2), np.int8)
+    lo = np.empty((rows, kp // 2), np.int8)
+    lib().ref_split_planes_grouped(_ptr(a_q), rows, K, group, _ptr(hi), _ptr(lo))
+    return hi, lo
+
+
 def midgroup_gemm(a_q: np.ndarray, a_scale_g: np.ndarray, w_codes: np.ndarray, w_scale_g: np.ndarray,
                   group: int, w_zero_g: Optional[np.ndarray] = None) -> np.ndarray:
     """ReferenceMidGroupGemm (gemm_ref.cpp:199-240): bf16 bits [M, N].

@@ -155,17 +155,25 @@ def unpack_int4(p: np.ndarray) -> np.ndarray:
     return np.where(out >= 8, out - 16, out).astype(np.int8)
 
 
+def pad_groups(v: np.ndarray, group: int) -> np.ndarray:
+    """[R, K] int8 -> [R, kpad] with group g's real members at g * group_stride
+    and zeros in every padding slot: the padded K layout of both operands
+    (weights: npu_ops/python/w4a8_ops.py:231-239; activations:
+    int4_cube_lab/host/gemm_ref.cpp:62-90, whose padding decodes to 0)."""
+    R, K = v.shape
+    out = np.zeros((R, kpad(K, group)), np.int8)
+    for g in range(num_groups(K, group)):
+        r = group_real(g, K, group)
+        out[:, g * group_stride(group):g * group_stride(group) + r] = v[:, g * group:g * group + r]
+    return out
+
+
 def pack_grouped(codes: np.ndarray, group: int) -> np.ndarray:
     """[N, K] codes -> [N, kpad/2] in the grouped zero-padded layout.
 
     npu_ops/python/w4a8_ops.py:231-239; int4_cube_lab/host/gemm_ref.cpp:42-60.
     """
-    N, K = codes.shape
-    padded = np.zeros((N, kpad(K, group)), np.int8)
-    for g in range(num_groups(K, group)):
-        r = group_real(g, K, group)
-        padded[:, g * group_stride(group):g * group_stride(group) + r] = codes[:, g * group:g * group + r]
-    return pack_int4(padded)
+    return pack_int4(pad_groups(codes, group))
 
 
 # ------------------------------------------------------------------ GEMM

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported(pkg, lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.w4a8_abi_version() == 1
+    assert lib.w4a8_abi_version() == 2
     # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
     assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
@@ -54,8 +54,8 @@ def _gemm(lib, **kw):
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(N=0), 2, "bad shape"),
     (dict(M=-1), 2, "bad shape"),
-    (dict(K=300), 5, "ragged"),
-    (dict(group=96, K=960), 5, "group % 64"),
+    (dict(K=300), 2, "kpad=320"),               # ragged K: A is read in the padded layout
+    (dict(group=96, K=192, lda=240), 2, "kpad=256"),  # groups padded to 128 each
     (dict(sd=7), 3, "scale_dtype"),
     (dict(a_q=None), 1, "NULL"),
     (dict(lda=100), 2, "lda"),
@@ -73,12 +73,16 @@ def test_m0_is_a_noop(lib):
 
 
 def test_quant_and_repack_reject_bad_arguments(lib):
-    assert lib.w4a8_quant_act(None, 64, None, 64, None, 4, 64, None) == 1
-    assert lib.w4a8_quant_act(16, 32, 16, 64, 16, 4, 64, None) == 2
-    assert lib.w4a8_quant_act(None, 64, None, 64, None, 0, 64, None) == 0
-    assert lib.w4a8_repack(16, 16, 0, 16, 16, 64, 300, 128, None) == 5
+    assert lib.w4a8_quant_act(None, 64, None, 64, None, 4, 64, 0, None) == 1
+    assert lib.w4a8_quant_act(16, 32, 16, 64, 16, 4, 64, 0, None) == 2
+    assert lib.w4a8_quant_act(None, 64, None, 64, None, 0, 64, 0, None) == 0
+    # the padded layout of K=100, group 33 is 4 * 64 = 256 wide
+    assert lib.w4a8_quant_act(16, 128, 16, 128, 16, 4, 100, 33, None) == 2
+    assert "output width 256" in lib.w4a8_last_error().decode()
+    assert lib.w4a8_quant_act(16, 128, 16, 256, 16, 4, 100, -1, None) == 2
     assert lib.w4a8_repack(16, 16, 2, 16, 16, 64, 256, 128, None) == 3
     assert lib.w4a8_repack(18, 16, 0, 16, 16, 64, 256, 128, None) == 4
+    assert lib.w4a8_repack(16, 16, 0, 16, 16, 64, 256, 0, None) == 2
 
 
 def test_errors_raise_runtimeerror_from_python(pkg):

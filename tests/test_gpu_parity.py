@@ -31,7 +31,7 @@ def make_problem(pkg, M, N, K, G, seed=0, scale_dtype="f16", codes="uniform"):
     xb = synth.activations(M, K, seed)
     w = synth.weight_codes_uniform(N, K, seed + 1) if codes == "uniform" else \
         synth.weight_codes_clipped_normal(N, K, seed + 1)
-    sb = synth.group_scales(N, K // G, seed + 2, scale_dtype)
+    sb = synth.group_scales(N, ow.num_groups(K, G), seed + 2, scale_dtype)
     ws32 = synth.scale_bits_to_f32(sb, scale_dtype)
     tdt = torch.float16 if scale_dtype == "f16" else torch.bfloat16
     w_scale = torch.from_numpy(np.ascontiguousarray(sb.T).view(np.int16)).view(tdt)
@@ -41,7 +41,7 @@ def make_problem(pkg, M, N, K, G, seed=0, scale_dtype="f16", codes="uniform"):
 def run_hip(dev, xb, w, w_scale, N, K, G, partials=True):
     w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
     w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
-    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xb).to(dev))
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xb).to(dev), G)
     if partials:
         y, P = torch.ops.npu.w4a8_gemm_partials(a_q, a_s, w_tiles, s_tiles, N, K, G)
     else:
@@ -181,11 +181,74 @@ def test_gemm_partials_bit_exact_and_output(pkg, dev, M, N, K, G, sd):
     xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + N, scale_dtype=sd)
     y, P, a_q, a_s = run_hip(dev, xb, w, w_scale, N, K, G)
     q_ref, s_ref = ow.quant_act_per_token(xb)
-    assert np.array_equal(a_q.cpu().numpy(), q_ref)
+    assert np.array_equal(a_q.cpu().numpy(), ow.pad_groups(q_ref, G))
     P_ref = ow.group_partials(q_ref, w, G)
     assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
     y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref, return_abs=True)
-    check_output(tensor_bf16_bits(y), y32, mag, K // G, f"M{M} N{N} K{K} G{G}")
+    check_output(tensor_bf16_bits(y), y32, mag, ow.num_groups(K, G), f"M{M} N{N} K{K} G{G}")
+
+
+# The reference's ragged-K cases (int4_cube_lab/host/ragged_layout_test.cpp:195-223:
+# TP shards of K at group 1024, short last groups down to one element, odd K,
+# groups that are not multiples of 64) plus one ragged case per group mode of
+# each kernel, at decode and prefill M.
+RAGGED_CASES = [
+    # (M, N, K, G, scale dtype)
+    (3, 128, 640, 1024, "bf16"),      # 5120 / 8: one short group
+    (3, 128, 3456, 1024, "bf16"),     # 27648 / 8: a short last group of 384
+    (1, 256, 13824, 1024, "f16"),     # 27648 / 2
+    (3, 128, 1057, 1024, "bf16"),
+    (3, 128, 1279, 1024, "f16"),
+    (3, 128, 1025, 1024, "bf16"),
+    (3, 128, 33, 1024, "bf16"),
+    (3, 128, 1, 1024, "bf16"),
+    (3, 128, 65, 1024, "f16"),
+    (3, 128, 63, 1024, "bf16"),
+    (3, 128, 2049, 1024, "bf16"),
+    (2, 128, 1023, 1024, "f16"),
+    (2, 128, 35, 1024, "bf16"),
+    (3, 128, 100, 33, "bf16"),        # group stride 64, every group padded
+    (3, 128, 1057, 96, "f16"),        # group stride 128
+    (17, 256, 777, 1024, "bf16"),     # ragged M and a single short group
+    (4, 200, 5000, 128, "f16"),       # stride 128, last group of 8 in a padding tile
+    (5, 96, 900, 256, "bf16"),        # stride 256: last group ends on a lower slab
+    (3, 200, 232, 192, "bf16"),       # stride 192: two groups end in one tile
+    (1, 64, 2000, 320, "f16"),        # stride 320 with a K split across waves
+    (100, 300, 1057, 1024, "bf16"),   # prefill
+    (130, 256, 100, 33, "f16"),       # prefill, stride 64
+    (96, 200, 5000, 128, "bf16"),     # prefill, stride 128, last group on a lower half
+    (200, 136, 232, 192, "f16"),      # prefill, stride 192
+    (80, 128, 3456, 1024, "bf16"),    # prefill, TP shard
+]
+
+
+@pytest.mark.parametrize("M,N,K,G,sd", RAGGED_CASES)
+def test_gemm_ragged_k(pkg, dev, M, N, K, G, sd):
+    say(f"gemm ragged M={M} N={N} K={K} G={G} scales={sd}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=K + G, scale_dtype=sd)
+    y, P, a_q, a_s = run_hip(dev, xb, w, w_scale, N, K, G)
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    assert np.array_equal(a_q.cpu().numpy(), ow.pad_groups(q_ref, G)), "padded activation layout"
+    assert np.array_equal(tensor_bf16_bits(a_s), s_ref)
+    P_ref = ow.group_partials(q_ref, w, G, exact_int64=True)
+    assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
+    y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref, return_abs=True)
+    check_output(tensor_bf16_bits(y), y32, mag, ow.num_groups(K, G), f"ragged M{M} N{N} K{K} G{G}")
+
+
+@pytest.mark.parametrize("K,G", [(1057, 1024), (100, 33), (1057, 96), (3456, 1024), (5000, 128), (35, 1024),
+                                 (1, 1024), (1001, 100)])
+def test_quant_padded_layout_byte_exact(pkg, dev, K, G):
+    """Vector path (K % 8 == 0 and group % 8 == 0) and scalar path alike write
+    the padded group layout with zeroed padding."""
+    say(f"quant padded K={K} G={G}")
+    xb = pkg.synth.activations(6, K, seed=K * 3 + G)
+    x = bf16_bits_tensor(xb).to(dev)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, G)
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    assert a_q.shape == (6, ow.kpad(K, G))
+    assert np.array_equal(tensor_bf16_bits(a_s), s_ref)
+    assert np.array_equal(a_q.cpu().numpy(), ow.pad_groups(q_ref, G))
 
 
 @pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
@@ -197,7 +260,7 @@ def test_gemm_qwq_decode_shapes(pkg, dev, proj, M):
     y, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, 128, partials=False)
     q_ref, s_ref = ow.quant_act_per_token(xb)
     y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, 128, return_abs=True)
-    check_output(tensor_bf16_bits(y), y32, mag, K // 128, f"{proj} M{M}")
+    check_output(tensor_bf16_bits(y), y32, mag, ow.num_groups(K, 128), f"{proj} M{M}")
 
 
 @pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
@@ -212,7 +275,7 @@ def test_gemm_qwq_prefill_column_sample(pkg, dev, proj):
     cols = np.sort(np.random.default_rng(0).choice(N, 192, replace=False))
     q_ref, s_ref = ow.quant_act_per_token(xb)
     y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], 128, return_abs=True)
-    check_output(tensor_bf16_bits(y)[:, cols], y32, mag, K // 128, f"{proj} M{M}")
+    check_output(tensor_bf16_bits(y)[:, cols], y32, mag, ow.num_groups(K, 128), f"{proj} M{M}")
 
 
 def test_gemm_deterministic_and_stress(pkg, dev):
@@ -243,9 +306,11 @@ def test_gemm_m0_and_errors(dev):
         torch.ops.npu.w4a8_gemm(a_q.float(), a_s, w_tiles, s_tiles, N, K, G)
     with pytest.raises(RuntimeError, match="kpad"):
         torch.ops.npu.w4a8_repack(w_q[:, :64], ws, K, G)
-    with pytest.raises(RuntimeError, match="UNSUPPORTED"):
-        torch.ops.npu.w4a8_repack(torch.zeros((N, 160), dtype=torch.int8, device=dev),
-                                  torch.ones((3, N), dtype=torch.float16, device=dev), 300, 128)
+    with pytest.raises(RuntimeError, match="padded group layout"):
+        torch.ops.npu.w4a8_gemm(torch.zeros((2, 300), dtype=torch.int8, device=dev), a_s[:0].new_zeros(2),
+                                *torch.ops.npu.w4a8_repack(torch.zeros((N, 160), dtype=torch.int8, device=dev),
+                                                           torch.ones((3, N), dtype=torch.float16, device=dev),
+                                                           300, 128), N, 300, 128)
 
 
 def test_w4a8_linear_module(pkg, dev):
@@ -280,4 +345,4 @@ def test_workspace_reuse_across_shapes(pkg, dev):
         y, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, G, partials=False)
         q_ref, s_ref = ow.quant_act_per_token(xb)
         y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, return_abs=True)
-        check_output(tensor_bf16_bits(y), y32, mag, K // G, f"reuse step {i}")
+        check_output(tensor_bf16_bits(y), y32, mag, ow.num_groups(K, G), f"reuse step {i}")

@@ -51,6 +51,9 @@ def test_fake_kernels_give_shapes(pkg):
         x = torch.empty((5, 1024), dtype=torch.bfloat16, device="cuda")
         a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x)
         assert a_q.shape == (5, 1024) and a_q.dtype == torch.int8 and a_s.shape == (5,)
+        # with a ragged group geometry the quant output is the padded layout
+        x2 = torch.empty((5, 1057), dtype=torch.bfloat16, device="cuda")
+        assert torch.ops.npu.w4a8_quant_pertoken(x2, 1024)[0].shape == (5, 1088)
         w_q = torch.empty((300, 512), dtype=torch.int8, device="cuda")
         ws = torch.empty((8, 300), dtype=torch.float16, device="cuda")
         wt, st = torch.ops.npu.w4a8_repack(w_q, ws, 1024, 128)

@@ -154,6 +154,32 @@ def test_geometry_and_grouped_pack_match_reference(K, gk):
 
 
 @needs_ref
+@pytest.mark.parametrize("K,gk", RAGGED_CASES)
+def test_padded_activation_layout_matches_reference_planes(K, gk):
+    """pad_groups places activations where the reference's grouped MSD plane
+    split does (recombined a = 16*hi + lo + 8), with its padding decoding to 0."""
+    a = np.random.default_rng(K + gk).integers(-128, 128, size=(3, K)).astype(np.int8)
+    hi, lo = oref.split_planes_grouped(a, gk)
+    recombined = 16 * ow.unpack_int4(hi).astype(np.int32) + ow.unpack_int4(lo).astype(np.int32) + 8
+    assert np.array_equal(ow.pad_groups(a, gk).astype(np.int32), recombined)
+
+
+def test_pad_groups_closed_form():
+    """Brute force on the geometry's definition: element k of group k // group
+    sits at (k // group) * ceil_to(group, 64) + k % group; everything else is 0."""
+    for K, gk in ((100, 33), (1057, 96), (232, 192), (5000, 128), (1, 1024)):
+        v = np.random.default_rng(K).integers(-128, 128, size=(2, K)).astype(np.int8)
+        out = ow.pad_groups(v, gk)
+        stride = -(-gk // 64) * 64
+        dst = np.array([(k // gk) * stride + k % gk for k in range(K)])
+        assert out.shape == (2, ow.kpad(K, gk))
+        assert np.array_equal(out[:, dst], v)
+        rest = np.ones(out.shape[1], bool)
+        rest[dst] = False
+        assert not out[:, rest].any()
+
+
+@needs_ref
 def test_reference_ragged_layout_binary_passes():
     out = subprocess.run([str(oref.RAGGED_TEST)], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and "ALL PASS" in out.stdout, out.stdout[-2000:]

@@ -43,12 +43,8 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 int check_problem(int64_t M, int64_t N, int64_t K, int64_t group) {
     if (M < 0 || N <= 0 || K <= 0 || group <= 0)
         return fail(W4A8_ERR_SHAPE, "bad shape: M=%lld N=%lld K=%lld (need M>=0, N>0, K>0)", M, N, K);
-    if (M >= (1ll << 31) || N >= (1ll << 30) || K >= (1ll << 30))
+    if (M >= (1ll << 31) || N >= (1ll << 30) || K >= (1ll << 30) || group >= (1ll << 30))
         return fail(W4A8_ERR_SHAPE, "shape too large: M=%lld N=%lld K=%lld", M, N, K);
-    if (!geom::is_slab_aligned(K, group))
-        return fail(W4A8_ERR_UNSUPPORTED,
-                    "K=%lld group=%lld: this build needs group %% 64 == 0 and K %% group == 0 "
-                    "(ragged-K groups are not implemented yet)", K, group);
     return W4A8_OK;
 }
 
@@ -61,7 +57,9 @@ int check_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_
         return fail(W4A8_ERR_DTYPE, "scale_dtype %lld is neither F16 (0) nor BF16 (1)", scale_dtype);
     if (M == 0) return W4A8_OK;
     if (!a_q || !a_scale || !w_tiles || !s_tiles || !y) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
-    if (lda < K || ldy < N) return fail(W4A8_ERR_SHAPE, "lda=%lld must be >= K and ldy=%lld >= N", lda, ldy);
+    const int64_t kp = geom::kpad(K, group);
+    if (lda < kp || ldy < N)
+        return fail(W4A8_ERR_SHAPE, "lda=%lld must be >= kpad=%lld and ldy=%lld >= N", lda, kp, ldy);
     if (lda % 16 != 0 || !aligned(a_q, 16))
         return fail(W4A8_ERR_ALIGN, "a_q must be 16-byte aligned with lda %% 16 == 0 (lda=%lld)", lda);
     if (!aligned(w_tiles, 16) || !aligned(s_tiles, 2) || !aligned(y, 2) || !aligned(a_scale, 2))
@@ -119,20 +117,23 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 1; }
+int w4a8_abi_version(void) { return 2; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
 int w4a8_quant_act(const void* x, int64_t ldx, void* a_q, int64_t lda, void* a_scale, int64_t M,
-                   int64_t K, void* stream) {
-    if (M < 0 || K <= 0 || M >= (1ll << 31) || K >= (1ll << 31))
-        return fail(W4A8_ERR_SHAPE, "bad shape: M=%lld K=%lld", M, K);
+                   int64_t K, int64_t group, void* stream) {
+    if (M < 0 || K <= 0 || M >= (1ll << 31) || K >= (1ll << 30) || group < 0 || group >= (1ll << 30))
+        return fail(W4A8_ERR_SHAPE, "bad shape: M=%lld K=%lld group=%lld", M, K, group);
     if (M == 0) return W4A8_OK;
     if (!x || !a_q || !a_scale) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
-    if (ldx < K || lda < K) return fail(W4A8_ERR_SHAPE, "ldx=%lld and lda=%lld must be >= K=%lld", ldx, lda, K);
+    const int64_t width = group > 0 ? geom::kpad(K, group) : K;
+    if (ldx < K || lda < width)
+        return fail(W4A8_ERR_SHAPE, "ldx=%lld must be >= K and lda=%lld >= the output width %lld", ldx, lda, width);
     if (!aligned(x, 2) || !aligned(a_scale, 2)) return fail(W4A8_ERR_ALIGN, "x and a_scale must be 2-byte aligned");
     return hip_status(launch_quant_act(static_cast<const uint16_t*>(x), ldx, static_cast<int8_t*>(a_q), lda,
-                                       static_cast<uint16_t*>(a_scale), M, K, static_cast<hipStream_t>(stream)),
+                                       static_cast<uint16_t*>(a_scale), M, K, group,
+                                       static_cast<hipStream_t>(stream)),
                       "w4a8_quant_act launch");
 }
 
@@ -161,7 +162,7 @@ int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_t
 }
 
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
-    if (M <= 0 || N <= 0 || K <= 0 || group <= 0 || !geom::is_slab_aligned(K, group)) return 0;
+    if (M <= 0 || N <= 0 || K <= 0 || group <= 0) return 0;
     return (M <= kDecodeMaxM) ? decode_workspace_bytes(M, N, K, group) : prefill_workspace_bytes(M, N, K, group);
 }
 

@@ -44,7 +44,8 @@ struct DecodeParams {
     int32_t* P;        // optional partial dump [NG, M, N]
     int M, N, K;
     int KT, NG, NB;
-    int spg;           // 64-K slabs per group
+    int nslab;         // 64-K slabs of the padded K axis (kpad / 64)
+    int spg;           // 64-K slabs per group stride (ceil_to(group, 64) / 64)
     int gshift;        // GM 1: log2(tiles per group)
     int unit;          // tiles per K-split unit (group and tile aligned)
     int units;         // ceil(KT / unit)
@@ -54,9 +55,13 @@ struct DecodeParams {
 // Offset that every buffer here treats as out of range (reads return zero).
 constexpr uint32_t kOOB = 0x80000000u;
 
-// GM: 0 = group 64 (a group per slab), 1 = group 128 * 2^gshift (groups end on
-// a tile's upper slab), 2 = any other multiple of 64 (a group ends on either
-// slab; at most one per tile).
+// K is walked in the padded group layout (kgeom.h): group g occupies slabs
+// [g*spg, (g+1)*spg) and only the last group may be shorter; the last slab
+// nslab-1 always ends a group, and a last tile may hold a padding slab.
+// GM: 0 = group stride 64 (a group per slab), 1 = group stride 128 * 2^gshift
+// (groups end on a tile's upper slab, or on the last tile), 2 = any other
+// stride (a group ends on either slab; a short last group may end right after
+// another group in the same tile, so each slab carries its own scale).
 template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP>
 __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodeParams p) {
     constexpr int R = 16 * MT;
@@ -98,13 +103,13 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
         ao[mt] = row < static_cast<uint32_t>(p.M) ? row * static_cast<uint32_t>(p.lda) + (lane >> 4) * 16u : kOOB;
     }
 
-    // Group bookkeeping.  end_slab(t): -1, 0 or 1 = which slab of tile t ends
-    // a group; gend(t): that group (clamped, for the scale load).
+    // gend(t, h): the group whose scale slab h of tile t folds with (GM 1:
+    // the group ending in tile t), clamped for the scale load.
     auto gend = [&](int t, int h) -> int {
         int g;
         if constexpr (GM == 0) g = 2 * t + h;
         else if constexpr (GM == 1) g = t >> p.gshift;
-        else g = ((2 * t + 1) % p.spg == 0) ? (2 * t) / p.spg : (2 * t + 1) / p.spg;
+        else g = (2 * t + h) / p.spg;
         return min(g, p.NG - 1);
     };
 
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     // ending in them (two per tile for group 64, one otherwise), and DA tiles
     // of activations (L2-resident, so a shallower ring keeps the registers of
     // the 32- to 64-row tiles in budget).
-    constexpr int NS = GM == 0 ? 2 : 1;
+    constexpr int NS = GM == 1 ? 1 : 2;
     constexpr int DA = MT >= 3 ? 2 : D;
     static_assert(D % DA == 0, "activation ring depth must divide D");
     uint4 wb[D][CPW];
@@ -205,12 +210,15 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
                 }
                 if (h == 1) load_a(s % DA, t + DA);
                 if constexpr (GM == 0) {
+                    // a padding slab past S folds group NG: zero partials,
+                    // not dumped
                     fold(2 * t + h, t < tb, sc, h);
                 } else if constexpr (GM == 1) {
-                    if (h == 1 && ((t + 1) & ((1 << p.gshift) - 1)) == 0) fold(t >> p.gshift, t < tb, sc, 0);
+                    if (h == 1 && (((t + 1) & ((1 << p.gshift) - 1)) == 0 || t == p.KT - 1))
+                        fold(t >> p.gshift, t < tb, sc, 0);
                 } else {
                     const int sg = 2 * t + h;
-                    if (((sg + 1) % p.spg) == 0) fold(sg / p.spg, t < tb, sc, 0);
+                    if (sg < p.nslab && (((sg + 1) % p.spg) == 0 || sg == p.nslab - 1)) fold(sg / p.spg, t < tb, sc, h);
                 }
             }
         }
@@ -314,10 +322,13 @@ DecodeParams make_params(const GemmArgs& a) {
     p.KT = static_cast<int>(geom::k_tiles(a.K, a.group));
     p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
     p.NB = static_cast<int>(geom::col_blocks(a.N));
-    p.spg = static_cast<int>(a.group / 64);
+    p.nslab = static_cast<int>(geom::kpad(a.K, a.group) / 64);
+    p.spg = static_cast<int>(geom::group_stride(a.group) / 64);
     p.gshift = 0;
     while ((2 << p.gshift) < p.spg) ++p.gshift;
-    p.a_bytes = static_cast<uint32_t>(a.M * a.lda);
+    // Rows end at kpad; reads past it (the padding slab of a last tile) meet
+    // zero weights, and in the last row they are out of range (zero).
+    p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + geom::kpad(a.K, a.group));
     p.w_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.KT) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.NG) * 16 * 2);
     // K-split boundaries fall on both tile (2 slabs) and group boundaries.

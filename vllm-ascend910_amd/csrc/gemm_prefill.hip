@@ -50,13 +50,16 @@ struct PrefillParams {
     int32_t* P;
     int M, N, K;
     int KT, NG, NB;
-    int group;
+    int gs;            // group stride on the padded K axis, ceil_to(group, 64)
+    int kpad;          // padded K; the last group ends here
     int tiles_m, tiles_n, band;
     uint32_t a_bytes, w_bytes, s_bytes;
 };
 
-// GMODE: 0 = group 64 (two groups per step), 1 = group 128 (one per step),
-// 2 = any other multiple of 64 (groups may start and end on either 64-K half).
+// K is walked in the padded group layout (kgeom.h): group g starts at g*gs,
+// only the last group may be shorter, and it ends at kpad.
+// GMODE: 0 = stride 64 (two groups per step), 1 = stride 128 (one per step),
+// 2 = any other stride (groups may start and end on either 64-K half).
 template <int GMODE, int DW, bool SBF16, bool DUMP>
 __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const PrefillParams p) {
     __shared__ __attribute__((aligned(16))) int8_t la[2][kBM * kLS];
@@ -120,7 +123,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         aoff[i] = r * kLS + cu;
     }
     auto load_a = [&](int kt, uint4 (&ra)[kNA]) {
-        // a half-empty last step reads past K: those bytes meet zero weights
+        // the padding half of a last step reads past kpad: zero weights there
         const uint32_t k = static_cast<uint32_t>(min(kt, p.KT - 1)) * 128u;
 #pragma unroll
         for (int i = 0; i < kNA; ++i) ra[i] = buf_load16(ra_rsrc, aoffg[i] + k);
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         const int ktc = min(kt, p.KT - 1);
 #pragma unroll
         for (int h = 0; h < NSC; ++h) {
-            const int g = min((ktc * 128 + (GMODE == 1 ? 127 : h * 64 + 63)) / p.group, p.NG - 1);
+            const int g = min((ktc * 128 + (GMODE == 1 ? 127 : h * 64 + 63)) / p.gs, p.NG - 1);
 #pragma unroll
             for (int j = 0; j < 2; ++j) sv[j][h] = buf_load_u16(rs_rsrc, soff[j] + static_cast<uint32_t>(g) * 32u);
         }
@@ -224,12 +227,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         // Slab-major: the four blocks' MFMA chains interleave, so no MFMA waits
         // on its predecessor's result.  A group ends after slab 1 or 3 (fixed
         // for groups 64/128, a uniform runtime test otherwise); both row blocks
-        // are folded then.  Groups past NG (the half-empty last step of an odd
-        // number of 64-groups) hold zero partials and fold nothing.
+        // are folded then.  Groups past NG (the padding half of a last step)
+        // hold zero partials and fold nothing; a short last group of stride
+        // 128 that ends on the lower half folds after the upper half's zero
+        // weights.
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             bool fresh = GMODE == 0 ? (s == 0 || s == 2) : (GMODE == 1 && s == 0);
-            if constexpr (GMODE == 2) fresh = (s == 0 || s == 2) && ((kt * 128 + s * 32) % p.group) == 0;
+            if constexpr (GMODE == 2) fresh = (s == 0 || s == 2) && ((kt * 128 + s * 32) % p.gs) == 0;
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 const v4i av = lds_a(rb, s);
@@ -238,8 +243,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
             }
             if (s == 1 || s == 3) {
                 const int kend = kt * 128 + (s + 1) * 32;   // K position after this slab
-                const int g = (kend - 1) / p.group;
-                const bool ends = GMODE == 0 || (GMODE == 1 ? s == 3 : (kend % p.group) == 0);
+                const int g = (kend - 1) / p.gs;
+                const bool ends = GMODE == 0 || (GMODE == 1 ? s == 3 : (kend <= p.kpad && (kend % p.gs == 0 || kend == p.kpad)));
                 if (ends) {
                     const int h = GMODE == 1 ? 0 : (s >> 1);
                     const uint32_t ws2[2] = {sc[0][h], sc[1][h]};
@@ -304,8 +309,8 @@ hipError_t launch_g(const PrefillParams& p, hipStream_t stream) {
 
 template <bool SBF16, bool DUMP>
 hipError_t launch(const PrefillParams& p, hipStream_t stream) {
-    if (p.group == 64) return launch_g<0, SBF16, DUMP>(p, stream);
-    if (p.group == 128) return launch_g<1, SBF16, DUMP>(p, stream);
+    if (p.gs == 64) return launch_g<0, SBF16, DUMP>(p, stream);
+    if (p.gs == 128) return launch_g<1, SBF16, DUMP>(p, stream);
     return launch_g<2, SBF16, DUMP>(p, stream);
 }
 
@@ -329,11 +334,14 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     p.KT = static_cast<int>(geom::k_tiles(a.K, a.group));
     p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
     p.NB = static_cast<int>(geom::col_blocks(a.N));
-    p.group = static_cast<int>(a.group);
+    p.gs = static_cast<int>(geom::group_stride(a.group));
+    p.kpad = static_cast<int>(geom::kpad(a.K, a.group));
     p.tiles_m = static_cast<int>(geom::ceil_div(a.M, kBM));
     p.tiles_n = static_cast<int>(geom::ceil_div(a.N, kBN));
     p.band = 4;
-    p.a_bytes = static_cast<uint32_t>(a.M * a.lda);
+    // rows end at kpad; the padding half of a last step meets zero weights and
+    // in the last row reads out of range (zero)
+    p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + p.kpad);
     p.w_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::k_tiles(a.K, a.group) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
     const bool dump = a.partials != nullptr;

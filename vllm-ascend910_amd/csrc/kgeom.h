@@ -57,10 +57,10 @@ __host__ __device__ constexpr int64_t kpad(int64_t K, int64_t group) {
 __host__ __device__ constexpr int64_t col_blocks(int64_t N) { return ceil_div(N, kTileN); }
 __host__ __device__ constexpr int64_t k_tiles(int64_t K, int64_t group) { return ceil_div(kpad(K, group), kTileK); }
 
-// The fast kernels need every group to be a whole number of 64-K slabs and no
-// ragged tail: K % group == 0 and group % 64 == 0.  Then kpad == K.
-__host__ __device__ constexpr bool is_slab_aligned(int64_t K, int64_t group) {
-    return group > 0 && K > 0 && (group % kSlabK) == 0 && (K % group) == 0;
+// True when the padded layout is the plain one (kpad == K): every group a
+// whole number of 64-element slabs, e.g. K % group == 0 and group % 64 == 0.
+__host__ __device__ constexpr bool is_unpadded(int64_t K, int64_t group) {
+    return group > 0 && K > 0 && kpad(K, group) == K;
 }
 
 }  // namespace geom

@@ -7,8 +7,10 @@
 
 namespace w4a8 {
 
+// group > 0 with a ragged geometry (kpad != K) writes the padded group layout.
 hipError_t launch_quant_act(const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t lda,
-                            uint16_t* a_scale, int64_t M, int64_t K, hipStream_t stream);
+                            uint16_t* a_scale, int64_t M, int64_t K, int64_t group,
+                            hipStream_t stream);
 
 hipError_t launch_repack(const uint8_t* w_q, const uint16_t* w_scale, uint8_t* w_tiles,
                          uint16_t* s_tiles, int64_t N, int64_t K, int64_t group,

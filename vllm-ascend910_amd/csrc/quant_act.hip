@@ -13,7 +13,14 @@
 // loads into registers, |x| is reduced as integers (for finite bf16 the
 // magnitude order equals the order of the 15 low bits), then the same
 // registers are quantised and written back as 8-byte int8 stores.
+//
+// Output order: plain (a_q[m, k]) or, for a ragged group geometry, the padded
+// group layout the GEMM reads (kgeom.h; the reference's quantiser writes its
+// activation planes in the same padded layout, midgroup_quant_a.inc:7-12):
+// code k goes to (k / group) * stride + k % group, and the padding slots of
+// every group are written as zero.
 #include "common.h"
+#include "kgeom.h"
 #include "launch.h"
 
 namespace w4a8 {
@@ -58,11 +65,40 @@ __device__ __forceinline__ uint32_t quant2(uint32_t u, float s) {
     return (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8);
 }
 
-// Vector path: K % 8 == 0, rows 16-byte aligned, K <= VPT * 8 * 256.
-template <int VPT>
+// Padded group layout of one row.
+struct PadMap {
+    int group;    // quant group
+    int stride;   // ceil_to(group, 64)
+    int G;        // groups
+    int kpad;     // padded row length
+};
+
+__device__ __forceinline__ int pad_dst(int k, const PadMap& pm) {
+    const int g = k / pm.group;
+    return g * pm.stride + (k - g * pm.group);
+}
+
+// Zero the padding slots [real, stride) of every group, in units of UNIT bytes
+// (real lengths are multiples of UNIT).
+template <int UNIT>
+__device__ __forceinline__ void zero_pads(int8_t* qr, int K, const PadMap& pm) {
+    for (int u = threadIdx.x; u < pm.kpad / UNIT; u += kThreads) {
+        const int p = u * UNIT;
+        const int g = p / pm.stride;
+        const int real = (g + 1 < pm.G) ? pm.group : K - (pm.G - 1) * pm.group;
+        if (p - g * pm.stride >= real) {
+            if constexpr (UNIT == 8) *reinterpret_cast<uint2*>(qr + p) = make_uint2(0u, 0u);
+            else qr[p] = 0;
+        }
+    }
+}
+
+// Vector path: K % 8 == 0, rows 16-byte aligned, K <= VPT * 8 * 256; with PAD
+// also group % 8 == 0 (an 8-code unit never straddles a group).
+template <int VPT, bool PAD>
 __global__ __launch_bounds__(kThreads) void quant_act_vec_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ aq, int64_t lda,
-    uint16_t* __restrict__ ascale, int K) {
+    uint16_t* __restrict__ ascale, int K, const PadMap pm) {
     __shared__ uint32_t red[4];
     const int64_t row = blockIdx.x;
     const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
@@ -80,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void quant_act_vec_kernel(
     const uint32_t sbits = scale_from_amax(amax);
     const float s = bf16_bits_to_f32(sbits);
     if (threadIdx.x == 0) ascale[row] = static_cast<uint16_t>(sbits);
-    uint2* qr = reinterpret_cast<uint2*>(aq + row * lda);
+    int8_t* qr = aq + row * lda;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
@@ -88,16 +124,17 @@ __global__ __launch_bounds__(kThreads) void quant_act_vec_kernel(
             uint2 o;
             o.x = quant2(v[i].x, s) | (quant2(v[i].y, s) << 16);
             o.y = quant2(v[i].z, s) | (quant2(v[i].w, s) << 16);
-            qr[idx] = o;
+            *reinterpret_cast<uint2*>(qr + (PAD ? pad_dst(idx * 8, pm) : idx * 8)) = o;
         }
     }
+    if constexpr (PAD) zero_pads<8>(qr, K, pm);
 }
 
 // General path: any K and strides; two passes over the row (the second one
 // hits cache).
 __global__ __launch_bounds__(kThreads) void quant_act_scalar_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ aq, int64_t lda,
-    uint16_t* __restrict__ ascale, int K) {
+    uint16_t* __restrict__ ascale, int K, bool pad, const PadMap pm) {
     __shared__ uint32_t red[4];
     const int64_t row = blockIdx.x;
     const uint16_t* xr = x + row * ldx;
@@ -109,34 +146,48 @@ __global__ __launch_bounds__(kThreads) void quant_act_scalar_kernel(
     if (threadIdx.x == 0) ascale[row] = static_cast<uint16_t>(sbits);
     int8_t* qr = aq + row * lda;
     for (int k = threadIdx.x; k < K; k += kThreads)
-        qr[k] = static_cast<int8_t>(quant1(bf16_bits_to_f32(xr[k]), s));
+        qr[pad ? pad_dst(k, pm) : k] = static_cast<int8_t>(quant1(bf16_bits_to_f32(xr[k]), s));
+    if (pad) zero_pads<1>(qr, K, pm);
 }
 
 }  // namespace
 
 hipError_t launch_quant_act(const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t lda,
-                            uint16_t* a_scale, int64_t M, int64_t K, hipStream_t stream) {
+                            uint16_t* a_scale, int64_t M, int64_t K, int64_t group, hipStream_t stream) {
     if (M == 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>(M));
     const dim3 block(kThreads);
-    const bool aligned = (K % 8 == 0) && (ldx % 8 == 0) && (lda % 8 == 0) &&
+    const bool pad = group > 0 && !geom::is_unpadded(K, group);
+    PadMap pm{};
+    if (pad) {
+        pm.group = static_cast<int>(group);
+        pm.stride = static_cast<int>(geom::group_stride(group));
+        pm.G = static_cast<int>(geom::num_groups(K, group));
+        pm.kpad = static_cast<int>(geom::kpad(K, group));
+    }
+    const bool aligned = (K % 8 == 0) && (ldx % 8 == 0) && (lda % 8 == 0) && (!pad || group % 8 == 0) &&
                          (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(a_q) % 8 == 0);
     const int64_t nvec = K / 8;
     const int iK = static_cast<int>(K);
-    if (aligned && nvec <= 1 * kThreads) {
-        quant_act_vec_kernel<1><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
-    } else if (aligned && nvec <= 2 * kThreads) {
-        quant_act_vec_kernel<2><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
-    } else if (aligned && nvec <= 4 * kThreads) {
-        quant_act_vec_kernel<4><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
-    } else if (aligned && nvec <= 8 * kThreads) {
-        quant_act_vec_kernel<8><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
-    } else if (aligned && nvec <= 16 * kThreads) {
-        quant_act_vec_kernel<16><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
-    } else {
-        quant_act_scalar_kernel<<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK);
+    int vpt = 0;
+    for (int v : {1, 2, 4, 8, 16})
+        if (vpt == 0 && aligned && nvec <= v * kThreads) vpt = v;
+#define W4A8_QVEC(V)                                                                                   \
+    case V:                                                                                            \
+        if (pad) quant_act_vec_kernel<V, true><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pm); \
+        else quant_act_vec_kernel<V, false><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pm);   \
+        break;
+    switch (vpt) {
+        W4A8_QVEC(1)
+        W4A8_QVEC(2)
+        W4A8_QVEC(4)
+        W4A8_QVEC(8)
+        W4A8_QVEC(16)
+        default:
+            quant_act_scalar_kernel<<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pad, pm);
     }
+#undef W4A8_QVEC
     return hipGetLastError();
 }
 

@@ -56,6 +56,7 @@ def repacked_scale_shape(N: int, K: int, group: int) -> tuple:
     return (col_blocks(N), num_groups(K, group), TILE_N)
 
 
-def is_slab_aligned(K: int, group: int) -> bool:
-    """True when the fast kernels apply: group % 64 == 0 and K % group == 0."""
-    return group > 0 and K > 0 and group % 64 == 0 and K % group == 0
+def is_unpadded(K: int, group: int) -> bool:
+    """True when the padded layout is the plain one (kpad == K), e.g. for
+    group % 64 == 0 and K % group == 0."""
+    return group > 0 and K > 0 and kpad(K, group) == K

@@ -5,7 +5,7 @@ its ops with TORCH_LIBRARY_FRAGMENT(npu, ...), npu_ops/host/midgroup_quant_a.cpp
 and npu_ops/host/midgroup_w4a8_gemm.cpp:149-153) and adds the per-token /
 group-size-parameterised ops of this build:
 
-    torch.ops.npu.w4a8_quant_pertoken(x) -> (a_q, a_scale)
+    torch.ops.npu.w4a8_quant_pertoken(x, group=0) -> (a_q, a_scale)
     torch.ops.npu.w4a8_repack(w_q, w_scale, K, group) -> (w_tiles, s_tiles)
     torch.ops.npu.w4a8_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> y
     torch.ops.npu.w4a8_gemm_partials(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> (y, partials)
@@ -27,7 +27,7 @@ from . import _abi
 from . import geometry as geo
 
 _LIB = torch.library.Library("npu", "FRAGMENT")
-_LIB.define("w4a8_quant_pertoken(Tensor x) -> (Tensor, Tensor)")
+_LIB.define("w4a8_quant_pertoken(Tensor x, int group=0) -> (Tensor, Tensor)")
 _LIB.define("w4a8_repack(Tensor w_q, Tensor w_scale, int K, int group) -> (Tensor, Tensor)")
 _LIB.define("w4a8_gemm(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
             "int N, int K, int group) -> Tensor")
@@ -63,26 +63,36 @@ def _workspace(dev: torch.device, need: int) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------- quant
+def _quant_width(K: int, group: int) -> int:
+    # group > 0: the GEMM's padded group layout (kpad == K when nothing is padded)
+    return geo.kpad(K, group) if group > 0 else K
+
+
 @torch.library.impl(_LIB, "w4a8_quant_pertoken", "CUDA")
-def _quant_pertoken_cuda(x: torch.Tensor):
+def _quant_pertoken_cuda(x: torch.Tensor, group: int = 0):
+    """a_q [M, K] (group 0) or [M, kpad(K, group)] in the padded group layout
+    the GEMM reads (padding slots zero), and a_scale bf16 [M]."""
     _require(x.dim() == 2, "w4a8_quant_pertoken: x must be [M, K]")
     _require(x.dtype == torch.bfloat16, "w4a8_quant_pertoken: x must be bfloat16")
+    _require(group >= 0, "w4a8_quant_pertoken: group must be >= 0")
     if x.stride(1) != 1:
         x = x.contiguous()
     M, K = x.shape
-    a_q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    width = _quant_width(K, group)
+    a_q = torch.empty((M, width), dtype=torch.int8, device=x.device)
     a_scale = torch.empty((M,), dtype=torch.bfloat16, device=x.device)
     if M:
-        _abi.check(_abi.lib().w4a8_quant_act(x.data_ptr(), x.stride(0), a_q.data_ptr(), K,
-                                             a_scale.data_ptr(), M, K, _stream(x.device)),
+        _abi.check(_abi.lib().w4a8_quant_act(x.data_ptr(), x.stride(0), a_q.data_ptr(), width,
+                                             a_scale.data_ptr(), M, K, group, _stream(x.device)),
                    "w4a8_quant_pertoken")
     return a_q, a_scale
 
 
 @torch.library.register_fake("npu::w4a8_quant_pertoken")
-def _quant_pertoken_fake(x):
+def _quant_pertoken_fake(x, group=0):
     M, K = x.shape
-    return x.new_empty((M, K), dtype=torch.int8), x.new_empty((M,), dtype=torch.bfloat16)
+    return (x.new_empty((M, _quant_width(K, group)), dtype=torch.int8),
+            x.new_empty((M,), dtype=torch.bfloat16))
 
 
 # ---------------------------------------------------------------- repack
@@ -121,8 +131,10 @@ def _repack_fake(w_q, w_scale, K, group):
 
 # ---------------------------------------------------------------- gemm
 def _check_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group):
-    _require(a_q.dim() == 2 and a_q.dtype == torch.int8, "w4a8_gemm: a_q must be int8 [M, K]")
-    _require(a_q.shape[1] == K, f"w4a8_gemm: a_q has {a_q.shape[1]} columns, K={K}")
+    _require(a_q.dim() == 2 and a_q.dtype == torch.int8, "w4a8_gemm: a_q must be int8 [M, kpad]")
+    _require(a_q.shape[1] == geo.kpad(K, group),
+             f"w4a8_gemm: a_q has {a_q.shape[1]} columns; the padded group layout of K={K}, "
+             f"group={group} has {geo.kpad(K, group)} (w4a8_quant_pertoken(x, group))")
     _require(a_scale.dtype == torch.bfloat16 and a_scale.dim() == 1 and a_scale.shape[0] == a_q.shape[0],
              "w4a8_gemm: a_scale must be bfloat16 [M]")
     _require(w_tiles.dtype == torch.uint8 and w_tiles.numel() == geo.repacked_weight_bytes(N, K, group),

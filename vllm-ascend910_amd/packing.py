@@ -41,11 +41,11 @@ def pack_grouped(codes: torch.Tensor, group: int) -> torch.Tensor:
     """[N, K] codes -> [N, kpad/2] packed with each group zero-padded to 64 elements.
 
     The reference's padded layout (npu_ops/python/w4a8_ops.py:231-239,
-    npu_ops/kernel/mg_kgeom.h:23-33).  For K % group == 0 and group % 64 == 0
-    this is just pack_int4(codes).
+    npu_ops/kernel/mg_kgeom.h:23-33).  When kpad == K (e.g. K % group == 0 and
+    group % 64 == 0) this is just pack_int4(codes).
     """
     N, K = codes.shape
-    if geo.is_slab_aligned(K, group):
+    if geo.is_unpadded(K, group):
         return pack_int4(codes)
     G = geo.num_groups(K, group)
     stride = geo.group_stride(group)
