@@ -119,6 +119,23 @@ int w4a8_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_t
               int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The same GEMM over a merged gate/up weight (N = 2*I output columns: gate
+ * rows [0, I), up rows [I, 2I), as vLLM's merged gate_up projection stores
+ * them) with the SwiGLU activation fused into its epilogue:
+ *   y[m, n] = bf16( bf16(silu(g)) * u ),  g = bf16(gemm[m, n]), u = bf16(gemm[m, n + I])
+ *   y        bf16 [M, ldy], ldy >= I;  I % 16 == 0
+ * silu(g) = g / (1 + exp(-g)) in fp32.  This is the rounding sequence of
+ * `F.silu(g) * u` on the bf16 GEMM output in the reference's decoder layer
+ * (npu_ops/python/bench_decode_layer.py:78-81; the vendor op it calls in its
+ * graph bench, torch_npu.npu_swiglu, npu_ops/python/bench_decode_graph.py:64),
+ * and every gate/up column accumulates exactly as in w4a8_gemm.  Saves the
+ * [M, 2I] intermediate and the activation kernel.
+ */
+int w4a8_gemm_swiglu(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
+                     const void* s_tiles, int scale_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Parity hook: the same GEMM, which also writes every per-group int32 partial
  *   partials int32 [G, M, N],  partials[g][m][n] = P_g[m,n]
  * from the production kernel's own accumulators.  The reference computes the

@@ -251,6 +251,25 @@ def gemm_f64(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_s
     return acc
 
 
+def silu_mul_bf16(g_bits: np.ndarray, u_bits: np.ndarray) -> np.ndarray:
+    """``F.silu(g) * u`` on bf16 tensors, as bf16 bits (npu_ops/python/bench_decode_layer.py:78-81).
+
+    torch evaluates silu of a bf16 tensor in fp32 as g / (1 + exp(-g)) and
+    rounds it to bf16, then multiplies two bf16 tensors in fp32 (exact: 8-bit
+    significands) and rounds to bf16.  Each fp32 step is restated correctly
+    rounded (exp taken in float64, then rounded to fp32, overflowing to inf
+    for g < -88.7 as the fp32 formula does, which gives silu = -0 there); an
+    fp32 exp may differ from it in the last bit, which moves the bf16 result
+    only at a rounding tie.
+    """
+    g = bf16_bits_to_f32(g_bits).astype(np.float32)
+    with np.errstate(over="ignore"):
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+        s32 = (g / (np.float32(1.0) + e).astype(np.float32)).astype(np.float32)
+    s = round_bf16(s32)
+    return f32_to_bf16_bits((s * bf16_bits_to_f32(u_bits)).astype(np.float32))
+
+
 def linear_bf16(x_bits: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray, group: int):
     """Whole path: per-token quant -> group GEMM -> bf16 (fakequant_lab/fake_linear.py:142-153).
 

@@ -346,3 +346,88 @@ def test_workspace_reuse_across_shapes(pkg, dev):
         q_ref, s_ref = ow.quant_act_per_token(xb)
         y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, return_abs=True)
         check_output(tensor_bf16_bits(y), y32, mag, ow.num_groups(K, G), f"reuse step {i}")
+
+
+# ------------------------------------------------------------------ SwiGLU epilogue
+def check_swiglu(got_bits: np.ndarray, exp_bits: np.ndarray, min_equal: float, tag: str) -> None:
+    """Every output within one bf16 ulp of the expected SwiGLU value and at least
+    `min_equal` of them bit-equal (the fp32 exp of the kernel and the correctly
+    rounded one of the oracle can straddle a bf16 rounding tie)."""
+    got = ow.bf16_bits_to_f32(got_bits).astype(np.float64)
+    exp = ow.bf16_bits_to_f32(exp_bits).astype(np.float64)
+    assert np.all(np.abs(got - exp) <= ow.bf16_ulp(exp)), f"{tag}: SwiGLU output off by more than 1 bf16 ulp"
+    eq = np.mean(got == exp)
+    assert eq >= min_equal, f"{tag}: only {eq:.5f} of SwiGLU outputs bit-equal"
+    assert np.any(exp != 0), f"{tag}: vacuous"
+
+
+def run_swiglu_pair(dev, xb, w, w_scale, N, K, G):
+    w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xb).to(dev), G)
+    y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+    yf = torch.ops.npu.w4a8_gemm_swiglu(a_q, a_s, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    return tensor_bf16_bits(y), tensor_bf16_bits(yf)
+
+
+SWIGLU_CASES = [
+    # (M, I, K, G, scale dtype): merged gate/up weight of N = 2*I rows
+    (1, 512, 1024, 128, "f16"),
+    (4, 1024, 2048, 64, "bf16"),
+    (33, 256, 1024, 256, "bf16"),
+    (64, 512, 5120, 512, "bf16"),
+    (3, 128, 1057, 1024, "bf16"),    # ragged K
+    (100, 272, 1024, 128, "bf16"),   # prefill, I not a multiple of the 64-column tile
+    (300, 512, 2048, 256, "f16"),
+    (130, 256, 1000, 192, "bf16"),   # prefill, ragged K at stride 192
+]
+
+
+@pytest.mark.parametrize("M,I,K,G,sd", SWIGLU_CASES)
+def test_gemm_swiglu(pkg, dev, M, I, K, G, sd):
+    """Fused epilogue == torch's F.silu(g) * u on the unfused GPU output (each
+    gate/up column accumulates as in the plain GEMM), and the whole chain
+    against the oracle."""
+    N = 2 * I
+    say(f"gemm swiglu M={M} I={I} K={K} G={G} scales={sd}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + I + K, scale_dtype=sd)
+    y, yf = run_swiglu_pair(dev, xb, w, w_scale, N, K, G)
+    assert yf.shape == (M, I)
+    check_swiglu(yf, ow.silu_mul_bf16(y[:, :I], y[:, I:]), 0.999, f"fused vs unfused M{M} I{I}")
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G)
+    full = ow.silu_mul_bf16(ow.f32_to_bf16_bits(y32[:, :I]), ow.f32_to_bf16_bits(y32[:, I:]))
+    got, exp = ow.bf16_bits_to_f32(yf).astype(np.float64), ow.bf16_bits_to_f32(full).astype(np.float64)
+    assert np.linalg.norm(got - exp) / np.linalg.norm(exp) <= 1e-3
+    assert np.mean(got == exp) > 0.99
+
+
+# Config 4 of the benchmark matrix: the four QwQ-32B projections at M in {16, 4096}
+# with groups 64/256/512, bf16 scales, codes round(clip(N(0, 2.5), -8, 7)); gate_up
+# with the fused SwiGLU (output 27648).  Oracle on a column sample (columns are
+# independent); the fused output against the unfused GPU output in full.
+@pytest.mark.parametrize("G", [64, 256, 512])
+@pytest.mark.parametrize("M", [16, 4096])
+@pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
+def test_config4_midgroup_variants(pkg, dev, proj, M, G):
+    K, N = pkg.synth.QWQ_SHAPES[proj]
+    say(f"config4 {proj} M={M} G={G}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + G, scale_dtype="bf16", codes="clipped_normal")
+    cols = np.sort(np.random.default_rng(G).choice(N // 2 if proj == "gate_up_proj" else N, 96, replace=False))
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    if proj == "gate_up_proj":
+        I = N // 2
+        y, yf = run_swiglu_pair(dev, xb, w, w_scale, N, K, G)
+        check_swiglu(yf, ow.silu_mul_bf16(y[:, :I], y[:, I:]), 0.999, f"config4 gate_up M{M} G{G}")
+        both = np.concatenate([cols, cols + I])
+        y32, mag = ow.gemm_fp32(q_ref, s_ref, w[both], ws32[both], G, return_abs=True)
+        check_output(y[:, both], y32, mag, ow.num_groups(K, G), f"config4 gate_up M{M} G{G}")
+        full = ow.silu_mul_bf16(ow.f32_to_bf16_bits(y32[:, :len(cols)]), ow.f32_to_bf16_bits(y32[:, len(cols):]))
+        got = ow.bf16_bits_to_f32(yf[:, cols]).astype(np.float64)
+        exp = ow.bf16_bits_to_f32(full).astype(np.float64)
+        assert np.linalg.norm(got - exp) / np.linalg.norm(exp) <= 1e-3
+    else:
+        y, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, G, partials=False)
+        y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G, return_abs=True)
+        check_output(tensor_bf16_bits(y)[:, cols], y32, mag, ow.num_groups(K, G), f"config4 {proj} M{M} G{G}")

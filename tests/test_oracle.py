@@ -238,3 +238,25 @@ def test_gemm_negative_control_transposed_scales():
     ws_bad = ow.bf16_bits_to_f32(wsb)[:, ::-1].copy()   # groups in the wrong order
     y_bad = ow.f32_to_bf16_bits(ow.gemm_fp32(a_q, a_s, w, ws_bad, 128))
     assert np.mean(y_bad == yr) < 0.5
+
+
+# --------------------------------------------------------------- SwiGLU
+def test_silu_mul_matches_torch_bf16():
+    """The oracle's SwiGLU against torch's own `F.silu(g) * u` on bf16 CPU
+    tensors (an independent fp32 silu): equal except where torch's fp32 silu
+    lands on the other side of a bf16 rounding tie, and never more than one
+    bf16 ulp apart."""
+    rng = np.random.default_rng(7)
+    g = ow.f32_to_bf16_bits((rng.standard_normal(200000) * 6).astype(np.float32))
+    u = ow.f32_to_bf16_bits((rng.standard_normal(200000) * 3).astype(np.float32))
+    g[:6] = ow.f32_to_bf16_bits(np.array([0.0, -0.0, 100.0, -100.0, 1e-30, -89.0], np.float32))
+    ours = ow.bf16_bits_to_f32(ow.silu_mul_bf16(g, u)).astype(np.float64)
+    tg = torch.from_numpy(g.view(np.int16)).view(torch.bfloat16)
+    tu = torch.from_numpy(u.view(np.int16)).view(torch.bfloat16)
+    ref = (torch.nn.functional.silu(tg) * tu).float().numpy().astype(np.float64)
+    assert np.mean(ours == ref) > 0.999
+    assert np.all(np.abs(ours - ref) <= ow.bf16_ulp(ref))
+    assert ours[3] == 0.0 and ours[5] == 0.0     # silu(-100), silu(-89): exp(-g) overflows fp32
+    # a plausible slip -- gate and up swapped -- is caught
+    wrong = ow.bf16_bits_to_f32(ow.silu_mul_bf16(u, g)).astype(np.float64)
+    assert np.mean(wrong == ref) < 0.5

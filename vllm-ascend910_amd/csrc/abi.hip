@@ -51,15 +51,18 @@ int check_problem(int64_t M, int64_t N, int64_t K, int64_t group) {
 int check_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
                const void* s_tiles, int scale_dtype, const void* y, int64_t ldy, int64_t M,
                int64_t N, int64_t K, int64_t group, const void* workspace,
-               int64_t workspace_bytes) {
+               int64_t workspace_bytes, bool swiglu) {
     if (int rc = check_problem(M, N, K, group)) return rc;
+    if (swiglu && N % 32 != 0)
+        return fail(W4A8_ERR_UNSUPPORTED, "SwiGLU needs N/2 (N=%lld) to be a multiple of 16", N);
     if (scale_dtype != W4A8_DT_F16 && scale_dtype != W4A8_DT_BF16)
         return fail(W4A8_ERR_DTYPE, "scale_dtype %lld is neither F16 (0) nor BF16 (1)", scale_dtype);
     if (M == 0) return W4A8_OK;
     if (!a_q || !a_scale || !w_tiles || !s_tiles || !y) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
     const int64_t kp = geom::kpad(K, group);
-    if (lda < kp || ldy < N)
-        return fail(W4A8_ERR_SHAPE, "lda=%lld must be >= kpad=%lld and ldy=%lld >= N", lda, kp, ldy);
+    const int64_t ncols = swiglu ? N / 2 : N;
+    if (lda < kp || ldy < ncols)
+        return fail(W4A8_ERR_SHAPE, "lda=%lld must be >= kpad=%lld and ldy=%lld >= the output width", lda, kp, ldy);
     if (lda % 16 != 0 || !aligned(a_q, 16))
         return fail(W4A8_ERR_ALIGN, "a_q must be 16-byte aligned with lda %% 16 == 0 (lda=%lld)", lda);
     if (!aligned(w_tiles, 16) || !aligned(s_tiles, 2) || !aligned(y, 2) || !aligned(a_scale, 2))
@@ -74,9 +77,9 @@ int check_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_
 int run_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
              const void* s_tiles, int scale_dtype, void* y, int64_t ldy, void* partials,
              int64_t M, int64_t N, int64_t K, int64_t group, void* workspace,
-             int64_t workspace_bytes, void* stream) {
+             int64_t workspace_bytes, void* stream, bool swiglu = false) {
     if (int rc = check_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, M, N, K,
-                            group, workspace, workspace_bytes))
+                            group, workspace, workspace_bytes, swiglu))
         return rc;
     if (M == 0) return W4A8_OK;
     GemmArgs a{};
@@ -89,6 +92,7 @@ int run_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_ti
     a.y = static_cast<uint16_t*>(y);
     a.ldy = ldy;
     a.partials = static_cast<int32_t*>(partials);
+    a.swiglu = swiglu;
     a.M = M;
     a.N = N;
     a.K = K;
@@ -171,6 +175,13 @@ int w4a8_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_t
               void* workspace, int64_t workspace_bytes, void* stream) {
     return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, nullptr, M, N, K, group,
                     workspace, workspace_bytes, stream);
+}
+
+int w4a8_gemm_swiglu(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
+                     const void* s_tiles, int scale_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream) {
+    return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, nullptr, M, N, K, group,
+                    workspace, workspace_bytes, stream, true);
 }
 
 int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,

@@ -50,6 +50,18 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     return u >> 16;
 }
 
+// SwiGLU of one gate/up output pair, rounded the way torch evaluates
+// `F.silu(g) * u` on bf16 tensors (the reference's decoder layer,
+// npu_ops/python/bench_decode_layer.py:78-81): g and u are first rounded to the
+// bf16 GEMM outputs, silu(g) = g / (1 + exp(-g)) is computed in fp32 and rounded
+// to bf16, and the product of the two bf16 values is rounded to bf16.
+__device__ __forceinline__ uint32_t swiglu_bf16_bits(float g32, float u32) {
+    const float g = bf16_bits_to_f32(f32_to_bf16_bits(g32));
+    const float u = bf16_bits_to_f32(f32_to_bf16_bits(u32));
+    const float s = bf16_bits_to_f32(f32_to_bf16_bits(g / (1.0f + expf(-g))));
+    return f32_to_bf16_bits(s * u);
+}
+
 // Scale entry -> fp32, for the two scale dtypes the op accepts.
 template <bool BF16>
 __device__ __forceinline__ float scale_to_f32(uint32_t bits) {

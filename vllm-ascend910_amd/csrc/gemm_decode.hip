@@ -44,6 +44,7 @@ struct DecodeParams {
     int32_t* P;        // optional partial dump [NG, M, N]
     int M, N, K;
     int KT, NG, NB;
+    int up_nb;         // SWIGLU: column blocks per half (gate block b pairs with up block b + up_nb)
     int nslab;         // 64-K slabs of the padded K axis (kpad / 64)
     int spg;           // 64-K slabs per group stride (ceil_to(group, 64) / 64)
     int gshift;        // GM 1: log2(tiles per group)
@@ -62,8 +63,12 @@ constexpr uint32_t kOOB = 0x80000000u;
 // (groups end on a tile's upper slab, or on the last tile), 2 = any other
 // stride (a group ends on either slab; a short last group may end right after
 // another group in the same tile, so each slab carries its own scale).
-template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP>
+// SWIGLU: the workgroup's first CPW/2 column blocks are gate blocks and the
+// rest the matching up blocks (output column n = silu(y[:, n]) * y[:, n + N/2]);
+// every column accumulates exactly as in the plain GEMM.
+template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP, bool SWIGLU>
 __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodeParams p) {
+    static_assert(!SWIGLU || (CPW % 2 == 0 && !DUMP), "SwiGLU pairs column blocks and dumps nothing");
     constexpr int R = 16 * MT;
     constexpr int C = 16 * CPW;
     // kw * R * C floats, sized at launch for the waves actually launched.
@@ -74,7 +79,9 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     // keeps the tile loop and fold conditions scalar.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kw = blockDim.x >> 6;
-    const int nb0 = blockIdx.x * CPW;
+    constexpr int CG = SWIGLU ? CPW / 2 : CPW;   // column blocks per output group
+    const int nb0 = blockIdx.x * CG;
+    auto block_of = [&](int c) { return (SWIGLU && c >= CG) ? nb0 + (c - CG) + p.up_nb : nb0 + c; };
     const int rowq = 4 * (lane >> 4);  // first output row of this lane in a 16-row tile
     const int colq = lane & 15;        // A row / output column of this lane in a 16-block
 
@@ -92,7 +99,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     for (int c = 0; c < CPW; ++c) {
         // a column block past NB (odd NB, last workgroup) re-reads the last
         // block; its columns are past N and never stored
-        const uint32_t nb = static_cast<uint32_t>(min(nb0 + c, p.NB - 1));
+        const uint32_t nb = static_cast<uint32_t>(min(block_of(c), p.NB - 1));
         wo[c] = nb * static_cast<uint32_t>(p.KT) * 1024u + lane * 16u;
         so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + colq) * 2u;
     }
@@ -163,7 +170,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 if constexpr (DUMP) {
-                    const int col = (nb0 + c) * 16 + colq;
+                    const int col = block_of(c) * 16 + colq;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int row = mt * 16 + rowq + i;
@@ -242,14 +249,31 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
 #pragma unroll
             for (int i = 0; i < 4; ++i) red[wave * R * C + (mt * 16 + rowq + i) * C + c * 16 + colq] = acc[mt][c][i];
     __syncthreads();
-    for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
-        const int row = e / C;
-        const int col = nb0 * 16 + (e - row * C);
-        if (row >= p.M || col >= p.N) continue;
-        float sum = red[e];
-        for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
-        const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
-        p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
+    if constexpr (SWIGLU) {
+        constexpr int CH = C / 2;
+        for (int e = threadIdx.x; e < R * CH; e += blockDim.x) {
+            const int row = e / CH;
+            const int cc = e - row * CH;
+            const int col = nb0 * 16 + cc;
+            if (row >= p.M || col >= p.up_nb * 16) continue;
+            float sg = red[row * C + cc], su = red[row * C + CH + cc];
+            for (int w = 1; w < kw; ++w) {
+                sg += red[w * R * C + row * C + cc];
+                su += red[w * R * C + row * C + CH + cc];
+            }
+            const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
+            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(swiglu_bf16_bits(sg * ts, su * ts));
+        }
+    } else {
+        for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
+            const int row = e / C;
+            const int col = nb0 * 16 + (e - row * C);
+            if (row >= p.M || col >= p.N) continue;
+            float sum = red[e];
+            for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
+            const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
+            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
+        }
     }
 }
 
@@ -264,15 +288,23 @@ int gcd_i(int a, int b) {
 
 constexpr int kwmax_for(int mt) { return mt == 1 ? 12 : (mt == 2 ? 8 : 4); }
 
-template <int MT, int CPW, int D, int GM, bool DUMP>
+// MODE: 0 = plain, 1 = plain with partial dump, 2 = SwiGLU epilogue.
+template <int MT, int CPW, int D, int GM, int MODE>
 hipError_t launch_g(const DecodeParams& p, int kw, bool sbf16, hipStream_t stream) {
     constexpr int KWM = kwmax_for(MT);
-    const int w = std::max(1, std::min(kw, KWM));
-    const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW)), block(64 * w);
-    const size_t lds = static_cast<size_t>(w) * 16 * MT * 16 * CPW * sizeof(float);
-    if (sbf16) gemm_decode_kernel<MT, CPW, KWM, D, GM, true, DUMP><<<grid, block, lds, stream>>>(p);
-    else gemm_decode_kernel<MT, CPW, KWM, D, GM, false, DUMP><<<grid, block, lds, stream>>>(p);
-    return hipGetLastError();
+    constexpr bool DUMP = MODE == 1, SWIGLU = MODE == 2;
+    if constexpr (SWIGLU && CPW % 2 != 0) {
+        return hipErrorInvalidValue;
+    } else {
+        const int w = std::max(1, std::min(kw, KWM));
+        constexpr int CG = SWIGLU ? CPW / 2 : CPW;
+        const int nbg = SWIGLU ? p.up_nb : p.NB;
+        const dim3 grid(static_cast<unsigned>((nbg + CG - 1) / CG)), block(64 * w);
+        const size_t lds = static_cast<size_t>(w) * 16 * MT * 16 * CPW * sizeof(float);
+        if (sbf16) gemm_decode_kernel<MT, CPW, KWM, D, GM, true, DUMP, SWIGLU><<<grid, block, lds, stream>>>(p);
+        else gemm_decode_kernel<MT, CPW, KWM, D, GM, false, DUMP, SWIGLU><<<grid, block, lds, stream>>>(p);
+        return hipGetLastError();
+    }
 }
 
 // Group mode: 64 -> 0; 128 * 2^s -> 1; anything else -> 2.
@@ -282,27 +314,30 @@ int group_mode(int spg) {
     return 2;
 }
 
-template <int MT, int CPW, int D, bool DUMP>
+template <int MT, int CPW, int D, int MODE>
 hipError_t launch_v(const DecodeParams& p, int kw, bool sbf16, hipStream_t stream) {
     switch (group_mode(p.spg)) {
-        case 0: return launch_g<MT, CPW, D, 0, DUMP>(p, kw, sbf16, stream);
-        case 1: return launch_g<MT, CPW, D, 1, DUMP>(p, kw, sbf16, stream);
-        default: return launch_g<MT, CPW, D, 2, DUMP>(p, kw, sbf16, stream);
+        case 0: return launch_g<MT, CPW, D, 0, MODE>(p, kw, sbf16, stream);
+        case 1: return launch_g<MT, CPW, D, 1, MODE>(p, kw, sbf16, stream);
+        default: return launch_g<MT, CPW, D, 2, MODE>(p, kw, sbf16, stream);
     }
 }
 
-// The variants that are built: (MT, D, CPW).
-template <bool DUMP>
+// The variants that are built: (MT, D, CPW); the SwiGLU epilogue needs an
+// even CPW.
+template <int MODE>
 hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool sbf16, hipStream_t s) {
     const int mt = (p.M + 15) / 16;
-    if (mt == 1 && c.D == 8 && c.CPW == 1) return launch_v<1, 1, 8, DUMP>(p, c.KW, sbf16, s);
-    if (mt == 1 && c.D == 4 && c.CPW == 1) return launch_v<1, 1, 4, DUMP>(p, c.KW, sbf16, s);
-    if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, DUMP>(p, c.KW, sbf16, s);
-    if (mt == 2 && c.D == 4 && c.CPW == 1) return launch_v<2, 1, 4, DUMP>(p, c.KW, sbf16, s);
-    if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, DUMP>(p, c.KW, sbf16, s);
-    if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, DUMP>(p, c.KW, sbf16, s);
-    if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, DUMP>(p, c.KW, sbf16, s);
-    if (mt == 4 && c.D == 2 && c.CPW == 4) return launch_v<4, 4, 2, DUMP>(p, c.KW, sbf16, s);
+    if constexpr (MODE != 2) {
+        if (mt == 1 && c.D == 8 && c.CPW == 1) return launch_v<1, 1, 8, MODE>(p, c.KW, sbf16, s);
+        if (mt == 1 && c.D == 4 && c.CPW == 1) return launch_v<1, 1, 4, MODE>(p, c.KW, sbf16, s);
+        if (mt == 2 && c.D == 4 && c.CPW == 1) return launch_v<2, 1, 4, MODE>(p, c.KW, sbf16, s);
+    }
+    if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 4 && c.D == 2 && c.CPW == 4) return launch_v<4, 4, 2, MODE>(p, c.KW, sbf16, s);
     return hipErrorInvalidValue;
 }
 
@@ -322,6 +357,7 @@ DecodeParams make_params(const GemmArgs& a) {
     p.KT = static_cast<int>(geom::k_tiles(a.K, a.group));
     p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
     p.NB = static_cast<int>(geom::col_blocks(a.N));
+    p.up_nb = a.swiglu ? static_cast<int>(a.N / 2 / geom::kTileN) : 0;
     p.nslab = static_cast<int>(geom::kpad(a.K, a.group) / 64);
     p.spg = static_cast<int>(geom::group_stride(a.group) / 64);
     p.gshift = 0;
@@ -370,8 +406,8 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
 
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream) {
     const DecodeParams p = make_params(a);
-    return a.partials ? dispatch<true>(p, cfg, a.scale_bf16, stream)
-                      : dispatch<false>(p, cfg, a.scale_bf16, stream);
+    if (a.swiglu) return dispatch<2>(p, cfg, a.scale_bf16, stream);
+    return a.partials ? dispatch<1>(p, cfg, a.scale_bf16, stream) : dispatch<0>(p, cfg, a.scale_bf16, stream);
 }
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {

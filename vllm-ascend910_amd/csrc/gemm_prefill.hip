@@ -52,6 +52,7 @@ struct PrefillParams {
     int KT, NG, NB;
     int gs;            // group stride on the padded K axis, ceil_to(group, 64)
     int kpad;          // padded K; the last group ends here
+    int half_n;        // SWIGLU: N / 2 (gate column n pairs with up column n + half_n)
     int tiles_m, tiles_n, band;
     uint32_t a_bytes, w_bytes, s_bytes;
 };
@@ -60,8 +61,13 @@ struct PrefillParams {
 // only the last group may be shorter, and it ends at kpad.
 // GMODE: 0 = stride 64 (two groups per step), 1 = stride 128 (one per step),
 // 2 = any other stride (groups may start and end on either 64-K half).
-template <int GMODE, int DW, bool SBF16, bool DUMP>
+// SWIGLU: a wave's two 32-column blocks are 32 gate columns and the matching
+// up columns, so each lane holds both operands of its outputs
+// silu(y[:, n]) * y[:, n + N/2] (a tile covers 64 outputs); every column
+// accumulates exactly as in the plain GEMM.
+template <int GMODE, int DW, bool SBF16, bool DUMP, bool SWIGLU>
 __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const PrefillParams p) {
+    static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
     __shared__ __attribute__((aligned(16))) int8_t la[2][kBM * kLS];
 
     const int tid = threadIdx.x;
@@ -87,7 +93,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         tile_n = inband / rows;
     }
     const int m0 = tile_m * kBM;
-    const int n0 = tile_n * kBN;
+    const int n0 = tile_n * (SWIGLU ? kBN / 2 : kBN);
     const int c32 = lane & 31;   // column (B) / row (A) inside a 32-block
     const int hh = lane >> 5;    // K half of the 32-K slab
 
@@ -102,7 +108,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     int colj[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int col = n0 + wn * 64 + j * 32 + c32;
+        const int col = SWIGLU ? n0 + wn * 32 + c32 + j * p.half_n : n0 + wn * 64 + j * 32 + c32;
         colj[j] = col;
         const uint32_t tile0 = static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u;
         woff[j][0] = tile0 + static_cast<uint32_t>((col & 15) + 16 * hh) * 16u;        // slabs 0, 2
@@ -289,10 +295,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
             const int row = m0 + wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
             if (row >= p.M) continue;
             const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
+            if constexpr (SWIGLU) {
+                const int col = colj[0];
+                if (col < p.half_n)
+                    p.Y[static_cast<int64_t>(row) * p.ldy + col] =
+                        static_cast<uint16_t>(swiglu_bf16_bits(acc[rb][0][i] * ts, acc[rb][1][i] * ts));
+            } else {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = colj[j];
-                if (col < p.N) p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][j][i] * ts));
+                for (int j = 0; j < 2; ++j) {
+                    const int col = colj[j];
+                    if (col < p.N) p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][j][i] * ts));
+                }
             }
         }
     }
@@ -300,18 +313,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
 
 constexpr int kDW = 2;   // weight prefetch depth in K steps
 
-template <int GMODE, bool SBF16, bool DUMP>
+template <int GMODE, bool SBF16, bool DUMP, bool SWIGLU>
 hipError_t launch_g(const PrefillParams& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
-    gemm_prefill_kernel<GMODE, kDW, SBF16, DUMP><<<grid, dim3(kThreads), 0, stream>>>(p);
+    gemm_prefill_kernel<GMODE, kDW, SBF16, DUMP, SWIGLU><<<grid, dim3(kThreads), 0, stream>>>(p);
     return hipGetLastError();
 }
 
-template <bool SBF16, bool DUMP>
+template <bool SBF16, bool DUMP, bool SWIGLU>
 hipError_t launch(const PrefillParams& p, hipStream_t stream) {
-    if (p.gs == 64) return launch_g<0, SBF16, DUMP>(p, stream);
-    if (p.gs == 128) return launch_g<1, SBF16, DUMP>(p, stream);
-    return launch_g<2, SBF16, DUMP>(p, stream);
+    if (p.gs == 64) return launch_g<0, SBF16, DUMP, SWIGLU>(p, stream);
+    if (p.gs == 128) return launch_g<1, SBF16, DUMP, SWIGLU>(p, stream);
+    return launch_g<2, SBF16, DUMP, SWIGLU>(p, stream);
 }
 
 }  // namespace
@@ -337,16 +350,18 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     p.gs = static_cast<int>(geom::group_stride(a.group));
     p.kpad = static_cast<int>(geom::kpad(a.K, a.group));
     p.tiles_m = static_cast<int>(geom::ceil_div(a.M, kBM));
-    p.tiles_n = static_cast<int>(geom::ceil_div(a.N, kBN));
+    p.half_n = a.swiglu ? static_cast<int>(a.N / 2) : 0;
+    p.tiles_n = static_cast<int>(a.swiglu ? geom::ceil_div(a.N / 2, kBN / 2) : geom::ceil_div(a.N, kBN));
     p.band = 4;
     // rows end at kpad; the padding half of a last step meets zero weights and
     // in the last row reads out of range (zero)
     p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + p.kpad);
     p.w_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::k_tiles(a.K, a.group) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
+    if (a.swiglu) return a.scale_bf16 ? launch<true, false, true>(p, stream) : launch<false, false, true>(p, stream);
     const bool dump = a.partials != nullptr;
-    if (a.scale_bf16) return dump ? launch<true, true>(p, stream) : launch<true, false>(p, stream);
-    return dump ? launch<false, true>(p, stream) : launch<false, false>(p, stream);
+    if (a.scale_bf16) return dump ? launch<true, true, false>(p, stream) : launch<true, false, false>(p, stream);
+    return dump ? launch<false, true, false>(p, stream) : launch<false, false, false>(p, stream);
 }
 
 }  // namespace w4a8

@@ -27,6 +27,7 @@ struct GemmArgs {
     uint16_t* y;               // bf16 [M, ldy]
     int64_t ldy;
     int32_t* partials;         // optional int32 [G, M, N]
+    bool swiglu;               // y[:, n] = silu(gemm[:, n]) * gemm[:, n + N/2], n < N/2
     int64_t M, N, K, group;
     void* workspace;
     int64_t workspace_bytes;

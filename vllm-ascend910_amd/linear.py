@@ -37,12 +37,31 @@ def linear(x: torch.Tensor, w_tiles: torch.Tensor, s_tiles: torch.Tensor, N: int
     return y.reshape(*lead, N)
 
 
+def linear_swiglu(x: torch.Tensor, w_tiles: torch.Tensor, s_tiles: torch.Tensor, N: int, group: int
+                  ) -> torch.Tensor:
+    """silu(g) * u of a merged gate/up projection (N = 2*I), fused into the GEMM.
+
+    Equals ``g, u = linear(x, ...).split(N // 2, -1); F.silu(g) * u`` in bf16, the
+    reference decoder layer's MLP activation (npu_ops/python/bench_decode_layer.py:78-81).
+    """
+    lead, K = x.shape[:-1], x.shape[-1]
+    x2 = x.reshape(-1, K).to(torch.bfloat16).contiguous()
+    a_q, a_scale = torch.ops.npu.w4a8_quant_pertoken(x2, group)
+    y = torch.ops.npu.w4a8_gemm_swiglu(a_q, a_scale, w_tiles, s_tiles, N, K, group)
+    return y.reshape(*lead, N // 2)
+
+
 class W4A8Linear(nn.Module):
     """Drop-in W4A8 linear (symmetric int4 per-group weights, per-token int8 activations)."""
 
     def __init__(self, in_features: int, out_features: int, group: int = 128, bias: bool = False,
-                 scale_dtype: torch.dtype = torch.bfloat16, device=None):
+                 scale_dtype: torch.dtype = torch.bfloat16, device=None, act: Optional[str] = None):
         super().__init__()
+        if act not in (None, "swiglu"):
+            raise ValueError(f"W4A8Linear: unknown act {act!r}")
+        if act == "swiglu" and (bias or out_features % 32):
+            raise ValueError("W4A8Linear(act='swiglu'): merged gate/up without bias, out_features = 2*I, I % 16 == 0")
+        self.act = act
         self.in_features = in_features
         self.out_features = out_features
         self.group = group
@@ -57,11 +76,11 @@ class W4A8Linear(nn.Module):
         self.s_tiles: Optional[torch.Tensor] = None
 
     @classmethod
-    def from_float(cls, lin: nn.Linear, group: int = 128, scale_dtype: torch.dtype = torch.bfloat16
-                   ) -> "W4A8Linear":
+    def from_float(cls, lin: nn.Linear, group: int = 128, scale_dtype: torch.dtype = torch.bfloat16,
+                   act: Optional[str] = None) -> "W4A8Linear":
         """Quantise an nn.Linear's weight (symmetric RTN per group) and prepare it."""
         N, K = lin.weight.shape
-        m = cls(K, N, group, lin.bias is not None, scale_dtype, device=lin.weight.device)
+        m = cls(K, N, group, lin.bias is not None, scale_dtype, device=lin.weight.device, act=act)
         w_q, w_scale = quantize_weight(lin.weight.data, group, scale_dtype)
         m.weight_packed.copy_(w_q)
         m.weight_scale.copy_(w_scale.T)
@@ -81,4 +100,6 @@ class W4A8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.w_tiles is None:
             raise RuntimeError("W4A8Linear: call process_weights_after_loading() after loading weights")
+        if self.act == "swiglu":
+            return linear_swiglu(x, self.w_tiles, self.s_tiles, self.out_features, self.group)
         return linear(x, self.w_tiles, self.s_tiles, self.out_features, self.group, self.bias)

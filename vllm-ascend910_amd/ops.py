@@ -9,6 +9,7 @@ group-size-parameterised ops of this build:
     torch.ops.npu.w4a8_repack(w_q, w_scale, K, group) -> (w_tiles, s_tiles)
     torch.ops.npu.w4a8_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> y
     torch.ops.npu.w4a8_gemm_partials(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> (y, partials)
+    torch.ops.npu.w4a8_gemm_swiglu(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> y [M, N/2]
 
 Only the CUDA (= HIP on ROCm) dispatch key and fake (meta) kernels are
 registered: CPU tensors raise, there is no fallback path.  Each impl checks
@@ -33,6 +34,8 @@ _LIB.define("w4a8_gemm(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tile
             "int N, int K, int group) -> Tensor")
 _LIB.define("w4a8_gemm_partials(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
             "int N, int K, int group) -> (Tensor, Tensor)")
+_LIB.define("w4a8_gemm_swiglu(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
+            "int N, int K, int group) -> Tensor")
 
 _SCALE_DT = {torch.float16: _abi.W4A8_DT_F16, torch.bfloat16: _abi.W4A8_DT_BF16}
 
@@ -143,14 +146,17 @@ def _check_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group):
              "w4a8_gemm: s_tiles must be the scale output of w4a8_repack for (N, K, group)")
 
 
-def _run_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group, partials):
+def _run_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group, partials, swiglu=False):
     _check_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group)
+    if swiglu:
+        _require(N % 32 == 0, f"w4a8_gemm_swiglu: N={N} must be 2*I with I a multiple of 16")
     if a_q.stride(1) != 1 or a_q.stride(0) % 16:
         a_q = a_q.contiguous()
     a_scale = a_scale.contiguous()
     M = a_q.shape[0]
     dev = a_q.device
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ncols = N // 2 if swiglu else N
+    y = torch.empty((M, ncols), dtype=torch.bfloat16, device=dev)
     if M == 0:
         return y
     lib = _abi.lib()
@@ -158,8 +164,10 @@ def _run_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group, partials):
     ws = _workspace(dev, need) if need > 0 else None
     ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
     args_head = (a_q.data_ptr(), a_q.stride(0), a_scale.data_ptr(), w_tiles.data_ptr(), s_tiles.data_ptr(),
-                 _SCALE_DT[s_tiles.dtype], y.data_ptr(), N)
-    if partials is None:
+                 _SCALE_DT[s_tiles.dtype], y.data_ptr(), ncols)
+    if swiglu:
+        st = lib.w4a8_gemm_swiglu(*args_head, M, N, K, group, ws_ptr, ws_bytes, _stream(dev))
+    elif partials is None:
         st = lib.w4a8_gemm(*args_head, M, N, K, group, ws_ptr, ws_bytes, _stream(dev))
     else:
         st = lib.w4a8_gemm_debug_partials(*args_head, partials.data_ptr(), M, N, K, group, ws_ptr, ws_bytes,
@@ -176,6 +184,17 @@ def _gemm_cuda(a_q, a_scale, w_tiles, s_tiles, N: int, K: int, group: int):
 @torch.library.register_fake("npu::w4a8_gemm")
 def _gemm_fake(a_q, a_scale, w_tiles, s_tiles, N, K, group):
     return a_q.new_empty((a_q.shape[0], N), dtype=torch.bfloat16)
+
+
+@torch.library.impl(_LIB, "w4a8_gemm_swiglu", "CUDA")
+def _gemm_swiglu_cuda(a_q, a_scale, w_tiles, s_tiles, N: int, K: int, group: int):
+    """silu(y[:, :N/2]) * y[:, N/2:] of the merged gate/up GEMM, fused."""
+    return _run_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group, None, swiglu=True)
+
+
+@torch.library.register_fake("npu::w4a8_gemm_swiglu")
+def _gemm_swiglu_fake(a_q, a_scale, w_tiles, s_tiles, N, K, group):
+    return a_q.new_empty((a_q.shape[0], N // 2), dtype=torch.bfloat16)
 
 
 @torch.library.impl(_LIB, "w4a8_gemm_partials", "CUDA")
