@@ -7,10 +7,12 @@ shapes, M=1..4096".
 One step = the decode configuration: dynamic per-token int8
 quant + W4A8 GEMM for each QwQ-32B projection (qkv 5120->7168, o 5120->5120,
 gate_up 5120->55296, down 27648->5120) at M in {1, 4, 16, 64}, group 128 --
-16 linears.  Weights are rotated over distinct copies totalling >= 1 GiB so
-that every step streams them from HBM, not from the 256 MB Infinity Cache
-(the reference's cold protocol, int4_cube_lab/host/mg_harness.h:42, :215-219).
-Each step is replayed as a HIP graph (one per weight copy).
+16 linears.  Cold protocol (the reference's, int4_cube_lab/host/mg_harness.h:42,
+:215-219): every projection has a pool of >= 8 distinct weight copies totalling
+>= 1 GiB; each of the 16 linears of a step reads its own copy, and per-shape
+timings rotate through the pool, so no weight byte is re-read within 1 GiB of
+traffic -- far beyond the 256 MB Infinity Cache.  Each step is replayed as a
+HIP graph (8 graphs over distinct copies).
 
 ``value`` = algorithmic bytes of the 16 linears per step / step time, in
 GB/s: GEMM bytes N*K/2 + (K/G)*N*2 + M*K + 4*M + 2*M*N (weights, group scales, int8
@@ -63,6 +65,8 @@ def main():
     ap.add_argument("--cold-bytes", type=float, default=1.0, help="GiB of distinct weight copies to rotate")
     ap.add_argument("--detail-launches", type=int, default=40)
     ap.add_argument("--prefill-m", default="1024,4096")
+    ap.add_argument("--config4", action="store_true",
+                    help="also time configs[3]: groups 64/256/512 at M 16/4096, gate_up with the fused SwiGLU")
     ap.add_argument("--no-detail", action="store_true", help="only the timed steps (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -98,22 +102,32 @@ def main():
     props = torch.cuda.get_device_properties(dev)
 
     # ---------------------------------------------------------------- data
-    per_set = sum(synth.QWQ_SHAPES[p][0] * synth.QWQ_SHAPES[p][1] // 2 for p in PROJS)
-    copies = max(2, math.ceil(args.cold_bytes * 2 ** 30 / per_set))
-    log(f"bench: {props.name}, {copies} weight copies x {per_set / 1e6:.0f} MB")
     gen = torch.Generator(device=dev)
-    weights = {}
-    for pi, p in enumerate(PROJS):
+
+    def make_pool(p, G, codes_dist, scale_dtype, seed):
+        """>= 8 distinct repacked copies of projection p's weight, >= cold_bytes in total."""
         K, N = synth.QWQ_SHAPES[p]
-        weights[p] = []
-        for r in range(copies):
-            gen.manual_seed(1000 * pi + r)
-            codes = torch.randint(-8, 8, (N, K), dtype=torch.int8, device=dev, generator=gen)
+        per = gemm_bytes(0, N, K, G)
+        n = max(8, math.ceil(args.cold_bytes * 2 ** 30 / per))
+        pool = []
+        for r in range(n):
+            gen.manual_seed(seed + r)
+            if codes_dist == "uniform":
+                codes = torch.randint(-8, 8, (N, K), dtype=torch.int8, device=dev, generator=gen)
+            else:   # round(clip(N(0, 2.5), -8, 7)), configs[3]
+                codes = torch.randn((N, K), device=dev, generator=gen).mul_(2.5).clamp_(-8, 7).round_().to(torch.int8)
             w_q = pkg.packing.pack_int4(codes)
             del codes
-            ws = (torch.rand((K // GROUP, N), device=dev, generator=gen) * 0.018 + 0.002).to(torch.float16)
-            weights[p].append(torch.ops.npu.w4a8_repack(w_q, ws, K, GROUP))
+            ws = (torch.rand((K // G, N), device=dev, generator=gen) * 0.018 + 0.002).to(scale_dtype)
+            pool.append(torch.ops.npu.w4a8_repack(w_q, ws, K, G))
             del w_q, ws
+        return pool
+
+    weights = {p: make_pool(p, GROUP, "uniform", torch.float16, 1000 * pi) for pi, p in enumerate(PROJS)}
+    pool_bytes = {p: len(weights[p]) * gemm_bytes(0, synth.QWQ_SHAPES[p][1], synth.QWQ_SHAPES[p][0])
+                  for p in PROJS}
+    log(f"bench: {props.name}, weight pools " +
+        ", ".join(f"{p} {len(weights[p])} x {pool_bytes[p] / len(weights[p]) / 1e6:.1f} MB" for p in PROJS))
     xs = {}
     for M in DECODE_MS:
         for p in PROJS:
@@ -122,12 +136,15 @@ def main():
             xs[(M, p)] = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
     torch.cuda.synchronize()
 
+    n_graphs = 8
+
     def step(r):
+        # linear (M index mi, projection p) of graph r reads copy 4r + mi of p's pool
         outs = []
-        for M in DECODE_MS:
+        for mi, M in enumerate(DECODE_MS):
             for p in PROJS:
                 K, N = synth.QWQ_SHAPES[p]
-                wt, st = weights[p][r]
+                wt, st = weights[p][(len(DECODE_MS) * r + mi) % len(weights[p])]
                 a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(xs[(M, p)])
                 outs.append(torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP))
         return outs
@@ -136,7 +153,7 @@ def main():
         for i, M in enumerate(DECODE_MS):
             for j, p in enumerate(PROJS):
                 K, N = synth.QWQ_SHAPES[p]
-                wt, st = weights[p][(i * len(PROJS) + j) % copies]
+                wt, st = weights[p][i % len(weights[p])]
                 a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(xs[(M, p)])
                 torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP)
         src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev)
@@ -150,12 +167,12 @@ def main():
     cap = torch.cuda.Stream(device=dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(cap):
-        for r in range(copies):      # warm the capture stream (workspace is allocated here, not in capture)
+        for r in range(n_graphs):    # warm the capture stream (any allocation happens here, not in capture)
             step(r)
     torch.cuda.current_stream(dev).wait_stream(cap)
     torch.cuda.synchronize()
     graphs = []
-    for r in range(copies):
+    for r in range(n_graphs):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=cap):
             step(r)
@@ -167,11 +184,11 @@ def main():
 
     # ---------------------------------------------------------------- timed region
     for i in range(args.warmup):
-        graphs[i % copies].replay()
+        graphs[i % n_graphs].replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        graphs[(args.warmup + i) % copies].replay()
+        graphs[(args.warmup + i) % n_graphs].replay()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
@@ -193,8 +210,10 @@ def main():
         "data": "synthetic (seeded): bf16 N(0,1) activations with 0.1% outlier channels x20; int4 codes "
                 "uniform [-8,7]; fp16 group scales U[0.002,0.02]",
         "config": {"workload": "configs[1]: decode W4A8 linears (quant+GEMM), QwQ-32B qkv/o/gate_up/down, "
-                               "M in {1,4,16,64}, group 128, cold (weights rotated over "
-                               f"{copies} copies = {copies * per_set / 2 ** 30:.2f} GiB)",
+                               "M in {1,4,16,64}, group 128, cold (every linear reads its own weight copy; "
+                               "per-projection pools of " +
+                               ", ".join(f"{len(weights[p])}" for p in PROJS) +
+                               f" copies, {sum(pool_bytes.values()) / 2 ** 30:.2f} GiB)",
                    "group": GROUP, "linears_per_step": len(DECODE_MS) * len(PROJS),
                    "bytes_per_step": bytes_per_step},
     }
@@ -235,7 +254,7 @@ def main():
 
             def gemms(a_q=a_q, a_s=a_s, p=p, K=K, N=N):
                 for i in range(T):
-                    wt, st = weights[p][i % copies]
+                    wt, st = weights[p][i % len(weights[p])]
                     torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP)
 
             def quants(M=M, p=p):
@@ -279,7 +298,7 @@ def main():
 
             def gemms(a_q=a_q, a_s=a_s, p=p, K=K, N=N, Tp=Tp):
                 for i in range(Tp):
-                    wt, st = weights[p][i % copies]
+                    wt, st = weights[p][i % len(weights[p])]
                     torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP)
 
             us = time_graph(gemms) / Tp
@@ -290,10 +309,60 @@ def main():
             del x, a_q, a_s
     result["prefill_shapes"] = prefill
 
+    # ---------------------------------------------------------------- mid-group variants
+    if args.config4:
+        del weights
+        torch.cuda.empty_cache()
+        result["config4_shapes"] = config4(pkg, dev, synth, make_pool, time_graph, T)
+
     # ---------------------------------------------------------------- CPU baseline
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(pkg, dev, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def config4(pkg, dev, synth, make_pool, time_graph, T):
+    """the four projections at M in {16, 4096} with groups 64/256/512, bf16 scales and
+    clipped-normal codes; gate_up followed by SwiGLU (output 27648), fused and unfused."""
+    import numpy as np
+    import torch
+    rows = []
+    for G in (64, 256, 512):
+        for pi, p in enumerate(PROJS):
+            K, N = synth.QWQ_SHAPES[p]
+            pool = make_pool(p, G, "clipped_normal", torch.bfloat16, 50000 + 1000 * pi + G)
+            for M in (16, 4096):
+                x = torch.from_numpy(synth.activations(M, K, seed=M + G).view(np.int16)).view(torch.bfloat16).to(dev)
+                a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, G)
+                n = T if M <= 64 else 4
+                ops = {"gemm": lambda wt, st: torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, G)}
+                if p == "gate_up_proj":
+                    I = N // 2
+
+                    def unfused(wt, st):
+                        y = torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, G)
+                        return torch.nn.functional.silu(y[:, :I]) * y[:, I:]
+
+                    ops = {"swiglu_fused": lambda wt, st: torch.ops.npu.w4a8_gemm_swiglu(a_q, a_s, wt, st, N, K, G),
+                           "swiglu_unfused": unfused}
+                for name, op in ops.items():
+                    def launches(op=op):
+                        for i in range(n):
+                            op(*pool[i % len(pool)])
+                    us = time_graph(launches) / n
+                    # the fused op writes [M, N/2] instead of [M, N]
+                    b = gemm_bytes(M, N, K, G) - (M * N if name == "swiglu_fused" else 0)
+                    tops = 2 * M * N * K / us / 1e6
+                    rows.append({"proj": p, "M": M, "group": G, "op": name, "us": round(us, 2),
+                                 "GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                 "TOPS": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)})
+                    log(f"  config4 {p:13s} G={G:3d} M={M:5d} {name:15s}: {us:9.2f} us "
+                        f"{b / us / 1e3:7.1f} GB/s ({b / us / 1e3 / HBM_PEAK_GBS:.1%})  {tops:7.1f} TOPS "
+                        f"({tops / INT8_PEAK_TOPS:.1%})")
+                del x, a_q, a_s
+            del pool
+            torch.cuda.empty_cache()
+    return rows
 
 
 def trace_summary(db):

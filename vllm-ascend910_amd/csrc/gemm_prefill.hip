@@ -53,6 +53,7 @@ struct PrefillParams {
     int gs;            // group stride on the padded K axis, ceil_to(group, 64)
     int kpad;          // padded K; the last group ends here
     int half_n;        // SWIGLU: N / 2 (gate column n pairs with up column n + half_n)
+    int tpg;           // GMODE 3: K steps per group stride
     int tiles_m, tiles_n, band;
     uint32_t a_bytes, w_bytes, s_bytes;
 };
@@ -60,7 +61,9 @@ struct PrefillParams {
 // K is walked in the padded group layout (kgeom.h): group g starts at g*gs,
 // only the last group may be shorter, and it ends at kpad.
 // GMODE: 0 = stride 64 (two groups per step), 1 = stride 128 (one per step),
-// 2 = any other stride (groups may start and end on either 64-K half).
+// 3 = stride 128*t, t >= 2 (a group spans t steps and ends on a step's last
+// slab, or on the last step), 2 = any other stride (groups may start and end
+// on either 64-K half).
 // SWIGLU: a wave's two 32-column blocks are 32 gate columns and the matching
 // up columns, so each lane holds both operands of its outputs
 // silu(y[:, n]) * y[:, n + N/2] (a tile covers 64 outputs); every column
@@ -146,12 +149,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     };
     // Scales of the groups that may end in step kt: at its 64-K halves h=0,1
     // (group 128 only ends on the step's last slab, so one scale suffices).
-    constexpr int NSC = GMODE == 1 ? 1 : 2;
+    constexpr bool ONE_END = GMODE == 1 || GMODE == 3;   // groups end only on a step's last slab
+    constexpr int NSC = ONE_END ? 1 : 2;
     auto load_s = [&](int kt, uint32_t (&sv)[2][NSC]) {
         const int ktc = min(kt, p.KT - 1);
 #pragma unroll
         for (int h = 0; h < NSC; ++h) {
-            const int g = min((ktc * 128 + (GMODE == 1 ? 127 : h * 64 + 63)) / p.gs, p.NG - 1);
+            const int g = min((ktc * 128 + (ONE_END ? 127 : h * 64 + 63)) / p.gs, p.NG - 1);
 #pragma unroll
             for (int j = 0; j < 2; ++j) sv[j][h] = buf_load_u16(rs_rsrc, soff[j] + static_cast<uint32_t>(g) * 32u);
         }
@@ -232,15 +236,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
 
         // Slab-major: the four blocks' MFMA chains interleave, so no MFMA waits
         // on its predecessor's result.  A group ends after slab 1 or 3 (fixed
-        // for groups 64/128, a uniform runtime test otherwise); both row blocks
-        // are folded then.  Groups past NG (the padding half of a last step)
-        // hold zero partials and fold nothing; a short last group of stride
-        // 128 that ends on the lower half folds after the upper half's zero
-        // weights.
+        // for strides 64/128, one uniform test per step for 128*t, per half
+        // otherwise); both row blocks are folded then.  Strides 64/128 start
+        // each group with a zero accumulator operand; the others, whose group
+        // starts are not known at compile time, clear the accumulators after a
+        // fold (a per-MFMA select would cost 16 VALU operations per MFMA).
+        // Groups past NG (the padding half of a last step) hold zero partials
+        // and fold nothing; a short last group that ends on the lower half
+        // folds after the upper half's zero weights.
+        bool step_ends = false;
+        if constexpr (GMODE == 3) step_ends = (kt + 1) % p.tpg == 0 || kt == p.KT - 1;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            bool fresh = GMODE == 0 ? (s == 0 || s == 2) : (GMODE == 1 && s == 0);
-            if constexpr (GMODE == 2) fresh = (s == 0 || s == 2) && ((kt * 128 + s * 32) % p.gs) == 0;
+            const bool fresh = GMODE == 0 ? (s == 0 || s == 2) : (GMODE == 1 && s == 0);
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 const v4i av = lds_a(rb, s);
@@ -250,12 +258,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
             if (s == 1 || s == 3) {
                 const int kend = kt * 128 + (s + 1) * 32;   // K position after this slab
                 const int g = (kend - 1) / p.gs;
-                const bool ends = GMODE == 0 || (GMODE == 1 ? s == 3 : (kend <= p.kpad && (kend % p.gs == 0 || kend == p.kpad)));
+                bool ends;
+                if constexpr (GMODE == 0) ends = true;
+                else if constexpr (GMODE == 1) ends = s == 3;
+                else if constexpr (GMODE == 3) ends = s == 3 && step_ends;
+                else ends = kend <= p.kpad && (kend % p.gs == 0 || kend == p.kpad);
                 if (ends) {
-                    const int h = GMODE == 1 ? 0 : (s >> 1);
+                    const int h = ONE_END ? 0 : (s >> 1);
                     const uint32_t ws2[2] = {sc[0][h], sc[1][h]};
                     fold_rb(0, g, ws2);
                     fold_rb(1, g, ws2);
+                    if constexpr (GMODE >= 2) {
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j) P[rb][j] = zero16;
+                    }
                 }
             }
         }
@@ -324,6 +342,7 @@ template <bool SBF16, bool DUMP, bool SWIGLU>
 hipError_t launch(const PrefillParams& p, hipStream_t stream) {
     if (p.gs == 64) return launch_g<0, SBF16, DUMP, SWIGLU>(p, stream);
     if (p.gs == 128) return launch_g<1, SBF16, DUMP, SWIGLU>(p, stream);
+    if (p.gs % 128 == 0) return launch_g<3, SBF16, DUMP, SWIGLU>(p, stream);
     return launch_g<2, SBF16, DUMP, SWIGLU>(p, stream);
 }
 
@@ -349,6 +368,7 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     p.NB = static_cast<int>(geom::col_blocks(a.N));
     p.gs = static_cast<int>(geom::group_stride(a.group));
     p.kpad = static_cast<int>(geom::kpad(a.K, a.group));
+    p.tpg = p.gs / 128;
     p.tiles_m = static_cast<int>(geom::ceil_div(a.M, kBM));
     p.half_n = a.swiglu ? static_cast<int>(a.N / 2) : 0;
     p.tiles_n = static_cast<int>(a.swiglu ? geom::ceil_div(a.N / 2, kBN / 2) : geom::ceil_div(a.N, kBN));
