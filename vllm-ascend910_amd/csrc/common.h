@@ -24,6 +24,18 @@ constexpr int kBufferWord3 = 0x00020000;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
 }
+// Descriptor over [base + off, base + bytes): a uniform offset moved into the
+// SGPR base instead of every lane's offset (saves a VALU add per load); the
+// range check then applies to the lane offsets against bytes - off (0 when
+// off >= bytes: every read returns zero).  off and bytes are below 2^31; the
+// record count is a signed max, which stays a scalar instruction (an unsigned
+// saturating subtract would be selected as a VALU op and make the descriptor
+// divergent).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_at(const void* base, uint32_t off, uint32_t bytes) {
+    const int n = max(static_cast<int>(bytes) - static_cast<int>(off), 0);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(static_cast<const char*>(base)) + off, 0, n,
+                                             kBufferWord3);
+}
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
     return make_uint4(v.x, v.y, v.z, v.w);

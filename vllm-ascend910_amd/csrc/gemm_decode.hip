@@ -59,10 +59,13 @@ constexpr uint32_t kOOB = 0x80000000u;
 // K is walked in the padded group layout (kgeom.h): group g occupies slabs
 // [g*spg, (g+1)*spg) and only the last group may be shorter; the last slab
 // nslab-1 always ends a group, and a last tile may hold a padding slab.
-// GM: 0 = group stride 64 (a group per slab), 1 = group stride 128 * 2^gshift
-// (groups end on a tile's upper slab, or on the last tile), 2 = any other
-// stride (a group ends on either slab; a short last group may end right after
-// another group in the same tile, so each slab carries its own scale).
+// GM: 0 = group stride 64 (a group per slab), 3 = stride 128 (a group per
+// tile), 1 = stride 128 * 2^gshift, gshift >= 1 (groups end on a tile's upper
+// slab, or on the last tile), 2 = any other stride (a group ends on either
+// slab; a short last group may end right after another group in the same
+// tile, so each slab carries its own scale).  Modes 0 and 3 start every group
+// with a zero accumulator operand; 1 and 2, whose group starts are runtime
+// values, clear the accumulators after each fold.
 // SWIGLU: the workgroup's first CPW/2 column blocks are gate blocks and the
 // rest the matching up blocks (output column n = silu(y[:, n]) * y[:, n + N/2]);
 // every column accumulates exactly as in the plain GEMM.
@@ -91,23 +94,24 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     const int ta = ua * p.unit;
     const int tb = min(p.KT, ub * p.unit);
 
-    const auto rw = make_rsrc(p.W, p.w_bytes);
-    const auto ra = make_rsrc(p.A, p.a_bytes);
-    const auto rs = make_rsrc(p.S, p.s_bytes);
-    uint32_t wo[CPW], so[CPW], ao[MT];
+    // Per-lane offsets are fixed for the whole K loop; the tile's uniform
+    // offset goes into the descriptor base (make_rsrc_at).
+    uint32_t wo[CPW], so[CPW], ao[MT][2];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
         // a column block past NB (odd NB, last workgroup) re-reads the last
         // block; its columns are past N and never stored
         const uint32_t nb = static_cast<uint32_t>(min(block_of(c), p.NB - 1));
-        wo[c] = nb * static_cast<uint32_t>(p.KT) * 1024u + lane * 16u;
-        so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + colq) * 2u;
+        wo[c] = nb * static_cast<uint32_t>(p.KT) * 1024u + lane * 16u;   // tile 0
+        so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + colq) * 2u;     // group 0
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         // rows past M start past the buffer end; a slab past K meets zero weights
         const uint32_t row = static_cast<uint32_t>(mt * 16 + colq);
-        ao[mt] = row < static_cast<uint32_t>(p.M) ? row * static_cast<uint32_t>(p.lda) + (lane >> 4) * 16u : kOOB;
+        const uint32_t o = row < static_cast<uint32_t>(p.M) ? row * static_cast<uint32_t>(p.lda) + (lane >> 4) * 16u : kOOB;
+        ao[mt][0] = o;         // slab 0 of tile 0
+        ao[mt][1] = o + 64u;   // slab 1 (kOOB + 64 stays out of range)
     }
 
     // gend(t, h): the group whose scale slab h of tile t folds with (GM 1:
@@ -115,6 +119,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     auto gend = [&](int t, int h) -> int {
         int g;
         if constexpr (GM == 0) g = 2 * t + h;
+        else if constexpr (GM == 3) g = t;
         else if constexpr (GM == 1) g = t >> p.gshift;
         else g = (2 * t + h) / p.spg;
         return min(g, p.NG - 1);
@@ -124,29 +129,29 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     // ending in them (two per tile for group 64, one otherwise), and DA tiles
     // of activations (L2-resident, so a shallower ring keeps the registers of
     // the 32- to 64-row tiles in budget).
-    constexpr int NS = GM == 1 ? 1 : 2;
+    constexpr int NS = (GM == 1 || GM == 3) ? 1 : 2;
     constexpr int DA = MT >= 3 ? 2 : D;
     static_assert(D % DA == 0, "activation ring depth must divide D");
     uint4 wb[D][CPW];
     uint4 ab[DA][MT][2];
     uint32_t sb[D][CPW][NS];
     auto load_a = [&](int sa, int t) {
-        const uint32_t ka = static_cast<uint32_t>(min(t, p.KT - 1)) * 128u;
+        const auto ra = make_rsrc_at(p.A, static_cast<uint32_t>(min(t, p.KT - 1)) * 128u, p.a_bytes);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) ab[sa][mt][h] = buf_load16(ra, ao[mt] + ka + h * 64u);
+            for (int h = 0; h < 2; ++h) ab[sa][mt][h] = buf_load16(ra, ao[mt][h]);
     };
     auto load_slot = [&](int s, int t) {
-        // tiles past this wave's range read zero weights
-        const uint32_t tw = t < tb ? static_cast<uint32_t>(t) * 1024u : kOOB;
+        // tiles past this wave's range read zero weights (an empty descriptor)
+        const auto rw = make_rsrc_at(p.W, static_cast<uint32_t>(t) * 1024u, t < tb ? p.w_bytes : 0u);
 #pragma unroll
-        for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, wo[c] + tw);
+        for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, wo[c]);
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-            const uint32_t g = static_cast<uint32_t>(gend(min(t, p.KT - 1), j)) * 32u;
+            const auto rs = make_rsrc_at(p.S, static_cast<uint32_t>(gend(min(t, p.KT - 1), j)) * 32u, p.s_bytes);
 #pragma unroll
-            for (int c = 0; c < CPW; ++c) sb[s][c][j] = buf_load_u16(rs, so[c] + g);
+            for (int c = 0; c < CPW; ++c) sb[s][c][j] = buf_load_u16(rs, so[c]);
         }
     };
 
@@ -180,7 +185,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[mt][c][i] += static_cast<float>(P[mt][c][i]) * ws;
-                P[mt][c] = v4i{0, 0, 0, 0};
+                if constexpr (GM == 1 || GM == 2) P[mt][c] = v4i{0, 0, 0, 0};
             }
         }
     };
@@ -208,18 +213,21 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
             const auto& av = ab[s % DA];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
+                const bool fresh = GM == 0 || (GM == 3 && h == 0);   // a group starts on this slab
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const uint4 v = av[mt][h];
                     const v4i a = {static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
 #pragma unroll
-                    for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(a, b[c][h], P[mt][c]);
+                    for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(a, b[c][h], fresh ? v4i{0, 0, 0, 0} : P[mt][c]);
                 }
                 if (h == 1) load_a(s % DA, t + DA);
                 if constexpr (GM == 0) {
                     // a padding slab past S folds group NG: zero partials,
                     // not dumped
                     fold(2 * t + h, t < tb, sc, h);
+                } else if constexpr (GM == 3) {
+                    if (h == 1) fold(t, t < tb, sc, 0);
                 } else if constexpr (GM == 1) {
                     if (h == 1 && (((t + 1) & ((1 << p.gshift) - 1)) == 0 || t == p.KT - 1))
                         fold(t >> p.gshift, t < tb, sc, 0);
@@ -286,12 +294,14 @@ int gcd_i(int a, int b) {
     return a;
 }
 
-constexpr int kwmax_for(int mt) { return mt == 1 ? 12 : (mt == 2 ? 8 : 4); }
+// Most waves per workgroup a variant is built for (its register budget: the
+// 64-row, 4-block variant needs 256 VGPRs at 2 waves per SIMD).
+constexpr int kwmax_for(int mt, int cpw) { return mt == 1 ? 12 : (mt == 2 || cpw <= 2 ? 8 : 4); }
 
 // MODE: 0 = plain, 1 = plain with partial dump, 2 = SwiGLU epilogue.
 template <int MT, int CPW, int D, int GM, int MODE>
 hipError_t launch_g(const DecodeParams& p, int kw, bool sbf16, hipStream_t stream) {
-    constexpr int KWM = kwmax_for(MT);
+    constexpr int KWM = kwmax_for(MT, CPW);
     constexpr bool DUMP = MODE == 1, SWIGLU = MODE == 2;
     if constexpr (SWIGLU && CPW % 2 != 0) {
         return hipErrorInvalidValue;
@@ -307,9 +317,11 @@ hipError_t launch_g(const DecodeParams& p, int kw, bool sbf16, hipStream_t strea
     }
 }
 
-// Group mode: 64 -> 0; 128 * 2^s -> 1; anything else -> 2.
+// Group mode by group stride: 64 -> 0; 128 -> 3; 128 * 2^s, s >= 1 -> 1;
+// anything else -> 2.
 int group_mode(int spg) {
     if (spg == 1) return 0;
+    if (spg == 2) return 3;
     if (spg % 2 == 0 && ((spg / 2) & (spg / 2 - 1)) == 0) return 1;
     return 2;
 }
@@ -319,6 +331,7 @@ hipError_t launch_v(const DecodeParams& p, int kw, bool sbf16, hipStream_t strea
     switch (group_mode(p.spg)) {
         case 0: return launch_g<MT, CPW, D, 0, MODE>(p, kw, sbf16, stream);
         case 1: return launch_g<MT, CPW, D, 1, MODE>(p, kw, sbf16, stream);
+        case 3: return launch_g<MT, CPW, D, 3, MODE>(p, kw, sbf16, stream);
         default: return launch_g<MT, CPW, D, 2, MODE>(p, kw, sbf16, stream);
     }
 }
