@@ -9,7 +9,9 @@
 // npu_ops/kernel/midgroup_quant_a.inc:55-62): a reciprocal multiply would flip
 // half-way cases relative to torch.
 //
-// Layout: one 256-thread workgroup per row.  The row is read once with 16-byte
+// Layout: one workgroup per row (256 threads, 1024 for rows longer than 8192
+// elements, so a decode-sized call still has enough loads in flight).  The row
+// is read once with 16-byte
 // loads into registers, |x| is reduced as integers (for finite bf16 the
 // magnitude order equals the order of the 15 low bits), then the same
 // registers are quantised and written back as 8-byte int8 stores.
@@ -33,14 +35,17 @@ __device__ __forceinline__ uint32_t abs_bits_max2(uint32_t u) {
     return max(u & 0x7fffu, (u >> 16) & 0x7fffu);
 }
 
-// Block-wide max of a uint32 over 256 threads.
+// Block-wide max of a uint32 over NT threads.
+template <int NT>
 __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64)));
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
-    v = max(max(red[0], red[1]), max(red[2], red[3]));
+    v = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) v = max(v, red[w]);
     return v;
 }
 
@@ -82,7 +87,7 @@ __device__ __forceinline__ int pad_dst(int k, const PadMap& pm) {
 // (real lengths are multiples of UNIT).
 template <int UNIT>
 __device__ __forceinline__ void zero_pads(int8_t* qr, int K, const PadMap& pm) {
-    for (int u = threadIdx.x; u < pm.kpad / UNIT; u += kThreads) {
+    for (int u = threadIdx.x; u < pm.kpad / UNIT; u += blockDim.x) {
         const int p = u * UNIT;
         const int g = p / pm.stride;
         const int real = (g + 1 < pm.G) ? pm.group : K - (pm.G - 1) * pm.group;
@@ -95,11 +100,11 @@ __device__ __forceinline__ void zero_pads(int8_t* qr, int K, const PadMap& pm) {
 
 // Vector path: K % 8 == 0, rows 16-byte aligned, K <= VPT * 8 * 256; with PAD
 // also group % 8 == 0 (an 8-code unit never straddles a group).
-template <int VPT, bool PAD>
-__global__ __launch_bounds__(kThreads) void quant_act_vec_kernel(
+template <int VPT, int NT, bool PAD>
+__global__ __launch_bounds__(NT) void quant_act_vec_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ aq, int64_t lda,
     uint16_t* __restrict__ ascale, int K, const PadMap pm) {
-    __shared__ uint32_t red[4];
+    __shared__ uint32_t red[NT / 64];
     const int64_t row = blockIdx.x;
     const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
     const int nvec = K >> 3;
@@ -107,19 +112,19 @@ __global__ __launch_bounds__(kThreads) void quant_act_vec_kernel(
     uint32_t amax = 0u;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-        const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+        const int idx = static_cast<int>(threadIdx.x) + i * NT;
         v[i] = (idx < nvec) ? xr[idx] : make_uint4(0u, 0u, 0u, 0u);
         amax = max(amax, max(max(abs_bits_max2(v[i].x), abs_bits_max2(v[i].y)),
                              max(abs_bits_max2(v[i].z), abs_bits_max2(v[i].w))));
     }
-    amax = block_max(amax, red);
+    amax = block_max<NT>(amax, red);
     const uint32_t sbits = scale_from_amax(amax);
     const float s = bf16_bits_to_f32(sbits);
     if (threadIdx.x == 0) ascale[row] = static_cast<uint16_t>(sbits);
     int8_t* qr = aq + row * lda;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-        const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+        const int idx = static_cast<int>(threadIdx.x) + i * NT;
         if (idx < nvec) {
             uint2 o;
             o.x = quant2(v[i].x, s) | (quant2(v[i].y, s) << 16);
@@ -140,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void quant_act_scalar_kernel(
     const uint16_t* xr = x + row * ldx;
     uint32_t amax = 0u;
     for (int k = threadIdx.x; k < K; k += kThreads) amax = max(amax, static_cast<uint32_t>(xr[k]) & 0x7fffu);
-    amax = block_max(amax, red);
+    amax = block_max<kThreads>(amax, red);
     const uint32_t sbits = scale_from_amax(amax);
     const float s = bf16_bits_to_f32(sbits);
     if (threadIdx.x == 0) ascale[row] = static_cast<uint16_t>(sbits);
@@ -170,22 +175,26 @@ hipError_t launch_quant_act(const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t
                          (reinterpret_cast<uintptr_t>(a_q) % 8 == 0);
     const int64_t nvec = K / 8;
     const int iK = static_cast<int>(K);
+    // rows of up to 8192 elements: 256 threads; longer rows: 1024 threads
     int vpt = 0;
-    for (int v : {1, 2, 4, 8, 16})
-        if (vpt == 0 && aligned && nvec <= v * kThreads) vpt = v;
-#define W4A8_QVEC(V)                                                                                   \
-    case V:                                                                                            \
-        if (pad) quant_act_vec_kernel<V, true><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pm); \
-        else quant_act_vec_kernel<V, false><<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pm);   \
-        break;
-    switch (vpt) {
-        W4A8_QVEC(1)
-        W4A8_QVEC(2)
-        W4A8_QVEC(4)
-        W4A8_QVEC(8)
-        W4A8_QVEC(16)
-        default:
-            quant_act_scalar_kernel<<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pad, pm);
+    const bool wide = nvec > 4 * kThreads;
+    const int nt = wide ? 4 * kThreads : kThreads;
+    for (int v : {1, 2, 4, 8})
+        if (vpt == 0 && aligned && nvec <= v * nt) vpt = v;
+#define W4A8_QVEC(V, NT)                                                                                      \
+    if (pad) quant_act_vec_kernel<V, NT, true><<<grid, dim3(NT), 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pm); \
+    else quant_act_vec_kernel<V, NT, false><<<grid, dim3(NT), 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pm);
+    if (vpt == 0) {
+        quant_act_scalar_kernel<<<grid, block, 0, stream>>>(x, ldx, a_q, lda, a_scale, iK, pad, pm);
+    } else if (!wide) {
+        if (vpt == 1) { W4A8_QVEC(1, kThreads) }
+        else if (vpt == 2) { W4A8_QVEC(2, kThreads) }
+        else { W4A8_QVEC(4, kThreads) }
+    } else {
+        if (vpt == 1) { W4A8_QVEC(1, 4 * kThreads) }
+        else if (vpt == 2) { W4A8_QVEC(2, 4 * kThreads) }
+        else if (vpt == 4) { W4A8_QVEC(4, 4 * kThreads) }
+        else { W4A8_QVEC(8, 4 * kThreads) }
     }
 #undef W4A8_QVEC
     return hipGetLastError();
