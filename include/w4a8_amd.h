@@ -147,6 +147,50 @@ int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale,
                              int64_t group, void* workspace, int64_t workspace_bytes,
                              void* stream);
 
+/*
+ * ---- Reference-compat mid-group path ----
+ * The reference's own op pair, on its own tensors, for callers that keep its
+ * exported mid-group checkpoints: per (token, K-group) activation scales, MSD
+ * activation planes and an asymmetric int4 weight with per-(group, channel)
+ * zero points.  Groups follow npu_ops/kernel/mg_kgeom.h (the reference fixes
+ * group = 1024).
+ *
+ * Mid-group activation quant.
+ *   x        bf16  [M, ldx]        (first K columns used)
+ *   a_hi     int8  [Mp, kpad/2]    packed int4, hi = q >> 4
+ *   a_lo     int8  [Mp, kpad/2]    packed int4, lo nibble = (q & 15) ^ 8
+ *   a_scale  bf16  [G, Mp]         s = bf16_rne(max_{k in g}|x| / 127), tiny if 0
+ *   a_ksum   int32 [G, Mp]         -sum_{k in g} q
+ * with q = clamp(rint(x / s), -128, 127) per group (fakequant_lab/quant.py:89-141),
+ * so that q = 16*hi + lo + 8.  Rows [M, Mp) are written as scale tiny, q = 0,
+ * ksum 0; padding slots of a short last group as q = 0.
+ * Replaces npu_ops/kernel/midgroup_quant_a.inc:112-410 bound by
+ * npu_ops/host/midgroup_quant_a.cpp:40-78 (run_midgroup_quant_a), whose caller
+ * chooses Mp = ceil_to(M, 16 | 64 | 128) (TileMFor, :37).
+ */
+int w4a8_midgroup_quant_a(const void* x, int64_t ldx, void* a_hi, void* a_lo, void* a_scale, void* a_ksum,
+                          int64_t M, int64_t Mp, int64_t K, int64_t group, void* stream);
+
+/*
+ * Mid-group W4A8 GEMM on the reference's tensors as stored:
+ *   a_hi, a_lo, a_scale, a_ksum   from w4a8_midgroup_quant_a (Ma rows; a_scale
+ *                                 and a_ksum [G, ld_as], ld_as >= Ma)
+ *   w_q      int8  [N, kpad/2]    packed int4 codes
+ *   w_scale  bf16  [G, N]
+ *   w_zero   bf16  [G, N]         zero point in code units, or NULL (symmetric)
+ *   y        bf16  [Ma, ldy]
+ *   partials int32 [G, Ma, N]     optional: I_g = sum_{k in g} A*(W - wz), exact
+ *   y[m,n] = bf16( sum_g (float(I_g[m,n]) * w_scale[g,n]) * a_scale[g,m] )
+ * (the reference's CPU definition, int4_cube_lab/host/gemm_ref.cpp:199-240).  The
+ * reference kernel's w_ksum input is not needed: the activation bytes are
+ * rebuilt exactly from the two planes.  Needs ceil_to(group, 64) % 128 == 0.
+ * Replaces npu_ops/kernel/midgroup_w4a8_gemm.inc:491-1169 bound by
+ * npu_ops/host/midgroup_w4a8_gemm.cpp:45-140 (run_midgroup_w4a8_gemm).
+ */
+int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
+                       int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y, int64_t ldy,
+                       void* partials, int64_t N, int64_t K, int64_t group, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,26 @@ def split_planes_grouped(a_q: np.ndarray, group: int):
     return hi, lo
 
 
+def act_ksum_neg(a_q: np.ndarray, group: int) -> np.ndarray:
+    """ActKSumNegPerGroup (gemm_ref.cpp): -sum_{k in g} A per (group, row), int32 [G, M]."""
+    a_q = np.ascontiguousarray(a_q, np.int8)
+    rows, K = a_q.shape
+    G = lib().ref_num_groups(K, group)
+    out = np.empty((G, rows), np.int32)
+    lib().ref_act_ksum_neg_per_group(_ptr(a_q), rows, K, group, _ptr(out))
+    return out
+
+
+def weight_ksum(w: np.ndarray, group: int) -> np.ndarray:
+    """WeightKSumPerGroup (gemm_ref.cpp): sum_{k in g} W per (group, column), int32 [G, N]."""
+    w = np.ascontiguousarray(w, np.int8)
+    rows, K = w.shape
+    G = lib().ref_num_groups(K, group)
+    out = np.empty((G, rows), np.int32)
+    lib().ref_weight_ksum_per_group(_ptr(w), rows, K, group, _ptr(out))
+    return out
+
+
 def midgroup_gemm(a_q: np.ndarray, a_scale_g: np.ndarray, w_codes: np.ndarray, w_scale_g: np.ndarray,
                   group: int, w_zero_g: Optional[np.ndarray] = None) -> np.ndarray:
     """ReferenceMidGroupGemm (gemm_ref.cpp:199-240): bf16 bits [M, N].

@@ -63,6 +63,11 @@ def group_stride(group: int) -> int:
     return -(-group // GROUP_ALIGN) * GROUP_ALIGN
 
 
+def group_pad(g: int, K: int, group: int) -> int:
+    """Padded width of group g (npu_ops/kernel/mg_kgeom.h:83-87)."""
+    return -(-group_real(g, K, group) // GROUP_ALIGN) * GROUP_ALIGN
+
+
 def kpad(K: int, group: int) -> int:
     """npu_ops/kernel/mg_kgeom.h:98-102."""
     G = num_groups(K, group)
@@ -249,6 +254,129 @@ def gemm_f64(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_s
     for g in range(G):
         acc += partials[g].astype(np.float64) * (a_s[:, None] * w_scale[:, g].astype(np.float64)[None, :])
     return acc
+
+
+# ------------------------------------------------------------------ mid-group compat path
+def quant_act_midgroup(x_bits: np.ndarray, group: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Per (token, K-group) int8 quant of a bf16 [M, K]: (q int8 [M, K], scale bf16 bits [G, M]).
+
+    fakequant_lab/quant.py:89-105, :135-141 applied to each group's real members
+    (the activation side of npu_ops/kernel/midgroup_quant_a.inc:49-62; a short
+    last group is quantised on what it holds).
+    """
+    M, K = x_bits.shape
+    G = num_groups(K, group)
+    x = bf16_bits_to_f32(x_bits)
+    q = np.empty((M, K), np.int8)
+    sc = np.empty((G, M), np.uint16)
+    for g in range(G):
+        sl = slice(g * group, g * group + group_real(g, K, group))
+        s = group_params_sym(x[:, sl], 8)
+        sc[g] = s
+        q[:, sl] = quantize_with(x[:, sl], s[:, None], None, 8)
+    return q, sc
+
+
+def msd_planes(q: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """int8 codes -> (hi, lo) int4 values with q = 16*hi + lo + 8:
+    hi = floor(q / 16), lo = q - 16*hi - 8 (npu_ops/kernel/midgroup_quant_a.inc:68-73)."""
+    hi = np.floor_divide(q.astype(np.int16), 16)
+    lo = q.astype(np.int16) - 16 * hi - 8
+    return hi.astype(np.int8), lo.astype(np.int8)
+
+
+def act_ksum_neg(q: np.ndarray, group: int) -> np.ndarray:
+    """-sum_{k in g} q per (group, row): int32 [G, M] (midgroup_quant_a.inc:326-337)."""
+    M, K = q.shape
+    G = num_groups(K, group)
+    out = np.empty((G, M), np.int32)
+    for g in range(G):
+        out[g] = -q[:, g * group:g * group + group_real(g, K, group)].astype(np.int64).sum(axis=1)
+    return out
+
+
+def tile_m_for(M: int) -> int:
+    """The reference's row padding unit (npu_ops/host/midgroup_quant_a.cpp:37)."""
+    return 16 if M <= 16 else (64 if M <= 64 else 128)
+
+
+def midgroup_quant_a(x_bits: np.ndarray, group: int = 1024, Mp: Optional[int] = None):
+    """The four tensors of the reference's midgroup_quant_a, as numpy arrays:
+    a_hi, a_lo int8 [Mp, kpad/2] (packed int4 planes in the padded K layout),
+    a_scale bf16 bits [G, Mp], a_ksum int32 [G, Mp]; rows [M, Mp) carry scale
+    tiny, q = 0, ksum 0 (npu_ops/host/midgroup_quant_a.cpp:40-78,
+    npu_ops/kernel/midgroup_quant_a.inc:7-28)."""
+    M, K = x_bits.shape
+    Mp = Mp if Mp is not None else -(-M // tile_m_for(M)) * tile_m_for(M)
+    G = num_groups(K, group)
+    q = np.zeros((Mp, K), np.int8)
+    sc = np.full((G, Mp), BF16_TINY_BITS, np.uint16)
+    qm, scm = quant_act_midgroup(x_bits, group)
+    q[:M] = qm
+    sc[:, :M] = scm
+    hi, lo = msd_planes(pad_groups(q, group))
+    # pad_groups leaves q = 0 in every padding slot, whose planes are hi 0, lo -8
+    return pack_int4(hi), pack_int4(lo), sc, act_ksum_neg(q, group)
+
+
+def quantize_weight_asym(w: np.ndarray, group: int, bits: int = 4):
+    """Asymmetric per-group weight quant of a float [N, K], the reference's export
+    (npu_ops/python/w4a8_ops.py:181-240 with QuantSpec(4, group, sym=False)):
+    (codes int8 [N, K], scale bf16 bits [G, N], zero bf16 bits [G, N], ksum int32
+    [G, N] of the raw codes).  A ragged last group is quantised as its own group."""
+    N, K = w.shape
+    G = num_groups(K, group)
+    codes = np.empty((N, K), np.int8)
+    sc = np.empty((G, N), np.uint16)
+    zr = np.empty((G, N), np.uint16)
+    ks = np.empty((G, N), np.int32)
+    for g in range(G):
+        sl = slice(g * group, g * group + group_real(g, K, group))
+        s, z = group_params_asym(w[:, sl], bits)
+        codes[:, sl] = quantize_with(w[:, sl], s[:, None], z[:, None], bits)
+        sc[g], zr[g] = s, z
+        ks[g] = codes[:, sl].astype(np.int64).sum(axis=1)
+    return codes, sc, zr, ks
+
+
+def group_partials_asym(a_q: np.ndarray, w_codes: np.ndarray, w_zero_bits: Optional[np.ndarray],
+                        group: int) -> np.ndarray:
+    """I[g, m, n] = sum_{k in g} A[m,k] * (W[n,k] - wz[g,n]) as int64, the definition the
+    reference's C++ checks against (int4_cube_lab/host/gemm_ref.cpp:216-227,
+    ragged_layout_test.cpp:128-135); wz is truncated to an integer as there."""
+    M, K = a_q.shape
+    N = w_codes.shape[0]
+    G = num_groups(K, group)
+    out = np.empty((G, M, N), np.int64)
+    for g in range(G):
+        sl = slice(g * group, g * group + group_real(g, K, group))
+        w = w_codes[:, sl].astype(np.int64)
+        if w_zero_bits is not None:
+            w = w - np.trunc(bf16_bits_to_f32(w_zero_bits[g])).astype(np.int64)[:, None]
+        out[g] = a_q[:, sl].astype(np.int64) @ w.T
+    return out
+
+
+def gemm_midgroup_fp32(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_scale_bits: np.ndarray,
+                       w_zero_bits: Optional[np.ndarray], group: int, partials: Optional[np.ndarray] = None,
+                       return_abs: bool = False):
+    """ReferenceMidGroupGemm (int4_cube_lab/host/gemm_ref.cpp:199-240) in its fp32
+    order: for g in order, acc += (float(I_g) * ws[g,n]) * as[g,m], each product and
+    sum rounded to fp32.  a_scale_bits [G, >= M], w_scale/w_zero bits [G, N].
+    With ``return_abs`` also sum_g |term_g| in float64 (for fp32_sum_error_bound)."""
+    M, K = a_q.shape
+    G = num_groups(K, group)
+    if partials is None:
+        partials = group_partials_asym(a_q, w_codes, w_zero_bits, group)
+    acc = np.zeros((M, w_codes.shape[0]), np.float32)
+    mag = np.zeros(acc.shape, np.float64) if return_abs else None
+    for g in range(G):
+        t1 = (partials[g].astype(np.float32) * bf16_bits_to_f32(w_scale_bits[g])[None, :]).astype(np.float32)
+        t2 = (t1 * bf16_bits_to_f32(a_scale_bits[g, :M])[:, None]).astype(np.float32)
+        acc = (acc + t2).astype(np.float32)
+        if return_abs:
+            mag += np.abs(t2.astype(np.float64))
+    return (acc, mag) if return_abs else acc
 
 
 def silu_mul_bf16(g_bits: np.ndarray, u_bits: np.ndarray) -> np.ndarray:

@@ -431,3 +431,108 @@ def test_config4_midgroup_variants(pkg, dev, proj, M, G):
         y, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, G, partials=False)
         y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G, return_abs=True)
         check_output(tensor_bf16_bits(y)[:, cols], y32, mag, ow.num_groups(K, G), f"config4 {proj} M{M} G{G}")
+
+
+# ------------------------------------------------------------------ mid-group compat pair
+def bits_tensor(a: np.ndarray, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(dtype)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 64, 65, 130])
+@pytest.mark.parametrize("K,G", [(5120, 1024), (1057, 1024), (3456, 1024), (27648, 1024), (300, 128)])
+def test_midgroup_quant_a_byte_exact(pkg, dev, M, K, G):
+    """All four tensors of midgroup_quant_a byte-exact, padded rows and slots included."""
+    say(f"midgroup quant_a M={M} K={K} G={G}")
+    xb = pkg.synth.activations(M, K, seed=M * 3 + K)
+    got = torch.ops.npu.midgroup_quant_a(bf16_bits_tensor(xb).to(dev), G)
+    torch.cuda.synchronize()
+    exp = ow.midgroup_quant_a(xb, G)
+    names = ("a_hi", "a_lo", "a_scale", "a_ksum")
+    for name, g, e in zip(names, got, exp):
+        gn = tensor_bf16_bits(g) if g.dtype == torch.bfloat16 else g.cpu().numpy()
+        assert gn.shape == e.shape, f"{name} shape {gn.shape} vs {e.shape}"
+        assert np.array_equal(gn.view(e.dtype) if gn.dtype != e.dtype else gn, e), f"{name} differs"
+
+
+MIDGROUP_CASES = [
+    # (M, N, K, G, asym)
+    (1, 512, 5120, 1024, True),
+    (5, 384, 1057, 1024, True),       # ragged K, single short group + full group
+    (16, 256, 3456, 1024, True),      # a K shard at group 1024
+    (33, 640, 2049, 1024, False),     # symmetric: zero point all 0
+    (64, 1024, 5120, 1024, True),
+    (100, 256, 1057, 1024, True),     # rows padded to 128 by quant_a
+    (300, 384, 5120, 1024, True),
+    (16, 200, 2048, 256, True),       # stride 256 (two tiles per group), N not a multiple of 16
+    (70, 160, 1000, 128, True),       # stride 128, ragged tail of 104
+]
+
+
+def run_midgroup(pkg, dev, M, N, K, G, asym, seed):
+    xb = pkg.synth.activations(M, K, seed=seed)
+    w = np.random.default_rng(seed).standard_normal((N, K)).astype(np.float32) * 0.05
+    codes, sc, zr, ks = ow.quantize_weight_asym(w, G)
+    if not asym:
+        zr = np.zeros_like(zr)
+    a = torch.ops.npu.midgroup_quant_a(bf16_bits_tensor(xb).to(dev), G)
+    args = (torch.from_numpy(ow.pack_grouped(codes, G)).to(dev), bits_tensor(sc, torch.bfloat16).to(dev),
+            torch.from_numpy(ks).to(dev), bits_tensor(zr, torch.bfloat16).to(dev))
+    y, P = torch.ops.npu.midgroup_w4a8_gemm_partials(*a, *args, K, G)
+    torch.cuda.synchronize()
+    return xb, codes, sc, zr, a, args, y, P
+
+
+@pytest.mark.parametrize("M,N,K,G,asym", MIDGROUP_CASES)
+def test_midgroup_gemm_partials_bit_exact_and_output(pkg, dev, M, N, K, G, asym):
+    """int32 I_g = sum A*(W - wz) bit-exact; bf16 output against ReferenceMidGroupGemm's
+    fp32 order (the oracle restates it bit for bit), to the same bars as the main path."""
+    say(f"midgroup gemm M={M} N={N} K={K} G={G} asym={asym}")
+    xb, codes, sc, zr, a, args, y, P = run_midgroup(pkg, dev, M, N, K, G, asym, seed=M + N + K)
+    Mp = a[0].shape[0]
+    q, s = ow.quant_act_midgroup(xb, G)
+    qp = np.zeros((Mp, K), np.int8)
+    qp[:M] = q
+    P_ref = ow.group_partials_asym(qp, codes, zr, G)
+    assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
+    a_scale = tensor_bf16_bits(a[2])
+    y32, mag = ow.gemm_midgroup_fp32(qp, a_scale, codes, sc, zr, G, partials=P_ref, return_abs=True)
+    assert y.shape == (Mp, N)
+    check_output(tensor_bf16_bits(y)[:M], y32[:M], mag[:M], ow.num_groups(K, G), f"midgroup M{M} N{N} K{K}")
+    assert not tensor_bf16_bits(y)[M:].any() or np.all(ow.bf16_bits_to_f32(tensor_bf16_bits(y)[M:]) == 0)
+
+
+@pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
+@pytest.mark.parametrize("M", [1, 16])
+def test_midgroup_qwq_decode_shapes(pkg, dev, proj, M):
+    """The reference's own decode configuration: group 1024 at QwQ-32B shapes."""
+    K, N = pkg.synth.QWQ_SHAPES[proj]
+    say(f"midgroup qwq {proj} M={M}")
+    xb, codes, sc, zr, a, args, y, P = run_midgroup(pkg, dev, M, N, K, 1024, True, seed=M)
+    Mp = a[0].shape[0]
+    q, _ = ow.quant_act_midgroup(xb, 1024)
+    qp = np.zeros((Mp, K), np.int8)
+    qp[:M] = q
+    y32, mag = ow.gemm_midgroup_fp32(qp, tensor_bf16_bits(a[2]), codes, sc, zr, 1024, return_abs=True)
+    check_output(tensor_bf16_bits(y)[:M], y32[:M], mag[:M], ow.num_groups(K, 1024), f"midgroup {proj} M{M}")
+
+
+def test_midgroup_linear_module(pkg, dev):
+    """The reference's MidGroupW4A8LinearMethod.apply semantics: [N, G] checkpoint tensors,
+    quant_a, GEMM, slice to the real rows, bias, reshape."""
+    say("MidGroupW4A8Linear")
+    K, N = 2049, 384
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(K, N, bias=True, dtype=torch.float32)
+    m = pkg.MidGroupW4A8Linear.from_float(lin.to(dev))
+    x = torch.randn(2, 3, K, dtype=torch.bfloat16)
+    y = m(x.to(dev))
+    torch.cuda.synchronize()
+    assert y.shape == (2, 3, N) and y.dtype == torch.bfloat16
+    codes, sc, zr, _ = ow.quantize_weight_asym(lin.weight.detach().cpu().numpy(), 1024)
+    xb = tensor_bf16_bits(x.reshape(-1, K))
+    q, s = ow.quant_act_midgroup(xb, 1024)
+    y32 = ow.gemm_midgroup_fp32(q, s, codes, sc, zr, 1024)
+    y_ref = (torch.from_numpy(ow.round_bf16(y32)).to(torch.bfloat16) + lin.bias.detach().cpu().to(torch.bfloat16)
+             ).float().numpy()
+    got = y.reshape(-1, N).float().cpu().numpy()
+    assert np.max(np.abs(got - y_ref) - 2 * ow.bf16_ulp(y_ref)) <= 0

@@ -68,3 +68,29 @@ def test_cpu_tensors_are_refused(pkg):
     x = torch.zeros((2, 64), dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         torch.ops.npu.w4a8_quant_pertoken(x)
+
+
+def test_quantize_weight_asym_matches_oracle(pkg):
+    """The torch export (the reference's quantize_weight, asymmetric) and the oracle's
+    restatement agree byte for byte, ragged tail and constant rows included."""
+    from oracle import w4a8 as ow
+    w = torch.randn(24, 1057, generator=torch.Generator().manual_seed(4)) * 0.03
+    w[5] = 0.125
+    w_q, ws, wk, wz = pkg.packing.quantize_weight_asym(w, 1024)
+    codes, sc, zr, ks = ow.quantize_weight_asym(w.numpy(), 1024)
+    assert np.array_equal(w_q.numpy(), ow.pack_grouped(codes, 1024))
+    assert np.array_equal(ws.view(torch.int16).numpy().view(np.uint16), sc)
+    assert np.array_equal(wz.view(torch.int16).numpy().view(np.uint16), zr)
+    assert np.array_equal(wk.numpy(), ks)
+
+
+def test_midgroup_fake_kernels_give_shapes(pkg):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty((5, 1057), dtype=torch.bfloat16, device="cuda")
+        a_hi, a_lo, a_s, a_k = torch.ops.npu.midgroup_quant_a(x)
+        assert a_hi.shape == (16, 544) and a_s.shape == (2, 16) and a_k.dtype == torch.int32
+        w_q = torch.empty((256, 544), dtype=torch.int8, device="cuda")
+        gn = torch.empty((2, 256), dtype=torch.bfloat16, device="cuda")
+        y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_s, a_k, w_q, gn, gn.int(), gn, 1057)
+        assert y.shape == (16, 256) and y.dtype == torch.bfloat16

@@ -260,3 +260,138 @@ def test_silu_mul_matches_torch_bf16():
     # a plausible slip -- gate and up swapped -- is caught
     wrong = ow.bf16_bits_to_f32(ow.silu_mul_bf16(u, g)).astype(np.float64)
     assert np.mean(wrong == ref) < 0.5
+
+
+# --------------------------------------------------------------- mid-group compat path
+MID_CASES = [(5120, 1024), (1057, 1024), (3456, 1024), (300, 128), (2049, 512)]
+
+
+def test_midgroup_quant_matches_rational_arithmetic():
+    """Per (token, group) quant == exact rational restatement of quant.py on each
+    group's real members, including a zero group and exact half-way quotients."""
+    rng = np.random.default_rng(3)
+    for K, gk in ((1057, 1024), (300, 128)):
+        x = ow.f32_to_bf16_bits((rng.standard_normal((3, K)) * 2).astype(np.float32))
+        x[1, :gk] = 0                                      # an all-zero group
+        x[2, :256] = tie_rows_bits(1, 256)[0]              # exact .5 quotients
+        q, sc = ow.quant_act_midgroup(x, gk)
+        for m in range(3):
+            for g in range(ow.num_groups(K, gk)):
+                sl = slice(g * gk, g * gk + ow.group_real(g, K, gk))
+                s, qe = exact_quant_row(x[m, sl])
+                assert Fraction(float(ow.bf16_bits_to_f32(sc[g:g + 1, m])[0])) == s
+                assert list(q[m, sl]) == qe
+
+
+def tie_rows_bits(n, K):
+    from conftest import tie_rows
+    return tie_rows(n, K, seed=9)
+
+
+@needs_ref
+@pytest.mark.parametrize("K,gk", MID_CASES)
+def test_midgroup_quant_a_layout_matches_reference(K, gk):
+    """The four compat tensors: planes == the reference's grouped MSD split of the
+    same codes, ksums == its ActKSumNegPerGroup, padded rows hold q = 0 / tiny."""
+    x = ow.f32_to_bf16_bits(np.random.default_rng(K).standard_normal((5, K)).astype(np.float32))
+    q, sc = ow.quant_act_midgroup(x, gk)
+    a_hi, a_lo, a_scale, a_ksum = ow.midgroup_quant_a(x, gk)        # Mp = 16
+    assert a_hi.shape == (16, ow.kpad(K, gk) // 2) and a_scale.shape == (ow.num_groups(K, gk), 16)
+    hi_ref, lo_ref = oref.split_planes_grouped(q, gk)
+    assert np.array_equal(a_hi[:5], hi_ref) and np.array_equal(a_lo[:5], lo_ref)
+    assert np.array_equal(a_ksum[:, :5], oref.act_ksum_neg(q, gk))
+    assert np.array_equal(a_scale[:, :5], sc)
+    assert not a_hi[5:].any() and np.all(a_lo[5:].view(np.uint8) == 0x88)
+    assert np.all(a_scale[:, 5:] == ow.BF16_TINY_BITS) and not a_ksum[:, 5:].any()
+
+
+def test_msd_planes_exhaustive():
+    q = np.arange(-128, 128, dtype=np.int8)
+    hi, lo = ow.msd_planes(q)
+    assert np.array_equal(16 * hi.astype(np.int32) + lo + 8, q.astype(np.int32))
+    assert hi.min() == -8 and hi.max() == 7 and lo.min() == -8 and lo.max() == 7
+
+
+def _exact_asym(xs, bits=4):
+    """quant.py:106-132 for one group in rational arithmetic with fp32/bf16 roundings."""
+    qmax, qmin = 7, -8
+    mx, mn = max(xs), min(xs)
+    rng_ = mx - mn
+    if rng_ == 0:
+        s = round_to_float(round_to_float(abs(mx) / qmax, 24), 8) if mx != 0 else Fraction(0)
+        return (s if s != 0 else Fraction(2) ** -126), Fraction(0)
+    rf = round_to_float(rng_, 24)                       # fp32 subtraction
+    s = round_to_float(round_to_float(rf / (qmax - qmin), 24), 8)
+    s = s if s != 0 else Fraction(2) ** -126
+    z = Fraction(qmin) - round_half_even(round_to_float(mn / s, 24) if mn >= 0 else -round_to_float(-mn / s, 24))
+    return s, round_to_float(z, 8) if z > 0 else (-round_to_float(-z, 8) if z < 0 else Fraction(0))
+
+
+def test_group_params_asym_matches_rational_arithmetic():
+    rng = np.random.default_rng(11)
+    w = ow.round_bf16((rng.standard_normal((40, 64)) * 0.05 + rng.uniform(-0.02, 0.02, (40, 1))).astype(np.float32))
+    w[3] = np.float32(0.25)                              # constant group: scale |v|/7, zero 0
+    w[4] = 0.0                                           # all-zero group
+    s_bits, z_bits = ow.group_params_asym(w, 4)
+    for r in range(w.shape[0]):
+        s, z = _exact_asym([Fraction(float(v)) for v in w[r]])
+        assert Fraction(float(ow.bf16_bits_to_f32(s_bits[r:r + 1])[0])) == s, r
+        assert Fraction(float(ow.bf16_bits_to_f32(z_bits[r:r + 1])[0])) == z, r
+
+
+@needs_ref
+def test_quantize_weight_asym_ksum_matches_reference():
+    w = np.random.default_rng(2).standard_normal((48, 1057)).astype(np.float32)
+    codes, sc, zr, ks = ow.quantize_weight_asym(w, 1024)
+    assert codes.min() >= -8 and codes.max() <= 7 and sc.shape == (2, 48)
+    assert np.array_equal(ks, oref.weight_ksum(codes, 1024))
+
+
+@needs_ref
+@pytest.mark.parametrize("K,gk", MID_CASES)
+def test_midgroup_partials_identity_and_definition(K, gk):
+    """I = sum A*(W - wz) by brute force, and the rank-1 identity the GPU kernel uses,
+    16*S_hi + S_lo + 8*w_ksum + wz*a_ksum (planes and ksums from the reference's C++)."""
+    rng = np.random.default_rng(K + gk)
+    M, N = 3, 20
+    a = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+    w = rng.integers(-8, 8, size=(N, K)).astype(np.int8)
+    wz = ow.f32_to_bf16_bits(rng.integers(-8, 8, size=(ow.num_groups(K, gk), N)).astype(np.float32))
+    I = ow.group_partials_asym(a, w, wz, gk)
+    hi_p, lo_p = oref.split_planes_grouped(a, gk)
+    hi = ow.unpack_int4(hi_p).astype(np.int64)
+    lo = ow.unpack_int4(lo_p).astype(np.int64)
+    wp = ow.unpack_int4(ow.pack_grouped(w, gk)).astype(np.int64)
+    aks, wks = oref.act_ksum_neg(a, gk), oref.weight_ksum(w, gk)
+    st = ow.group_stride(gk)
+    for g in range(ow.num_groups(K, gk)):
+        sl = slice(g * st, g * st + ow.group_pad(g, K, gk))
+        s_hi, s_lo = hi[:, sl] @ wp[:, sl].T, lo[:, sl] @ wp[:, sl].T
+        zi = ow.bf16_bits_to_f32(wz[g]).astype(np.int64)
+        ident = 16 * s_hi + s_lo + 8 * wks[g][None, :] + zi[None, :] * aks[g][:, None]
+        assert np.array_equal(ident, I[g])
+        brute = np.array([[sum(int(a[m, k]) * (int(w[n, k]) - int(zi[n]))
+                               for k in range(g * gk, g * gk + ow.group_real(g, K, gk)))
+                           for n in range(2)] for m in range(2)])
+        assert np.array_equal(brute, I[g][:2, :2])
+
+
+@needs_ref
+@pytest.mark.parametrize("K,gk", MID_CASES)
+@pytest.mark.parametrize("asym", [True, False])
+def test_midgroup_gemm_matches_reference_cpp_bitwise(K, gk, asym):
+    """gemm_midgroup_fp32 restates ReferenceMidGroupGemm's fp32 order exactly: the
+    bf16 outputs are identical; scales taken from the wrong groups (a plausible
+    indexing slip) are caught."""
+    rng = np.random.default_rng(K * 3 + asym)
+    M, N = 7, 40
+    xb = ow.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    q, sc = ow.quant_act_midgroup(xb, gk)
+    codes, ws, wz, _ = ow.quantize_weight_asym(rng.standard_normal((N, K)).astype(np.float32), gk)
+    wz = wz if asym else None
+    ours = ow.f32_to_bf16_bits(ow.gemm_midgroup_fp32(q, sc, codes, ws, wz, gk))
+    ref = oref.midgroup_gemm(q, sc, codes, ws, gk, wz)
+    assert np.array_equal(ours, ref)
+    if ow.num_groups(K, gk) > 1:
+        wrong = ow.f32_to_bf16_bits(ow.gemm_midgroup_fp32(q, sc, codes, ws[::-1].copy(), wz, gk))
+        assert not np.array_equal(wrong, ref)

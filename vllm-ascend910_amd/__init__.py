@@ -11,6 +11,7 @@ The directory name is not a Python identifier, so the package is imported as
 """
 from . import geometry, packing, synth  # noqa: F401
 from . import ops  # noqa: F401
-from .linear import W4A8Linear, linear, linear_swiglu  # noqa: F401
+from .linear import MidGroupW4A8Linear, W4A8Linear, linear, linear_swiglu, midgroup_linear  # noqa: F401
 
-__all__ = ["W4A8Linear", "linear", "linear_swiglu", "geometry", "packing", "ops", "synth"]
+__all__ = ["W4A8Linear", "MidGroupW4A8Linear", "linear", "linear_swiglu", "midgroup_linear", "geometry",
+           "packing", "ops", "synth"]

@@ -32,6 +32,9 @@ SIGNATURES = {
     "w4a8_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "w4a8_gemm": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
     "w4a8_gemm_swiglu": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
+    "w4a8_midgroup_quant_a": (_I, [_VP, _I64, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP]),
+    "w4a8_midgroup_gemm": (_I, [_VP, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
+                                _VP]),
     "w4a8_gemm_debug_partials": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _VP, _I64, _I64, _I64, _I64,
                                       _VP, _I64, _VP]),
 }

@@ -194,4 +194,64 @@ int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale, 
                     workspace, workspace_bytes, stream);
 }
 
+int w4a8_midgroup_quant_a(const void* x, int64_t ldx, void* a_hi, void* a_lo, void* a_scale, void* a_ksum,
+                          int64_t M, int64_t Mp, int64_t K, int64_t group, void* stream) {
+    if (M < 0 || Mp < M || K <= 0 || group <= 0 || Mp >= (1ll << 31) || K >= (1ll << 30) || group >= (1ll << 30))
+        return fail(W4A8_ERR_SHAPE, "bad shape: M=%lld Mp=%lld K=%lld (need 0 <= M <= Mp, K > 0)", M, Mp, K);
+    if (Mp == 0) return W4A8_OK;
+    if (!a_hi || !a_lo || !a_scale || !a_ksum || (M > 0 && !x)) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (M > 0 && ldx < K) return fail(W4A8_ERR_SHAPE, "ldx=%lld must be >= K=%lld", ldx, K);
+    if (geom::num_groups(K, group) >= 65536)
+        return fail(W4A8_ERR_UNSUPPORTED, "K=%lld group=%lld: more than 65535 groups", K, group);
+    if ((M > 0 && !aligned(x, 2)) || !aligned(a_scale, 2) || !aligned(a_ksum, 4) || !aligned(a_hi, 4) ||
+        !aligned(a_lo, 4))
+        return fail(W4A8_ERR_ALIGN, "x/a_scale 2-byte, a_ksum/a_hi/a_lo 4-byte aligned");
+    return hip_status(launch_quant_midgroup(static_cast<const uint16_t*>(x), ldx, static_cast<uint8_t*>(a_hi),
+                                            static_cast<uint8_t*>(a_lo), static_cast<uint16_t*>(a_scale),
+                                            static_cast<int32_t*>(a_ksum), M, Mp, K, group,
+                                            static_cast<hipStream_t>(stream)),
+                      "w4a8_midgroup_quant_a launch");
+}
+
+int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
+                       int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y, int64_t ldy,
+                       void* partials, int64_t N, int64_t K, int64_t group, void* stream) {
+    if (int rc = check_problem(Ma, N, K, group)) return rc;
+    if (geom::group_stride(group) % 128 != 0)
+        return fail(W4A8_ERR_UNSUPPORTED, "group=%lld: the mid-group path needs ceil_to(group, 64) %% 128 == 0",
+                    group);
+    if (Ma == 0) return W4A8_OK;
+    if (!a_hi || !a_lo || !a_scale || !a_ksum || !w_q || !w_scale || !y)
+        return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (ld_as < Ma || ldy < N) return fail(W4A8_ERR_SHAPE, "ld_as=%lld must be >= rows and ldy=%lld >= N", ld_as, ldy);
+    if (!aligned(a_hi, 16) || !aligned(a_lo, 16) || !aligned(w_q, 16) || !aligned(a_scale, 2) ||
+        !aligned(a_ksum, 4) || !aligned(w_scale, 2) || (w_zero && !aligned(w_zero, 2)) || !aligned(y, 2) ||
+        (partials && !aligned(partials, 4)))
+        return fail(W4A8_ERR_ALIGN, "planes and w_q 16-byte aligned; scales 2-, ksum and partials 4-byte aligned");
+    const int64_t kb = geom::kpad(K, group) / 2;
+    if ((Ma + 16) * kb >= (1ll << 31) || (N + 16) * kb >= (1ll << 31))
+        return fail(W4A8_ERR_UNSUPPORTED, "operands too large for 32-bit offsets (%lld rows, N=%lld, %lld B/row)", Ma,
+                    N, kb);
+    if (midgroup_lds_bytes(Ma, K, group) > 64 * 1024)
+        return fail(W4A8_ERR_UNSUPPORTED, "K=%lld group=%lld: too many groups for the staged scales (%lld B LDS)", K,
+                    group, midgroup_lds_bytes(Ma, K, group));
+    MidgroupArgs a{};
+    a.a_hi = a_hi;
+    a.a_lo = a_lo;
+    a.a_scale = a_scale;
+    a.a_ksum = a_ksum;
+    a.Ma = Ma;
+    a.ld_as = ld_as;
+    a.w_q = w_q;
+    a.w_scale = w_scale;
+    a.w_zero = w_zero;
+    a.y = y;
+    a.ldy = ldy;
+    a.partials = partials;
+    a.N = N;
+    a.K = K;
+    a.group = group;
+    return hip_status(launch_gemm_midgroup(a, static_cast<hipStream_t>(stream)), "w4a8_midgroup_gemm launch");
+}
+
 }  // extern "C"

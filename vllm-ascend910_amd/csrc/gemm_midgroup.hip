@@ -1,0 +1,309 @@
+// Mid-group W4A8 GEMM on the reference's compat tensors (gfx950).
+//
+// Computes the reference's `midgroup_w4a8_gemm` (host
+// npu_ops/host/midgroup_w4a8_gemm.cpp:45-140, kernel
+// npu_ops/kernel/midgroup_w4a8_gemm.inc; CPU definition
+// int4_cube_lab/host/gemm_ref.cpp:199-240, ReferenceMidGroupGemm):
+//   I_g[m,n] = sum_{k in g} A[m,k] * (W[n,k] - wz[g,n])          (int32, exact)
+//   y[m,n]   = bf16( sum_g (float(I_g) * ws[g,n]) * as[g,m] )     (fp32, group order)
+// where A = 16*hi + lo + 8 comes from the MSD planes of `midgroup_quant_a` and
+// W, wz, ws, as are the reference's tensors as stored -- nothing is repacked.
+//
+// Operand loading.  The contraction is invariant under any permutation of K
+// applied to both operands, which lets every lane read contiguous bytes of the
+// row-major packed tensors: in a 128-K tile, lane l (column or row l % 16,
+// quad q = l / 16) takes K [32q, 32q + 32) -- 16 bytes of w_q, a_hi and a_lo
+// each -- as its chunk of slab 0 (first 16 codes) and slab 1 (next 16).  Inside a
+// chunk both operands are split into even and odd codes the same way: the
+// weight's nibbles move into the high half of each byte (16*W, as in the
+// per-token kernels) and each activation byte is rebuilt from its two nibbles
+// ((hi << 4) | (lo ^ 8)), so v_mfma_i32_16x16x64_i8 accumulates 16 * sum A*W.
+// The zero point enters through the rank-1 identity
+//   sum A*(W - wz) = sum A*W + wz * a_ksum     (a_ksum = -sum A, as stored)
+// whose int32 result is exact, then the fold follows the reference's fp32
+// order: (float(I) * ws) * as, added to the accumulator group by group.
+//
+// Work split as in the decode kernel: a workgroup owns CPW column blocks of 16
+// and a block of 16*MT rows (grid.y walks row blocks), its KW waves split K at
+// group boundaries and are reduced through LDS in a fixed order.  The
+// activation scales and ksums of the workgroup's rows, and the weight scales
+// and zero points of its columns, are staged in LDS once.  All global reads are
+// raw buffer loads; rows and columns past the tensors, and the K tail past
+// kpad, read as zero.
+#include <algorithm>
+
+#include "common.h"
+#include "kgeom.h"
+#include "launch.h"
+
+namespace w4a8 {
+namespace {
+
+constexpr uint32_t kOOBm = 0x80000000u;
+constexpr size_t kMidLdsLimit = 64 * 1024;
+
+struct MidParams {
+    const uint8_t* a_hi;
+    const uint8_t* a_lo;
+    const uint16_t* a_scale;   // bf16 [G, ld_as]
+    const int32_t* a_ksum;     // int32 [G, ld_as]
+    const uint8_t* w_q;        // [N, kpad/2]
+    const uint16_t* w_scale;   // bf16 [G, N]
+    const uint16_t* w_zero;    // bf16 [G, N] or null
+    uint16_t* Y;
+    int32_t* P;                // optional [G, Ma, N]
+    int64_t ldy;
+    int Ma, ld_as, N, K;
+    int kb;                    // packed row pitch (kpad / 2 bytes)
+    int kpad, KT, NG, NB;
+    int tpg;                   // 128-K tiles per group stride
+    uint32_t a_bytes, w_bytes;
+};
+
+__device__ __forceinline__ int act_even(uint32_t h, uint32_t l) {
+    return static_cast<int>(((h << 4) & 0xf0f0f0f0u) | ((l ^ 0x08080808u) & 0x0f0f0f0fu));
+}
+__device__ __forceinline__ int act_odd(uint32_t h, uint32_t l) {
+    return static_cast<int>((h & 0xf0f0f0f0u) | (((l >> 4) ^ 0x08080808u) & 0x0f0f0f0fu));
+}
+
+template <int MT, int CPW, int KWMAX, int D, bool ASYM, bool DUMP>
+__global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidParams p) {
+    constexpr int R = 16 * MT;
+    constexpr int C = 16 * CPW;
+    extern __shared__ float smem[];
+    // [NG][R] activation scales (fp32), [NG][R] ksums, [NG][C] weight scales,
+    // [NG][C] zero points, then the K-split reduction buffer [kw][R][C].
+    float* s_as = smem;
+    int* s_ak = reinterpret_cast<int*>(s_as + p.NG * R);
+    float* s_ws = reinterpret_cast<float*>(s_ak + p.NG * R);
+    float* s_wz = s_ws + p.NG * C;
+    float* red = s_wz + p.NG * C;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kw = blockDim.x >> 6;
+    const int nb0 = blockIdx.x * CPW;
+    const int m0 = blockIdx.y * R;
+    const int q = lane >> 4;
+    const int rowq = 4 * q;
+    const int colq = lane & 15;
+
+    for (int e = threadIdx.x; e < p.NG * R; e += blockDim.x) {
+        const int g = e / R, r = e - g * R;
+        const int row = m0 + r;
+        const bool ok = row < p.Ma;
+        s_as[e] = ok ? bf16_bits_to_f32(p.a_scale[static_cast<int64_t>(g) * p.ld_as + row]) : 0.0f;
+        s_ak[e] = ok ? p.a_ksum[static_cast<int64_t>(g) * p.ld_as + row] : 0;
+    }
+    for (int e = threadIdx.x; e < p.NG * C; e += blockDim.x) {
+        const int g = e / C, cc = e - g * C;
+        const int col = nb0 * 16 + cc;
+        const bool ok = col < p.N;
+        s_ws[e] = ok ? bf16_bits_to_f32(p.w_scale[static_cast<int64_t>(g) * p.N + col]) : 0.0f;
+        s_wz[e] = (ASYM && ok) ? bf16_bits_to_f32(p.w_zero[static_cast<int64_t>(g) * p.N + col]) : 0.0f;
+    }
+
+    // This wave's tile range, in whole groups.
+    const int ua = (wave * p.NG) / kw;
+    const int ub = ((wave + 1) * p.NG) / kw;
+    const int ta = ua * p.tpg;
+    const int tb = min(p.KT, ub * p.tpg);
+
+    uint32_t wo[CPW], ao[MT];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int col = (nb0 + c) * 16 + colq;
+        wo[c] = col < p.N ? static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 16u * q : kOOBm;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int row = m0 + mt * 16 + colq;
+        ao[mt] = row < p.Ma ? static_cast<uint32_t>(row) * static_cast<uint32_t>(p.kb) + 16u * q : kOOBm;
+    }
+
+    uint4 wb[D][CPW];
+    uint4 hb[D][MT], lb[D][MT];
+    auto load_slot = [&](int s, int t) {
+        // tiles past the wave's range read zero weights; in a last tile that
+        // is half padding, the upper quads read zero weights
+        const uint32_t base = static_cast<uint32_t>(min(t, p.KT - 1)) * 64u;
+        const bool half = q >= 2 && (p.kpad - t * 128) < 128;
+        const auto rw = make_rsrc_at(p.w_q, base, t < tb ? p.w_bytes : 0u);
+        const auto rh = make_rsrc_at(p.a_hi, base, p.a_bytes);
+        const auto rl = make_rsrc_at(p.a_lo, base, p.a_bytes);
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, half ? kOOBm : wo[c]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            hb[s][mt] = buf_load16(rh, ao[mt]);
+            lb[s][mt] = buf_load16(rl, ao[mt]);
+        }
+    };
+
+    float acc[MT][CPW][4];
+    v4i P[MT][CPW];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            P[mt][c] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mt][c][i] = 0.0f;
+        }
+    __syncthreads();   // LDS scales staged
+
+    auto fold = [&](int g, bool own) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const float ws = s_ws[g * C + c * 16 + colq];
+            const int wz = ASYM ? static_cast<int>(s_wz[g * C + c * 16 + colq]) : 0;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = mt * 16 + rowq + i;
+                    const int I = (P[mt][c][i] >> 4) + (ASYM ? wz * s_ak[g * R + r] : 0);
+                    if constexpr (DUMP) {
+                        const int row = m0 + r, col = (nb0 + c) * 16 + colq;
+                        if (own && row < p.Ma && col < p.N && g < p.NG)
+                            p.P[(static_cast<int64_t>(g) * p.Ma + row) * p.N + col] = I;
+                    }
+                    const float t1 = __fmul_rn(static_cast<float>(I), ws);
+                    acc[mt][c][i] = __fadd_rn(acc[mt][c][i], __fmul_rn(t1, s_as[g * R + r]));
+                }
+                P[mt][c] = v4i{0, 0, 0, 0};
+            }
+        }
+    };
+
+    if (tb > ta) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) load_slot(s, ta + s);
+        for (int t0 = ta; t0 < tb; t0 += D) {
+#pragma unroll
+            for (int s = 0; s < D; ++s) {
+                const int t = t0 + s;
+                if (t >= tb) break;
+                v4i bw[CPW][2];
+#pragma unroll
+                for (int c = 0; c < CPW; ++c) {
+                    const uint4 w = wb[s][c];
+                    bw[c][0] = v4i{unpack_lo4(w.x), unpack_hi4(w.x), unpack_lo4(w.y), unpack_hi4(w.y)};
+                    bw[c][1] = v4i{unpack_lo4(w.z), unpack_hi4(w.z), unpack_lo4(w.w), unpack_hi4(w.w)};
+                }
+                v4i av[MT][2];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const uint4 h = hb[s][mt], l = lb[s][mt];
+                    av[mt][0] = v4i{act_even(h.x, l.x), act_odd(h.x, l.x), act_even(h.y, l.y), act_odd(h.y, l.y)};
+                    av[mt][1] = v4i{act_even(h.z, l.z), act_odd(h.z, l.z), act_even(h.w, l.w), act_odd(h.w, l.w)};
+                }
+                load_slot(s, t + D);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(av[mt][h], bw[c][h], P[mt][c]);
+                if ((t + 1) % p.tpg == 0 || t == p.KT - 1) fold(t / p.tpg, true);
+            }
+        }
+    }
+
+    // Fixed-order reduction of the kw wave partials.
+    if (kw > 1) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int c = 0; c < CPW; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave * R * C + (mt * 16 + rowq + i) * C + c * 16 + colq] = acc[mt][c][i];
+        __syncthreads();
+        for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
+            const int r = e / C;
+            const int row = m0 + r;
+            const int col = nb0 * 16 + (e - r * C);
+            if (row >= p.Ma || col >= p.N) continue;
+            float sum = red[e];
+            for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
+            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum));
+        }
+    } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int c = 0; c < CPW; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = m0 + mt * 16 + rowq + i, col = (nb0 + c) * 16 + colq;
+                    if (row < p.Ma && col < p.N)
+                        p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][c][i]));
+                }
+    }
+}
+
+constexpr int kwmax_mid(int mt) { return mt == 1 ? 12 : 8; }
+
+template <int MT, bool ASYM, bool DUMP>
+hipError_t launch_mid(const MidParams& p, int kw, hipStream_t stream) {
+    constexpr int CPW = 2, D = 4, KWM = kwmax_mid(MT);
+    // dynamic LDS stays within the 64 KiB a launch gets without a function
+    // attribute: the staged scales, then as many reduction slices as fit
+    const size_t staged = static_cast<size_t>(p.NG) * (2 * 16 * MT + 2 * 16 * CPW) * sizeof(float);
+    const size_t slice = static_cast<size_t>(16 * MT) * 16 * CPW * sizeof(float);
+    if (staged + slice > kMidLdsLimit) return hipErrorInvalidValue;
+    const int wfit = static_cast<int>((kMidLdsLimit - staged) / slice);
+    const int w = std::max(1, std::min({kw, KWM, p.NG, wfit}));
+    const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW), static_cast<unsigned>((p.Ma + 16 * MT - 1) / (16 * MT)));
+    const size_t lds = staged + static_cast<size_t>(w) * slice;
+    gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP><<<grid, dim3(64 * w), lds, stream>>>(p);
+    return hipGetLastError();
+}
+
+template <bool ASYM, bool DUMP>
+hipError_t launch_mt(const MidParams& p, int kw, hipStream_t stream) {
+    return p.Ma <= 16 ? launch_mid<1, ASYM, DUMP>(p, kw, stream) : launch_mid<4, ASYM, DUMP>(p, kw, stream);
+}
+
+}  // namespace
+
+int64_t midgroup_lds_bytes(int64_t Ma, int64_t K, int64_t group) {
+    const int64_t mt = Ma <= 16 ? 1 : 4;
+    const int64_t ng = geom::num_groups(K, group);
+    return (ng * (2 * 16 * mt + 2 * 32) + 16 * mt * 32) * 4;
+}
+
+hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream) {
+    MidParams p{};
+    p.a_hi = static_cast<const uint8_t*>(a.a_hi);
+    p.a_lo = static_cast<const uint8_t*>(a.a_lo);
+    p.a_scale = static_cast<const uint16_t*>(a.a_scale);
+    p.a_ksum = static_cast<const int32_t*>(a.a_ksum);
+    p.w_q = static_cast<const uint8_t*>(a.w_q);
+    p.w_scale = static_cast<const uint16_t*>(a.w_scale);
+    p.w_zero = static_cast<const uint16_t*>(a.w_zero);
+    p.Y = static_cast<uint16_t*>(a.y);
+    p.P = static_cast<int32_t*>(a.partials);
+    p.ldy = a.ldy;
+    p.Ma = static_cast<int>(a.Ma);
+    p.ld_as = static_cast<int>(a.ld_as);
+    p.N = static_cast<int>(a.N);
+    p.K = static_cast<int>(a.K);
+    p.kpad = static_cast<int>(geom::kpad(a.K, a.group));
+    p.kb = p.kpad / 2;
+    p.KT = static_cast<int>(geom::ceil_div(p.kpad, 128));
+    p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
+    p.NB = static_cast<int>(geom::col_blocks(a.N));
+    p.tpg = static_cast<int>(geom::group_stride(a.group) / 128);
+    p.a_bytes = static_cast<uint32_t>(a.Ma * static_cast<int64_t>(p.kb));
+    p.w_bytes = static_cast<uint32_t>(a.N * static_cast<int64_t>(p.kb));
+    // waves per workgroup: about two groups each, more for few column blocks
+    const int64_t wgs = (p.NB + 1) / 2;
+    const int kw = wgs >= 512 ? 1 : std::max(1, std::min(p.NG, static_cast<int>((p.NG + 1) / 2)));
+    const bool asym = a.w_zero != nullptr, dump = a.partials != nullptr;
+    if (asym) return dump ? launch_mt<true, true>(p, kw, stream) : launch_mt<true, false>(p, kw, stream);
+    return dump ? launch_mt<false, true>(p, kw, stream) : launch_mt<false, false>(p, kw, stream);
+}
+
+}  // namespace w4a8

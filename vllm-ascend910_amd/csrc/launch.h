@@ -56,6 +56,30 @@ hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hi
 int64_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
 
+// Mid-group compat path (the reference's midgroup_quant_a / midgroup_w4a8_gemm).
+hipError_t launch_quant_midgroup(const uint16_t* x, int64_t ldx, uint8_t* a_hi, uint8_t* a_lo,
+                                 uint16_t* a_scale, int32_t* a_ksum, int64_t M, int64_t Mp, int64_t K,
+                                 int64_t group, hipStream_t stream);
+
+struct MidgroupArgs {
+    const void* a_hi;
+    const void* a_lo;
+    const void* a_scale;   // bf16 [G, ld_as]
+    const void* a_ksum;    // int32 [G, ld_as]
+    int64_t Ma, ld_as;
+    const void* w_q;       // [N, kpad/2]
+    const void* w_scale;   // bf16 [G, N]
+    const void* w_zero;    // bf16 [G, N] or null (symmetric)
+    void* y;
+    int64_t ldy;
+    void* partials;        // optional int32 [G, Ma, N]
+    int64_t N, K, group;
+};
+// Bytes of LDS the staged scales need for one workgroup (the launch refuses
+// shapes above 64 KiB).
+int64_t midgroup_lds_bytes(int64_t Ma, int64_t K, int64_t group);
+hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace w4a8

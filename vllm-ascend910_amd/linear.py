@@ -103,3 +103,77 @@ class W4A8Linear(nn.Module):
         if self.act == "swiglu":
             return linear_swiglu(x, self.w_tiles, self.s_tiles, self.out_features, self.group)
         return linear(x, self.w_tiles, self.s_tiles, self.out_features, self.group, self.bias)
+
+
+# ---------------------------------------------------------------- mid-group compat pair
+def midgroup_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wk: torch.Tensor, wz: torch.Tensor,
+                    group: int = 1024) -> torch.Tensor:
+    """y = x @ W.T with the reference's mid-group W4A8 tensors; x is bf16 [..., K].
+
+    The reference's ``w4a8_ops.linear`` (npu_ops/python/w4a8_ops.py:243-252): quant_a pads the
+    rows to TILE_M, so y has >= x's rows and is sliced before reshaping.
+    """
+    lead, K = x.shape[:-1], x.shape[-1]
+    x2 = x.reshape(-1, K).to(torch.bfloat16).contiguous()
+    a_hi, a_lo, a_scale, a_ksum = torch.ops.npu.midgroup_quant_a(x2, group)
+    y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, wq, ws, wk, wz, K, group)
+    return y[:x2.shape[0]].reshape(*lead, y.shape[-1])
+
+
+class MidGroupW4A8Linear(nn.Module):
+    """The reference's ``MidGroupW4A8LinearMethod`` as a module (npu_ops/python/midgroup_quant.py:102-178).
+
+    Parameters in the checkpoint layout the reference exports (``weight_packed [N, kpad/2]`` int8,
+    ``weight_scale``/``weight_zero`` ``[N, G]`` bf16, ``weight_ksum [N, G]`` int32, output_dim 0 so
+    fused loaders concatenate along N); ``process_weights_after_loading`` transposes the three
+    per-group tensors to ``[G, N]`` (midgroup_quant.py:148-161); ``forward`` is ``apply``
+    (:163-178): quant_a, GEMM, slice to the real rows, bias, reshape.
+    """
+
+    def __init__(self, in_features: int, out_features: int, group: int = 1024, bias: bool = False, device=None):
+        super().__init__()
+        self.in_features, self.out_features, self.group = in_features, out_features, group
+        K, N = in_features, out_features
+        G = geo.num_groups(K, group)
+        self.register_buffer("weight_packed", torch.zeros((N, geo.kpad(K, group) // 2), dtype=torch.int8,
+                                                          device=device))
+        self.register_buffer("weight_scale", torch.zeros((N, G), dtype=torch.bfloat16, device=device))
+        self.register_buffer("weight_zero", torch.zeros((N, G), dtype=torch.bfloat16, device=device))
+        self.register_buffer("weight_ksum", torch.zeros((N, G), dtype=torch.int32, device=device))
+        self.bias = nn.Parameter(torch.zeros(N, dtype=torch.bfloat16, device=device),
+                                 requires_grad=False) if bias else None
+        self._gn = None
+
+    @classmethod
+    def from_float(cls, lin: nn.Linear, group: int = 1024) -> "MidGroupW4A8Linear":
+        """Export an nn.Linear the way the reference's quantize_weight does, then load it."""
+        from .packing import quantize_weight_asym
+        N, K = lin.weight.shape
+        m = cls(K, N, group, lin.bias is not None, device=lin.weight.device)
+        w_q, ws, wk, wz = quantize_weight_asym(lin.weight.data, group)
+        m.weight_packed.copy_(w_q)
+        m.weight_scale.copy_(ws.T)
+        m.weight_zero.copy_(wz.T)
+        m.weight_ksum.copy_(wk.T)
+        if lin.bias is not None:
+            m.bias.data.copy_(lin.bias.data.to(torch.bfloat16))
+        m.process_weights_after_loading()
+        return m
+
+    def process_weights_after_loading(self) -> None:
+        self._gn = tuple(getattr(self, n).t().contiguous() for n in ("weight_scale", "weight_ksum", "weight_zero"))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._gn is None:
+            raise RuntimeError("MidGroupW4A8Linear: call process_weights_after_loading() after loading weights")
+        ws, wk, wz = self._gn
+        lead, k = x.shape[:-1], x.shape[-1]
+        x2 = x.reshape(-1, k).to(torch.bfloat16).contiguous()
+        rows = x2.shape[0]
+        a_hi, a_lo, a_scale, a_ksum = torch.ops.npu.midgroup_quant_a(x2, self.group)
+        y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, self.weight_packed, ws, wk, wz, k,
+                                             self.group)
+        y = y[:rows]
+        if self.bias is not None:
+            y = y + self.bias
+        return y.reshape(*lead, self.out_features)

@@ -11,6 +11,14 @@ group-size-parameterised ops of this build:
     torch.ops.npu.w4a8_gemm_partials(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> (y, partials)
     torch.ops.npu.w4a8_gemm_swiglu(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> y [M, N/2]
 
+and, with the reference's own names and schemas (group appended with the
+reference's fixed value as default), its mid-group compat pair:
+
+    torch.ops.npu.midgroup_quant_a(x, group=1024) -> [a_hi, a_lo, a_scale, a_ksum]
+    torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero,
+                                     K, group=1024) -> y
+    torch.ops.npu.midgroup_w4a8_gemm_partials(...) -> (y, partials)   (parity hook)
+
 Only the CUDA (= HIP on ROCm) dispatch key and fake (meta) kernels are
 registered: CPU tensors raise, there is no fallback path.  Each impl checks
 dtypes and shapes like the reference's host impls (TORCH_CHECK ->
@@ -36,6 +44,11 @@ _LIB.define("w4a8_gemm_partials(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tens
             "int N, int K, int group) -> (Tensor, Tensor)")
 _LIB.define("w4a8_gemm_swiglu(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
             "int N, int K, int group) -> Tensor")
+_LIB.define("midgroup_quant_a(Tensor x, int group=1024) -> Tensor[]")
+_LIB.define("midgroup_w4a8_gemm(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
+            "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> Tensor")
+_LIB.define("midgroup_w4a8_gemm_partials(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
+            "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> (Tensor, Tensor)")
 
 _SCALE_DT = {torch.float16: _abi.W4A8_DT_F16, torch.bfloat16: _abi.W4A8_DT_BF16}
 
@@ -210,3 +223,112 @@ def _gemm_partials_fake(a_q, a_scale, w_tiles, s_tiles, N, K, group):
     M = a_q.shape[0]
     return (a_q.new_empty((M, N), dtype=torch.bfloat16),
             a_q.new_empty((geo.num_groups(K, group), M, N), dtype=torch.int32))
+
+
+# ---------------------------------------------------------------- mid-group compat pair
+def tile_m_for(M: int) -> int:
+    """Row padding unit of the reference's compat pair (npu_ops/host/midgroup_quant_a.cpp:37)."""
+    return 16 if M <= 16 else (64 if M <= 64 else 128)
+
+
+def _padded_rows(M: int) -> int:
+    t = tile_m_for(M)
+    return -(-M // t) * t
+
+
+@torch.library.impl(_LIB, "midgroup_quant_a", "CUDA")
+def _midgroup_quant_a_cuda(x: torch.Tensor, group: int = 1024):
+    """The reference's run_midgroup_quant_a (npu_ops/host/midgroup_quant_a.cpp:40-78):
+    a_hi/a_lo int8 [Mp, kpad/2], a_scale bf16 [G, Mp], a_ksum int32 [G, Mp]."""
+    _require(x.dim() == 2, "midgroup_quant_a: x must be [M, K]")
+    _require(x.dtype == torch.bfloat16, "midgroup_quant_a: x must be bfloat16")
+    _require(group > 0, "midgroup_quant_a: group must be > 0")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    G, kb = geo.num_groups(K, group), geo.kpad(K, group) // 2
+    Mp = _padded_rows(M) if M else 0
+    dev = x.device
+    a_hi = torch.empty((Mp, kb), dtype=torch.int8, device=dev)
+    a_lo = torch.empty((Mp, kb), dtype=torch.int8, device=dev)
+    a_scale = torch.empty((G, Mp), dtype=torch.bfloat16, device=dev)
+    a_ksum = torch.empty((G, Mp), dtype=torch.int32, device=dev)
+    if Mp:
+        _abi.check(_abi.lib().w4a8_midgroup_quant_a(x.data_ptr(), x.stride(0), a_hi.data_ptr(), a_lo.data_ptr(),
+                                                    a_scale.data_ptr(), a_ksum.data_ptr(), M, Mp, K, group,
+                                                    _stream(dev)), "midgroup_quant_a")
+    return [a_hi, a_lo, a_scale, a_ksum]
+
+
+@torch.library.register_fake("npu::midgroup_quant_a")
+def _midgroup_quant_a_fake(x, group=1024):
+    M, K = x.shape
+    G, kb = geo.num_groups(K, group), geo.kpad(K, group) // 2
+    Mp = _padded_rows(M) if M else 0
+    return [x.new_empty((Mp, kb), dtype=torch.int8), x.new_empty((Mp, kb), dtype=torch.int8),
+            x.new_empty((G, Mp), dtype=torch.bfloat16), x.new_empty((G, Mp), dtype=torch.int32)]
+
+
+def _check_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group):
+    # the reference's checks (npu_ops/host/midgroup_w4a8_gemm.cpp:51-85); N % 128 is not required here
+    _require(a_hi.dim() == 2 and a_lo.dim() == 2 and w_q.dim() == 2,
+             "midgroup_w4a8_gemm: a_hi/a_lo [M,K/2] and w_q [N,K/2] must be 2-D")
+    _require(a_hi.dtype == torch.int8 and a_lo.dtype == torch.int8 and w_q.dtype == torch.int8,
+             "midgroup_w4a8_gemm: packed int4 planes must be int8 tensors")
+    _require(a_scale.dtype == torch.bfloat16 and w_scale.dtype == torch.bfloat16 and w_zero.dtype == torch.bfloat16,
+             "midgroup_w4a8_gemm: a_scale/w_scale/w_zero must be bfloat16")
+    _require(a_ksum.dtype == torch.int32 and w_ksum.dtype == torch.int32,
+             "midgroup_w4a8_gemm: a_ksum/w_ksum must be int32")
+    kb = geo.kpad(K, group) // 2
+    _require(a_hi.shape[1] == kb and a_lo.shape == a_hi.shape and w_q.shape[1] == kb,
+             f"midgroup_w4a8_gemm: packed row length must be Kpad/2 = {kb} for K={K} (group-padded layout); "
+             f"got a_hi {a_hi.shape[1]} w_q {w_q.shape[1]}")
+    M, N, G = a_hi.shape[0], w_q.shape[0], geo.num_groups(K, group)
+    _require(a_scale.dim() == 2 and a_scale.shape[0] == G and a_scale.shape[1] >= M and a_ksum.shape == a_scale.shape,
+             "midgroup_w4a8_gemm: a_scale/a_ksum must be group-major [K/group, M]")
+    _require(tuple(w_scale.shape) == (G, N) and tuple(w_zero.shape) == (G, N) and tuple(w_ksum.shape) == (G, N),
+             "midgroup_w4a8_gemm: w_scale/w_zero/w_ksum must be group-major [K/group, N]")
+    return M, N, G
+
+
+def _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, partials: bool):
+    M, N, G = _check_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group)
+    a_hi, a_lo, w_q = a_hi.contiguous(), a_lo.contiguous(), w_q.contiguous()
+    a_scale, a_ksum = a_scale.contiguous(), a_ksum.contiguous()
+    w_scale, w_zero = w_scale.contiguous(), w_zero.contiguous()
+    dev = a_hi.device
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    P = torch.empty((G, M, N), dtype=torch.int32, device=dev) if partials else None
+    if M:
+        # w_ksum is validated but not read: the activation bytes are rebuilt
+        # exactly from the two planes, so the kernel needs no +8 correction
+        _abi.check(_abi.lib().w4a8_midgroup_gemm(a_hi.data_ptr(), a_lo.data_ptr(), a_scale.data_ptr(),
+                                                 a_ksum.data_ptr(), M, a_scale.stride(0), w_q.data_ptr(),
+                                                 w_scale.data_ptr(), w_zero.data_ptr(), y.data_ptr(), N,
+                                                 P.data_ptr() if P is not None else None, N, K, group,
+                                                 _stream(dev)), "midgroup_w4a8_gemm")
+    return (y, P) if partials else y
+
+
+@torch.library.impl(_LIB, "midgroup_w4a8_gemm", "CUDA")
+def _midgroup_gemm_cuda(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K: int, group: int = 1024):
+    """The reference's run_midgroup_w4a8_gemm (npu_ops/host/midgroup_w4a8_gemm.cpp:45-140): y bf16
+    [a_hi rows, N]; callers slice back to their real rows, as with the reference."""
+    return _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, False)
+
+
+@torch.library.register_fake("npu::midgroup_w4a8_gemm")
+def _midgroup_gemm_fake(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group=1024):
+    return a_scale.new_empty((a_hi.shape[0], w_q.shape[0]), dtype=torch.bfloat16)
+
+
+@torch.library.impl(_LIB, "midgroup_w4a8_gemm_partials", "CUDA")
+def _midgroup_gemm_partials_cuda(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K: int,
+                                 group: int = 1024):
+    return _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, True)
+
+
+@torch.library.register_fake("npu::midgroup_w4a8_gemm_partials")
+def _midgroup_gemm_partials_fake(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group=1024):
+    M, N, G = a_hi.shape[0], w_q.shape[0], geo.num_groups(K, group)
+    return (a_scale.new_empty((M, N), dtype=torch.bfloat16), a_scale.new_empty((G, M, N), dtype=torch.int32))

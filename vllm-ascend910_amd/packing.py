@@ -86,5 +86,45 @@ def quantize_weight(w: torch.Tensor, group: int, scale_dtype: torch.dtype = torc
     return pack_grouped(codes, group), scales.to(scale_dtype).T.contiguous()
 
 
+def quantize_weight_asym(w: torch.Tensor, group: int = 1024
+                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Asymmetric int4 per-group RTN, the reference's export for its mid-group pair
+    (npu_ops/python/w4a8_ops.py:181-240): float [N, K] -> (w_q [N, kpad/2] int8,
+    w_scale [G, N] bf16, w_ksum [G, N] int32 of the raw codes, w_zero [G, N] bf16).
+
+    Per group (fakequant_lab/quant.py:106-141 with QuantSpec(4, group, sym=False)):
+    s = bf16((max - min) / 15) (bf16 tiny if zero), z = bf16(-8 - round(min / s)),
+    q = clamp(round(w / s) + z, -8, 7); a constant group takes s = bf16(|v| / 7),
+    z = 0.  The ragged tail is quantised as its own group.
+    """
+    N, K = w.shape
+    G = geo.num_groups(K, group)
+    codes = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    scales = torch.empty((N, G), dtype=torch.bfloat16, device=w.device)
+    zeros = torch.empty((N, G), dtype=torch.bfloat16, device=w.device)
+    k_full = group * (K // group)
+    tiny = lambda t: torch.where(t == 0, torch.full_like(t, BF16_TINY), t)  # noqa: E731
+    for g0, width, gl in ((0, k_full, group), (k_full, K - k_full, K - k_full)):
+        if width == 0:
+            continue
+        ng = width // gl
+        wg = w[:, g0:g0 + width].float().reshape(N, ng, gl)
+        mx, mn = wg.amax(dim=-1, keepdim=True), wg.amin(dim=-1, keepdim=True)
+        rng = mx - mn
+        s = tiny((rng / 15.0).to(torch.bfloat16))
+        z = (-8.0 - torch.round(mn / s.float())).to(torch.bfloat16)
+        const = rng == 0
+        s = torch.where(const, tiny((mx.abs() / 7.0).to(torch.bfloat16)), s)
+        z = torch.where(const, torch.zeros_like(z), z)
+        q = (torch.round(wg / s.float()) + z.float()).clamp_(-8, 7).to(torch.int8)
+        codes[:, g0:g0 + width] = q.reshape(N, width)
+        gi = g0 // group
+        scales[:, gi:gi + ng] = s.squeeze(-1)
+        zeros[:, gi:gi + ng] = z.squeeze(-1)
+    ksum = torch.stack([codes[:, g * group:g * group + geo.group_real(g, K, group)].to(torch.int32).sum(dim=1)
+                        for g in range(G)], dim=0).to(torch.int32)
+    return pack_grouped(codes, group), scales.T.contiguous(), ksum.contiguous(), zeros.T.contiguous()
+
+
 def repacked_sizes(N: int, K: int, group: int) -> Tuple[int, tuple]:
     return geo.repacked_weight_bytes(N, K, group), geo.repacked_scale_shape(N, K, group)
