@@ -65,6 +65,8 @@ def main():
     ap.add_argument("--cold-bytes", type=float, default=1.0, help="GiB of distinct weight copies to rotate")
     ap.add_argument("--detail-launches", type=int, default=40)
     ap.add_argument("--prefill-m", default="1024,4096")
+    ap.add_argument("--compat", action="store_true",
+                    help="also time the reference-compat mid-group pair (group 1024, asymmetric) at M 1/16/64/1024")
     ap.add_argument("--config4", action="store_true",
                     help="also time configs[3]: groups 64/256/512 at M 16/4096, gate_up with the fused SwiGLU")
     ap.add_argument("--no-detail", action="store_true", help="only the timed steps (for profiling)")
@@ -314,6 +316,8 @@ def main():
         del weights
         torch.cuda.empty_cache()
         result["config4_shapes"] = config4(pkg, dev, synth, make_pool, time_graph, T)
+    if args.compat:
+        result["compat_shapes"] = compat(pkg, dev, synth, time_graph, T, args.cold_bytes)
 
     # ---------------------------------------------------------------- CPU baseline
     if not args.no_cpu_baseline:
@@ -362,6 +366,54 @@ def config4(pkg, dev, synth, make_pool, time_graph, T):
                 del x, a_q, a_s
             del pool
             torch.cuda.empty_cache()
+    return rows
+
+
+def compat(pkg, dev, synth, time_graph, T, cold_bytes):
+    """The reference-compat pair (midgroup_quant_a + midgroup_w4a8_gemm, group 1024, asymmetric) on
+    the reference's packed tensors, cold pools as for the main path."""
+    import numpy as np
+    import torch
+    G = 1024
+    gen = torch.Generator(device=dev)
+    rows = []
+    for pi, p in enumerate(PROJS):
+        K, N = synth.QWQ_SHAPES[p]
+        kb, ng = pkg.geometry.kpad(K, G) // 2, pkg.geometry.num_groups(K, G)
+        per = N * kb + ng * N * 8
+        pool = []
+        for r in range(max(8, math.ceil(cold_bytes * 2 ** 30 / per))):
+            gen.manual_seed(70000 + 1000 * pi + r)
+            w_q = torch.randint(-128, 128, (N, kb), dtype=torch.int8, device=dev, generator=gen)
+            ws = (torch.rand((ng, N), device=dev, generator=gen) * 0.018 + 0.002).to(torch.bfloat16)
+            wz = torch.randint(-8, 8, (ng, N), device=dev, generator=gen).to(torch.bfloat16)
+            wk = torch.zeros((ng, N), dtype=torch.int32, device=dev)
+            pool.append((w_q, ws, wk, wz))
+        for M in (1, 16, 64, 1024):
+            x = torch.from_numpy(synth.activations(M, K, seed=M).view(np.int16)).view(torch.bfloat16).to(dev)
+            a = torch.ops.npu.midgroup_quant_a(x, G)
+            n = T if M <= 64 else 4
+
+            def gemms(a=a, K=K, n=n):
+                for i in range(n):
+                    torch.ops.npu.midgroup_w4a8_gemm(*a, *pool[i % len(pool)], K, G)
+
+            def quants(x=x, n=n):
+                for _ in range(n):
+                    torch.ops.npu.midgroup_quant_a(x, G)
+
+            us, qus = time_graph(gemms) / n, time_graph(quants) / n
+            Mp = a[0].shape[0]
+            b = N * kb + ng * N * 6 + Mp * kb * 2 + ng * Mp * 6 + 2 * Mp * N
+            tops = 2 * M * N * K / us / 1e6
+            rows.append({"proj": p, "M": M, "gemm_us": round(us, 2), "GBs": round(b / us / 1e3, 1),
+                         "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "TOPS": round(tops, 1),
+                         "mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "quant_a_us": round(qus, 2)})
+            log(f"  compat {p:13s} M={M:5d}: gemm {us:9.2f} us {b / us / 1e3:7.1f} GB/s "
+                f"({b / us / 1e3 / HBM_PEAK_GBS:.1%}) {tops:7.1f} TOPS  quant_a {qus:7.2f} us")
+            del x, a
+        del pool
+        torch.cuda.empty_cache()
     return rows
 
 
