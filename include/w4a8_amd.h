@@ -148,6 +148,23 @@ int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale,
                              void* stream);
 
 /*
+ * RMSNorm fused with the per-token activation quant (the producer-side fusion
+ * the reference ranked first for decode, whose quant launches are pure
+ * overhead: MGCKPT/P4_E2E.md:1043).  Per row:
+ *   s = bf16(x + residual)   (residual may be NULL: s = x)
+ *   h = bf16( bf16(s * (1 / sqrt(mean(s^2) + eps))) * weight )
+ *   a_q, a_scale = w4a8_quant_act of h with the same group (padded layout)
+ * the reference decoder layer's `rms_norm` (npu_ops/python/bench_decode_layer.py:36-38)
+ * on the residual stream it keeps (:69-79).  sum_out (s) and h_out (h) are
+ * optional bf16 outputs.  K % 8 == 0, K <= 65536; bf16 rows 16-byte aligned.
+ * No counterpart entry point in the reference, which runs these as separate
+ * vendor kernels (npu_rms_norm, then midgroup_quant_a).
+ */
+int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight, float eps,
+                       void* sum_out, int64_t lds, void* h_out, int64_t ldh, void* a_q, int64_t lda, void* a_scale,
+                       int64_t M, int64_t K, int64_t group, void* stream);
+
+/*
  * ---- Reference-compat mid-group path ----
  * The reference's own op pair, on its own tensors, for callers that keep its
  * exported mid-group checkpoints: per (token, K-group) activation scales, MSD

@@ -256,6 +256,27 @@ def gemm_f64(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_s
     return acc
 
 
+# ------------------------------------------------------------------ RMSNorm (decoder layer)
+def add_bf16(x_bits: np.ndarray, r_bits: np.ndarray) -> np.ndarray:
+    """bf16 + bf16 -> bf16 (the fp32 sum of two bf16 values, rounded once)."""
+    return f32_to_bf16_bits((bf16_bits_to_f32(x_bits) + bf16_bits_to_f32(r_bits)).astype(np.float32))
+
+
+def rms_norm_bf16(s_bits: np.ndarray, w_bits: np.ndarray, eps: float, return_h1: bool = False):
+    """The reference decoder layer's rms_norm on a bf16 row (npu_ops/python/bench_decode_layer.py:36-38):
+    v = float(s); h = bf16(v * rsqrt(mean(v^2) + eps)) * w in bf16.  The mean is taken exactly
+    (float64) and rounded to fp32, rsqrt correctly rounded in fp32; torch's own fp32 summation
+    order may move r by an fp32 ulp, so a bf16 result can differ by one ulp at a rounding tie."""
+    v = bf16_bits_to_f32(s_bits)
+    K = v.shape[-1]
+    ms = ((v.astype(np.float64) ** 2).sum(axis=-1) / K).astype(np.float32)
+    t = (ms + np.float32(eps)).astype(np.float32)
+    r = (1.0 / np.sqrt(t.astype(np.float64))).astype(np.float32)
+    h1 = round_bf16((v * r[..., None]).astype(np.float32))
+    h = f32_to_bf16_bits((h1 * bf16_bits_to_f32(w_bits)).astype(np.float32))
+    return (h, h1) if return_h1 else h
+
+
 # ------------------------------------------------------------------ mid-group compat path
 def quant_act_midgroup(x_bits: np.ndarray, group: int) -> Tuple[np.ndarray, np.ndarray]:
     """Per (token, K-group) int8 quant of a bf16 [M, K]: (q int8 [M, K], scale bf16 bits [G, M]).

@@ -536,3 +536,42 @@ def test_midgroup_linear_module(pkg, dev):
              ).float().numpy()
     got = y.reshape(-1, N).float().cpu().numpy()
     assert np.max(np.abs(got - y_ref) - 2 * ow.bf16_ulp(y_ref)) <= 0
+
+
+# ------------------------------------------------------------------ RMSNorm + quant
+@pytest.mark.parametrize("M", [1, 4, 16, 64, 300])
+@pytest.mark.parametrize("K,G", [(5120, 0), (5120, 128), (27648, 128), (3456, 1024), (1024, 0)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_rmsnorm_quant(pkg, dev, M, K, G, with_res):
+    """Two-stage bar: the emitted normalised row within one bf16 ulp of the oracle's
+    rms_norm (>= 99.9% equal: the fp32 sum order is not fixed by any reference file), and
+    the int8 codes and scales byte-exact against the per-token quant of that emitted row;
+    the residual sum exactly."""
+    say(f"rmsnorm_quant M={M} K={K} G={G} res={with_res}")
+    rng = np.random.default_rng(M + K + G)
+    xb = pkg.synth.activations(M, K, seed=M + K)
+    rb = ow.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32)) if with_res else None
+    wb = ow.f32_to_bf16_bits(rng.uniform(0.5, 1.5, K).astype(np.float32))
+    x = bf16_bits_tensor(xb).to(dev)
+    w = bf16_bits_tensor(wb).to(dev)
+    r = bf16_bits_tensor(rb).to(dev) if with_res else None
+    a_q, a_s, s, h = torch.ops.npu.w4a8_rmsnorm_quant(x, w, 1e-6, r, G, True)
+    torch.cuda.synchronize()
+    sb = ow.add_bf16(xb, rb) if with_res else xb
+    if with_res:
+        assert np.array_equal(tensor_bf16_bits(s), sb), "residual sum"
+    hg = tensor_bf16_bits(h)
+    he, h1 = ow.rms_norm_bf16(sb, wb, 1e-6, return_h1=True)
+    # the GPU's intermediate bf16(s * r) may sit one bf16 ulp from the oracle's (r differs
+    # in its last fp32 bit); the final product must then be one of the three outcomes
+    wf = ow.bf16_bits_to_f32(wb)
+    ok = hg == he
+    for k in (-1, 1):
+        h1k = (h1.astype(np.float64) + k * ow.bf16_ulp(h1)).astype(np.float32)
+        ok |= hg == ow.f32_to_bf16_bits((h1k * wf).astype(np.float32))
+    bad = np.argwhere(~ok)
+    assert ok.all(), f"{len(bad)} normed values outside one intermediate ulp, first at {bad[:3].tolist()}"
+    assert np.mean(hg == he) >= 0.999
+    q, sc = ow.quant_act_per_token(hg)
+    assert np.array_equal(tensor_bf16_bits(a_s), sc)
+    assert np.array_equal(a_q.cpu().numpy(), ow.pad_groups(q, G) if G else q)

@@ -395,3 +395,48 @@ def test_midgroup_gemm_matches_reference_cpp_bitwise(K, gk, asym):
     if ow.num_groups(K, gk) > 1:
         wrong = ow.f32_to_bf16_bits(ow.gemm_midgroup_fp32(q, sc, codes, ws[::-1].copy(), wz, gk))
         assert not np.array_equal(wrong, ref)
+
+
+
+# --------------------------------------------------------------- RMSNorm
+def test_rms_norm_matches_torch_formula():
+    """The oracle against the reference's own torch expression on CPU
+    (bench_decode_layer.py:36-38), with its fp32 summation order."""
+    rng = np.random.default_rng(8)
+    x = ow.f32_to_bf16_bits((rng.standard_normal((64, 5120)) * rng.uniform(0.1, 20, (64, 1))).astype(np.float32))
+    w = ow.f32_to_bf16_bits(rng.uniform(0.5, 1.5, 5120).astype(np.float32))
+    ours = ow.bf16_bits_to_f32(ow.rms_norm_bf16(x, w, 1e-6)).astype(np.float64)
+    tx = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    tw = torch.from_numpy(w.view(np.int16)).view(torch.bfloat16)
+    v = tx.float()
+    ref = ((v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * tw).float().numpy()
+    assert np.mean(ours == ref) > 0.999
+    assert np.all(np.abs(ours - ref) <= ow.bf16_ulp(ref))
+
+
+def test_rms_norm_matches_high_precision():
+    """Small rows against exact rational mean and a 40-digit square root, each fp32
+    step rounded as the formula prescribes; and the residual add exactly."""
+    from decimal import Decimal, getcontext
+    getcontext().prec = 40
+    rng = np.random.default_rng(1)
+    for _ in range(20):
+        s = ow.f32_to_bf16_bits((rng.standard_normal(16) * 3).astype(np.float32))
+        w = ow.f32_to_bf16_bits(rng.uniform(0.5, 1.5, 16).astype(np.float32))
+        vs = [Fraction(float(v)) for v in ow.bf16_bits_to_f32(s)]
+        ms = round_to_float(sum(v * v for v in vs) / 16, 24)
+        t = round_to_float(ms + round_to_float(Fraction(1e-6), 24), 24)
+        rd = Decimal(1) / (Decimal(t.numerator) / Decimal(t.denominator)).sqrt()
+        r = round_to_float(Fraction(rd), 24)
+        exp = []
+        for v, wv in zip(vs, ow.bf16_bits_to_f32(w)):
+            p = v * r
+            h1 = (round_to_float(round_to_float(abs(p), 24), 8) if p else Fraction(0)) * (1 if p >= 0 else -1)
+            q = h1 * Fraction(float(wv))
+            exp.append(float((round_to_float(abs(q), 8) if q else Fraction(0)) * (1 if q >= 0 else -1)))
+        got = ow.bf16_bits_to_f32(ow.rms_norm_bf16(s[None, :], w, 1e-6))[0]
+        assert list(got) == exp
+    # a half-ulp tie rounds to even, just above half rounds up, exact cancellation
+    a = ow.f32_to_bf16_bits(np.array([1.0, 1.0, -2.5], np.float32))
+    b = ow.f32_to_bf16_bits(np.array([2.0 ** -8, 3 * 2.0 ** -9, 2.5], np.float32))
+    assert list(ow.bf16_bits_to_f32(ow.add_bf16(a, b))) == [1.0, 1.0078125, 0.0]

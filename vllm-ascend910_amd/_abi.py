@@ -35,6 +35,8 @@ SIGNATURES = {
     "w4a8_midgroup_quant_a": (_I, [_VP, _I64, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP]),
     "w4a8_midgroup_gemm": (_I, [_VP, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
                                 _VP]),
+    "w4a8_rmsnorm_quant": (_I, [_VP, _I64, _VP, _I64, _VP, ctypes.c_float, _VP, _I64, _VP, _I64, _VP, _I64, _VP,
+                                _I64, _I64, _I64, _VP]),
     "w4a8_gemm_debug_partials": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _VP, _I64, _I64, _I64, _I64,
                                       _VP, _I64, _VP]),
 }

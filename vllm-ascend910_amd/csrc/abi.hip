@@ -254,4 +254,43 @@ int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, 
     return hip_status(launch_gemm_midgroup(a, static_cast<hipStream_t>(stream)), "w4a8_midgroup_gemm launch");
 }
 
+int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight, float eps,
+                       void* sum_out, int64_t lds, void* h_out, int64_t ldh, void* a_q, int64_t lda, void* a_scale,
+                       int64_t M, int64_t K, int64_t group, void* stream) {
+    if (M < 0 || K <= 0 || M >= (1ll << 31) || group < 0)
+        return fail(W4A8_ERR_SHAPE, "bad shape: M=%lld K=%lld group=%lld", M, K, group);
+    if (K % 8 != 0 || K > 65536)
+        return fail(W4A8_ERR_UNSUPPORTED, "K=%lld: the fused RMSNorm needs K %% 8 == 0 and K <= 65536", K);
+    if (group > 0 && group % 8 != 0 && !geom::is_unpadded(K, group))
+        return fail(W4A8_ERR_UNSUPPORTED, "group=%lld: a padded output layout needs group %% 8 == 0", group);
+    if (!(eps >= 0.0f)) return fail(W4A8_ERR_SHAPE, "eps must be >= 0");
+    if (M == 0) return W4A8_OK;
+    if (!x || !weight || !a_q || !a_scale) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    const int64_t width = group > 0 ? geom::kpad(K, group) : K;
+    if (ldx < K || lda < width || (residual && ldr < K) || (sum_out && lds < K) || (h_out && ldh < K))
+        return fail(W4A8_ERR_SHAPE, "leading dimensions must cover the row (K=%lld, a_q width %lld)", K, width);
+    auto al16 = [](const void* p, int64_t ld) { return !p || (aligned(p, 16) && ld % 8 == 0); };
+    if (!al16(x, ldx) || !al16(residual, ldr) || !al16(sum_out, lds) || !al16(h_out, ldh) || !aligned(weight, 16) ||
+        !aligned(a_q, 8) || lda % 8 != 0 || !aligned(a_scale, 2))
+        return fail(W4A8_ERR_ALIGN, "bf16 rows 16-byte aligned (ld %% 8 == 0), a_q 8-byte aligned (lda %% 8 == 0)");
+    RmsNormArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.residual = residual;
+    a.ldr = ldr;
+    a.weight = weight;
+    a.eps = eps;
+    a.sum_out = sum_out;
+    a.lds = lds;
+    a.h_out = h_out;
+    a.ldh = ldh;
+    a.a_q = a_q;
+    a.lda = lda;
+    a.a_scale = a_scale;
+    a.M = M;
+    a.K = K;
+    a.group = group;
+    return hip_status(launch_rmsnorm_quant(a, static_cast<hipStream_t>(stream)), "w4a8_rmsnorm_quant launch");
+}
+
 }  // extern "C"

@@ -80,6 +80,25 @@ struct MidgroupArgs {
 int64_t midgroup_lds_bytes(int64_t Ma, int64_t K, int64_t group);
 hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream);
 
+// RMSNorm (+ optional residual add) fused with the per-token quant.
+struct RmsNormArgs {
+    const void* x;
+    int64_t ldx;
+    const void* residual;   // optional
+    int64_t ldr;
+    const void* weight;     // bf16 [K]
+    float eps;
+    void* sum_out;          // optional bf16 [M, lds]
+    int64_t lds;
+    void* h_out;            // optional bf16 [M, ldh]
+    int64_t ldh;
+    void* a_q;
+    int64_t lda;
+    void* a_scale;
+    int64_t M, K, group;
+};
+hipError_t launch_rmsnorm_quant(const RmsNormArgs& a, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace w4a8

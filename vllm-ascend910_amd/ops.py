@@ -44,6 +44,8 @@ _LIB.define("w4a8_gemm_partials(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tens
             "int N, int K, int group) -> (Tensor, Tensor)")
 _LIB.define("w4a8_gemm_swiglu(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
             "int N, int K, int group) -> Tensor")
+_LIB.define("w4a8_rmsnorm_quant(Tensor x, Tensor weight, float eps, Tensor? residual=None, int group=0, "
+            "bool want_normed=False) -> (Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("midgroup_quant_a(Tensor x, int group=1024) -> Tensor[]")
 _LIB.define("midgroup_w4a8_gemm(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
             "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> Tensor")
@@ -223,6 +225,48 @@ def _gemm_partials_fake(a_q, a_scale, w_tiles, s_tiles, N, K, group):
     M = a_q.shape[0]
     return (a_q.new_empty((M, N), dtype=torch.bfloat16),
             a_q.new_empty((geo.num_groups(K, group), M, N), dtype=torch.int32))
+
+
+# ---------------------------------------------------------------- RMSNorm + quant
+@torch.library.impl(_LIB, "w4a8_rmsnorm_quant", "CUDA")
+def _rmsnorm_quant_cuda(x: torch.Tensor, weight: torch.Tensor, eps: float, residual=None, group: int = 0,
+                        want_normed: bool = False):
+    """(a_q, a_scale, s, h): the per-token quant of h = rms_norm(s) * weight, s = x + residual
+    (s is empty without a residual -- the stream is x itself; h is empty unless want_normed)."""
+    _require(x.dim() == 2 and x.dtype == torch.bfloat16, "w4a8_rmsnorm_quant: x must be bfloat16 [M, K]")
+    M, K = x.shape
+    _require(weight.dtype == torch.bfloat16 and tuple(weight.shape) == (K,),
+             "w4a8_rmsnorm_quant: weight must be bfloat16 [K]")
+    if x.stride(1) != 1 or x.stride(0) % 8:
+        x = x.contiguous()
+    weight = weight.contiguous()
+    dev = x.device
+    if residual is not None:
+        _require(residual.dtype == torch.bfloat16 and residual.shape == x.shape,
+                 "w4a8_rmsnorm_quant: residual must match x")
+        if residual.stride(1) != 1 or residual.stride(0) % 8:
+            residual = residual.contiguous()
+        s = torch.empty_like(x)
+    else:
+        s = x.new_empty((0, K))
+    width = _quant_width(K, group)
+    a_q = torch.empty((M, width), dtype=torch.int8, device=dev)
+    a_scale = torch.empty((M,), dtype=torch.bfloat16, device=dev)
+    h = torch.empty((M, K) if want_normed else (0, K), dtype=torch.bfloat16, device=dev)
+    if M:
+        _abi.check(_abi.lib().w4a8_rmsnorm_quant(
+            x.data_ptr(), x.stride(0), residual.data_ptr() if residual is not None else None,
+            residual.stride(0) if residual is not None else 0, weight.data_ptr(), float(eps),
+            s.data_ptr() if residual is not None else None, K, h.data_ptr() if want_normed else None, K,
+            a_q.data_ptr(), width, a_scale.data_ptr(), M, K, group, _stream(dev)), "w4a8_rmsnorm_quant")
+    return a_q, a_scale, s, h
+
+
+@torch.library.register_fake("npu::w4a8_rmsnorm_quant")
+def _rmsnorm_quant_fake(x, weight, eps, residual=None, group=0, want_normed=False):
+    M, K = x.shape
+    return (x.new_empty((M, _quant_width(K, group)), dtype=torch.int8), x.new_empty((M,), dtype=torch.bfloat16),
+            x.new_empty((M, K) if residual is not None else (0, K)), x.new_empty((M, K) if want_normed else (0, K)))
 
 
 # ---------------------------------------------------------------- mid-group compat pair
