@@ -1,0 +1,255 @@
+"""QwQ-32B-shaped decoder forward with every linear on the W4A8 kernels.
+
+The reference measures its W4A8 linear inside whole decoder layers
+(npu_ops/python/bench_decode_layer.py:40-82, bench_decode_graph.py:44-65):
+RMSNorm -> qkv -> attention over a KV cache -> o -> residual -> RMSNorm ->
+gate_up -> SwiGLU -> down -> residual.  This module builds that model
+(Qwen2 architecture: grouped-query attention with q/k/v bias, rotary
+embeddings, RMSNorm) on this build's ops:
+
+* RMSNorm, the residual add and the activation quant run as one kernel
+  (``torch.ops.npu.w4a8_rmsnorm_quant``) in front of qkv and gate_up;
+* gate_up runs with the fused SwiGLU epilogue (``w4a8_gemm_swiglu``);
+* o and down take ``w4a8_quant_pertoken`` activations;
+* attention stays on PyTorch-ROCm in bf16, written with contiguous batched
+  products only: the K cache is stored transposed ``[B, KVH, D, L]`` and the
+  query heads of one KV head form the rows of one product, so grouped-query
+  attention needs no head repeat and no transposed operand;
+* the decode step is shape-static -- position, RoPE row, KV write index and
+  mask are device tensors -- so it is captured once per batch size in a HIP
+  graph and replayed, the greedy token feeding the next step inside the graph.
+
+Weights are random (seeded), as in the reference's latency benches: codes
+uniform in [-8, 7], group scales U[0.002, 0.02] at group 128.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+
+from . import geometry as geo
+from . import ops  # noqa: F401  (registers torch.ops.npu.*)
+
+
+@dataclass
+class DecoderConfig:
+    """QwQ-32B (Qwen2) shapes by default."""
+    layers: int = 64
+    hidden: int = 5120
+    heads: int = 40
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 27648
+    vocab: int = 152064
+    group: int = 128
+    rms_eps: float = 1e-5
+    rope_theta: float = 1.0e6
+    qkv_bias: bool = True
+
+    @property
+    def qkv_out(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+class _Linear:
+    """Repacked W4A8 weight of one projection (random codes, seeded)."""
+
+    def __init__(self, N: int, K: int, group: int, gen: torch.Generator, device, bias: bool = False,
+                 keep: bool = False):
+        codes = torch.randint(-8, 8, (N, K), dtype=torch.int8, device=device, generator=gen)
+        from .packing import pack_grouped
+        w_q = pack_grouped(codes, group)
+        G = geo.num_groups(K, group)
+        ws = (torch.rand((G, N), device=device, generator=gen) * 0.018 + 0.002).to(torch.bfloat16)
+        self.w_tiles, self.s_tiles = torch.ops.npu.w4a8_repack(w_q, ws, K, group)
+        # codes and scales kept only for reference checks of small models
+        self.codes, self.scales = (codes, ws) if keep else (None, None)
+        del codes
+        self.N, self.K, self.group = N, K, group
+        self.bias = ((torch.rand((N,), device=device, generator=gen) - 0.5) * 0.2).to(torch.bfloat16) if bias \
+            else None
+
+    def __call__(self, a_q: torch.Tensor, a_s: torch.Tensor) -> torch.Tensor:
+        y = torch.ops.npu.w4a8_gemm(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+        return y + self.bias if self.bias is not None else y
+
+    def swiglu(self, a_q: torch.Tensor, a_s: torch.Tensor) -> torch.Tensor:
+        return torch.ops.npu.w4a8_gemm_swiglu(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+
+
+class W4A8Decoder:
+    """The decoder with a static KV cache for ``batch`` sequences of up to ``max_len`` tokens."""
+
+    def __init__(self, cfg: DecoderConfig, batch: int, max_len: int, device="cuda", seed: int = 0,
+                 keep_weights: bool = False):
+        self.cfg, self.batch, self.max_len = cfg, batch, max_len
+        dev = torch.device(device)
+        self.device = dev
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        c = cfg
+        self.embed = (torch.randn((c.vocab, c.hidden), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        self.lm_head = (torch.randn((c.vocab, c.hidden), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        self.final_norm = (1.0 + 0.1 * torch.randn((c.hidden,), device=dev, generator=gen)).to(torch.bfloat16)
+        self.layers = []
+        for _ in range(c.layers):
+            self.layers.append({
+                "ln1": (1.0 + 0.1 * torch.randn((c.hidden,), device=dev, generator=gen)).to(torch.bfloat16),
+                "ln2": (1.0 + 0.1 * torch.randn((c.hidden,), device=dev, generator=gen)).to(torch.bfloat16),
+                "qkv": _Linear(c.qkv_out, c.hidden, c.group, gen, dev, bias=c.qkv_bias, keep=keep_weights),
+                "o": _Linear(c.hidden, c.heads * c.head_dim, c.group, gen, dev, keep=keep_weights),
+                "gate_up": _Linear(2 * c.ffn, c.hidden, c.group, gen, dev, keep=keep_weights),
+                "down": _Linear(c.hidden, c.ffn, c.group, gen, dev, keep=keep_weights),
+            })
+        kvh, d = c.kv_heads, c.head_dim
+        # K stored transposed so that q @ K is a product of contiguous operands
+        self.k_cache = [torch.zeros((batch, kvh, d, max_len), dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        self.v_cache = [torch.zeros((batch, kvh, max_len, d), dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        inv = 1.0 / (c.rope_theta ** (torch.arange(0, d, 2, device=dev, dtype=torch.float32) / d))
+        ang = torch.arange(max_len, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+        self.cos, self.sin = torch.cos(ang), torch.sin(ang)          # [L, d/2] fp32
+        self.positions = torch.arange(max_len, device=dev)
+        # decode-step state (device tensors, so a captured step is position-independent)
+        self.pos = torch.zeros((1,), dtype=torch.long, device=dev)
+        self.tokens = torch.zeros((batch,), dtype=torch.long, device=dev)
+        self._graph: Optional[torch.cuda.CUDAGraph] = None
+
+    # ------------------------------------------------------------ pieces
+    def _rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """Rotary embedding, rotate-half form; x [..., T, heads, d], cos/sin [T, d/2]."""
+        h = x.shape[-1] // 2
+        xf = x.float()
+        x1, x2 = xf[..., :h], xf[..., h:]
+        c, s = cos[:, None, :], sin[:, None, :]
+        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1).to(torch.bfloat16)
+
+    def _attend(self, q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+        """q [B, KVH, R, D] (R = query heads per KV head x query tokens), kc [B, KVH, D, L],
+        vc [B, KVH, L, D], additive bias broadcast to [B, KVH, R, L] -> [B, KVH, R, D]."""
+        scores = torch.matmul(q, kc).float() * (1.0 / math.sqrt(self.cfg.head_dim)) + bias
+        p = torch.softmax(scores, dim=-1).to(torch.bfloat16)
+        return torch.matmul(p, vc)
+
+    def _mlp_and_next(self, L: dict, s: torch.Tensor, a_attn: torch.Tensor):
+        """o projection, residual, RMSNorm+quant, gate_up+SwiGLU, down; returns (stream, delta)."""
+        c = self.cfg
+        aq, as_ = torch.ops.npu.w4a8_quant_pertoken(a_attn, c.group)
+        o = L["o"](aq, as_)
+        aq2, as2, s2, _ = torch.ops.npu.w4a8_rmsnorm_quant(o, L["ln2"], c.rms_eps, s, c.group)
+        h = L["gate_up"].swiglu(aq2, as2)
+        aq3, as3 = torch.ops.npu.w4a8_quant_pertoken(h, c.group)
+        return s2, L["down"](aq3, as3)
+
+    # ------------------------------------------------------------ prefill
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor) -> torch.Tensor:
+        """tokens [B, S] -> greedy next tokens [B]; fills the KV cache for positions [0, S)."""
+        c, B = self.cfg, self.batch
+        S = tokens.shape[1]
+        assert tokens.shape[0] == B and S <= self.max_len
+        G = c.heads // c.kv_heads
+        cos, sin = self.cos[:S], self.sin[:S]
+        causal = torch.full((S, S), float("-inf"), device=self.device).triu_(1)
+        x = self.embed[tokens.reshape(-1)]                               # [B*S, hidden]
+        delta = None
+        for li, L in enumerate(self.layers):
+            aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
+            x = s if delta is not None else x
+            qkv = L["qkv"](aq, as_).view(B, S, c.heads + 2 * c.kv_heads, c.head_dim)
+            q = self._rope(qkv[:, :, :c.heads], cos, sin)
+            k = self._rope(qkv[:, :, c.heads:c.heads + c.kv_heads], cos, sin)
+            v = qkv[:, :, c.heads + c.kv_heads:]
+            self.k_cache[li][:, :, :, :S] = k.permute(0, 2, 3, 1)
+            self.v_cache[li][:, :, :S, :] = v.permute(0, 2, 1, 3)
+            kc = self.k_cache[li][:, :, :, :S].contiguous()
+            vc = self.v_cache[li][:, :, :S, :].contiguous()
+            out = torch.empty((B, S, c.heads, c.head_dim), dtype=torch.bfloat16, device=self.device)
+            for b in range(B):                                        # one sequence at a time bounds the scores
+                qb = q[b].view(S, c.kv_heads, G, c.head_dim).permute(1, 2, 0, 3).reshape(1, c.kv_heads, G * S,
+                                                                                        c.head_dim)
+                bias = causal.repeat(G, 1)                               # rows are (query head, token)
+                ob = self._attend(qb.contiguous(), kc[b:b + 1], vc[b:b + 1], bias)   # [1, KVH, G*S, D]
+                out[b] = ob.view(c.kv_heads, G, S, c.head_dim).permute(2, 0, 1, 3).reshape(S, c.heads, c.head_dim)
+            x, delta = self._mlp_and_next(L, x, out.view(B * S, c.heads * c.head_dim))
+        last = (x + delta).view(B, S, c.hidden)[:, -1]
+        return self._logits_argmax(last)
+
+    def _logits(self, x_last: torch.Tensor) -> torch.Tensor:
+        c = self.cfg
+        v = x_last.float()
+        h = (v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + c.rms_eps)).to(torch.bfloat16) * self.final_norm
+        return torch.nn.functional.linear(h, self.lm_head)
+
+    def _logits_argmax(self, x_last: torch.Tensor) -> torch.Tensor:
+        logits = self._logits(x_last)
+        self.last_logits = logits
+        return logits.argmax(dim=-1)
+
+    # ------------------------------------------------------------ decode
+    def _decode_step(self) -> None:
+        """One greedy step at self.pos for self.tokens, updating both in place (capturable)."""
+        c, B = self.cfg, self.batch
+        G = c.heads // c.kv_heads
+        cos = self.cos.index_select(0, self.pos)
+        sin = self.sin.index_select(0, self.pos)
+        bias = torch.where(self.positions > self.pos, float("-inf"), 0.0).view(1, 1, 1, self.max_len)
+        x = self.embed.index_select(0, self.tokens)                      # [B, hidden]
+        delta = None
+        for li, L in enumerate(self.layers):
+            aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
+            x = s if delta is not None else x
+            qkv = L["qkv"](aq, as_).view(B, 1, c.heads + 2 * c.kv_heads, c.head_dim)
+            q = self._rope(qkv[:, :, :c.heads], cos, sin)                # [B, 1, H, D]
+            k = self._rope(qkv[:, :, c.heads:c.heads + c.kv_heads], cos, sin)
+            v = qkv[:, :, c.heads + c.kv_heads:]
+            self.k_cache[li].index_copy_(3, self.pos, k.view(B, c.kv_heads, c.head_dim, 1))
+            self.v_cache[li].index_copy_(2, self.pos, v.reshape(B, c.kv_heads, 1, c.head_dim))
+            qg = q.view(B, c.kv_heads, G, c.head_dim)
+            o = self._attend(qg, self.k_cache[li], self.v_cache[li], bias)          # [B, KVH, G, D]
+            x, delta = self._mlp_and_next(L, x, o.reshape(B, c.heads * c.head_dim))
+        self.tokens.copy_(self._logits_argmax(x + delta))
+        self.pos.add_(1)
+
+    @torch.no_grad()
+    def decode(self, first_tokens: torch.Tensor, start_pos: int, steps: int, graph: bool = True) -> List[torch.Tensor]:
+        """Greedy decode ``steps`` tokens after a prefill of ``start_pos`` tokens; returns them."""
+        assert start_pos + steps <= self.max_len
+        self.tokens.copy_(first_tokens)
+        self.pos.fill_(start_pos)
+        out = []
+        if not graph:
+            for _ in range(steps):
+                self._decode_step()
+                out.append(self.tokens.clone())
+            return out
+        g = self.capture()
+        self.tokens.copy_(first_tokens)
+        self.pos.fill_(start_pos)
+        for _ in range(steps):
+            g.replay()
+            out.append(self.tokens.clone())
+        return out
+
+    def capture(self) -> torch.cuda.CUDAGraph:
+        """Capture one decode step (once); the step advances its own position."""
+        if self._graph is None:
+            saved_t, saved_p = self.tokens.clone(), self.pos.clone()
+            s = torch.cuda.Stream(device=self.device)
+            s.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(s):
+                self._decode_step()               # warm-up outside capture (allocator, lazy init)
+            torch.cuda.current_stream(self.device).wait_stream(s)
+            self.tokens.copy_(saved_t)
+            self.pos.copy_(saved_p)
+            torch.cuda.synchronize(self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                self._decode_step()
+            torch.cuda.synchronize(self.device)
+            self.tokens.copy_(saved_t)
+            self.pos.copy_(saved_p)
+            self._graph = g
+        return self._graph
