@@ -65,6 +65,10 @@ def main():
     ap.add_argument("--cold-bytes", type=float, default=1.0, help="GiB of distinct weight copies to rotate")
     ap.add_argument("--detail-launches", type=int, default=40)
     ap.add_argument("--prefill-m", default="1024,4096")
+    ap.add_argument("--decoder", action="store_true",
+                    help="also run configs[4]: the 64-layer QwQ-32B-shaped decoder, 1024-token prompts + 256 "
+                         "greedy decode steps at concurrency 1, 8, 64")
+    ap.add_argument("--decoder-layers", type=int, default=64)
     ap.add_argument("--compat", action="store_true",
                     help="also time the reference-compat mid-group pair (group 1024, asymmetric) at M 1/16/64/1024")
     ap.add_argument("--config4", action="store_true",
@@ -318,6 +322,8 @@ def main():
         result["config4_shapes"] = config4(pkg, dev, synth, make_pool, time_graph, T)
     if args.compat:
         result["compat_shapes"] = compat(pkg, dev, synth, time_graph, T, args.cold_bytes)
+    if args.decoder:
+        result["decoder"] = decoder_bench(pkg, dev, args.decoder_layers)
 
     # ---------------------------------------------------------------- CPU baseline
     if not args.no_cpu_baseline:
@@ -366,6 +372,43 @@ def config4(pkg, dev, synth, make_pool, time_graph, T):
                 del x, a_q, a_s
             del pool
             torch.cuda.empty_cache()
+    return rows
+
+
+def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
+    """prefill tokens/s and greedy decode tokens/s of the QwQ-32B-shaped decoder
+    (random W4A8 weights at group 128, bf16 attention on PyTorch-ROCm, decode steps replayed
+    from a HIP graph)."""
+    import torch
+    cfg = pkg.decoder.DecoderConfig(layers=layers)
+    t0 = time.perf_counter()
+    m = pkg.decoder.W4A8Decoder(cfg, batch=batches[0], max_len=prompt + steps, device=dev, seed=7)
+    torch.cuda.synchronize()
+    log(f"  decoder: {layers} layers built in {time.perf_counter() - t0:.1f} s")
+    rows = []
+    for B in batches:
+        m.resize(B, prompt + steps)
+        toks = torch.randint(0, cfg.vocab, (B, prompt), device=dev, generator=torch.Generator(device=dev).manual_seed(B))
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        torch.cuda.synchronize()
+        e[0].record()
+        first = m.prefill(toks)
+        e[1].record()
+        m.capture()
+        torch.cuda.synchronize()
+        e[2].record()
+        out = m.decode(first, prompt, steps, graph=True)
+        e[3].record()
+        torch.cuda.synchronize()
+        pre_ms, dec_ms = e[0].elapsed_time(e[1]), e[2].elapsed_time(e[3])
+        rows.append({"concurrency": B, "prompt_tokens": prompt, "decode_steps": steps,
+                     "prefill_ms": round(pre_ms, 1), "prefill_tok_s": round(B * prompt / pre_ms * 1e3, 1),
+                     "decode_ms_per_step": round(dec_ms / steps, 3), "decode_tok_s": round(B * steps / dec_ms * 1e3, 1),
+                     "last_tokens": [int(t) for t in out[-1][:4].tolist()]})
+        log(f"  decoder B={B:3d}: prefill {pre_ms:9.1f} ms ({B * prompt / pre_ms * 1e3:9.0f} tok/s), decode "
+            f"{dec_ms / steps:7.3f} ms/step ({B * steps / dec_ms * 1e3:8.1f} tok/s)")
+    del m
+    torch.cuda.empty_cache()
     return rows
 
 

@@ -136,3 +136,26 @@ def test_forward_matches_float_reference(pkg, dev):
     rel = (got - ref).norm() / ref.norm()
     say(f"decoder logits rel-L2 vs float64 reference: {rel:.5f}")
     assert rel < 2e-2, f"rel-L2 {rel}"
+
+
+def test_resize_then_capture_after_full_decode(pkg, dev):
+    """Regression: a decode that runs to max_len leaves the position at max_len; a later
+    resize + prefill + capture must neither index past the cache nor disturb the prefilled
+    cache (the captured step then matches eager decode)."""
+    say("decoder: resize after a full decode")
+    cfg = tiny_cfg(pkg)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=1, max_len=16, device=dev, seed=4)
+    p1 = torch.randint(0, cfg.vocab, (1, 8), generator=torch.Generator().manual_seed(5)).to(dev)
+    m.decode(m.prefill(p1), 8, 8, graph=True)                  # position ends at max_len
+    assert int(m.pos.item()) == 16
+    m.resize(2, 16)
+    assert int(m.pos.item()) == 0
+    p2 = torch.randint(0, cfg.vocab, (2, 8), generator=torch.Generator().manual_seed(6)).to(dev)
+    first = m.prefill(p2)
+    k0 = [k.clone() for k in m.k_cache]
+    m.capture()
+    assert all(torch.equal(a, b) for a, b in zip(m.k_cache, k0)), "capture changed the KV cache"
+    graph_out = m.decode(first, 8, 8, graph=True)
+    m2 = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=16, device=dev, seed=4)
+    eager_out = m2.decode(m2.prefill(p2), 8, 8, graph=False)
+    assert all(torch.equal(a, b) for a, b in zip(graph_out, eager_out))

@@ -117,6 +117,24 @@ class W4A8Decoder:
         self.tokens = torch.zeros((batch,), dtype=torch.long, device=dev)
         self._graph: Optional[torch.cuda.CUDAGraph] = None
 
+    def resize(self, batch: int, max_len: int) -> None:
+        """New KV cache and decode state for another batch size (weights are kept)."""
+        c, dev = self.cfg, self.device
+        self.batch, self.max_len = batch, max_len
+        self._graph = None
+        self.k_cache = self.v_cache = None
+        torch.cuda.empty_cache()
+        self.k_cache = [torch.zeros((batch, c.kv_heads, c.head_dim, max_len), dtype=torch.bfloat16, device=dev)
+                        for _ in self.layers]
+        self.v_cache = [torch.zeros((batch, c.kv_heads, max_len, c.head_dim), dtype=torch.bfloat16, device=dev)
+                        for _ in self.layers]
+        inv = 1.0 / (c.rope_theta ** (torch.arange(0, c.head_dim, 2, device=dev, dtype=torch.float32) / c.head_dim))
+        ang = torch.arange(max_len, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+        self.cos, self.sin = torch.cos(ang), torch.sin(ang)
+        self.positions = torch.arange(max_len, device=dev)
+        self.tokens = torch.zeros((batch,), dtype=torch.long, device=dev)
+        self.pos.zero_()
+
     # ------------------------------------------------------------ pieces
     def _rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
         """Rotary embedding, rotate-half form; x [..., T, heads, d], cos/sin [T, d/2]."""
@@ -234,16 +252,26 @@ class W4A8Decoder:
         return out
 
     def capture(self) -> torch.cuda.CUDAGraph:
-        """Capture one decode step (once); the step advances its own position."""
+        """Capture one decode step (once); the step advances its own position.
+
+        The warm-up step before capture runs at the last cache slot, whatever the
+        current position (a position left at max_len by an earlier decode would
+        index past the cache), and that slot's K/V are restored afterwards, so
+        capturing leaves the cache and the decode state as they were.  The graph
+        may only be replayed while the position is below max_len (decode()
+        checks this).
+        """
         if self._graph is None:
+            slot = self.max_len - 1
             saved_t, saved_p = self.tokens.clone(), self.pos.clone()
+            saved_k = [k[..., slot].clone() for k in self.k_cache]
+            saved_v = [v[:, :, slot].clone() for v in self.v_cache]
             s = torch.cuda.Stream(device=self.device)
             s.wait_stream(torch.cuda.current_stream(self.device))
             with torch.cuda.stream(s):
+                self.pos.fill_(slot)
                 self._decode_step()               # warm-up outside capture (allocator, lazy init)
             torch.cuda.current_stream(self.device).wait_stream(s)
-            self.tokens.copy_(saved_t)
-            self.pos.copy_(saved_p)
             torch.cuda.synchronize(self.device)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
@@ -251,5 +279,9 @@ class W4A8Decoder:
             torch.cuda.synchronize(self.device)
             self.tokens.copy_(saved_t)
             self.pos.copy_(saved_p)
+            for k, sk in zip(self.k_cache, saved_k):
+                k[..., slot] = sk
+            for v, sv in zip(self.v_cache, saved_v):
+                v[:, :, slot] = sv
             self._graph = g
         return self._graph
