@@ -575,3 +575,42 @@ def test_rmsnorm_quant(pkg, dev, M, K, G, with_res):
     q, sc = ow.quant_act_per_token(hg)
     assert np.array_equal(tensor_bf16_bits(a_s), sc)
     assert np.array_equal(a_q.cpu().numpy(), ow.pad_groups(q, G) if G else q)
+
+
+# ------------------------------------------------------------------ checkpoint formats
+def test_vendor_checkpoint_linear(pkg, dev):
+    """A vendor W4A8_DYNAMIC linear (packed along N, per-channel x per-group scales) loaded
+    onto the per-token path, against the oracle with the same codes and scales."""
+    say("vendor W4A8_DYNAMIC linear")
+    g = torch.Generator().manual_seed(9)
+    N, K, G = 256, 1024, 128
+    codes = torch.randint(-8, 8, (N, K), dtype=torch.int8, generator=g)
+    s2 = (torch.rand((N, K // G), generator=g) * 0.01 + 0.002).to(torch.float16)
+    c = codes.to(torch.int16) & 0xF
+    base = "model.layers.0.self_attn.o_proj"
+    t = {f"{base}.weight": (c[0::2] | (c[1::2] << 4)).to(torch.uint8).view(torch.int8),
+         f"{base}.weight_scale": torch.ones((N, 1)), f"{base}.weight_offset": torch.zeros((N, 1)),
+         f"{base}.weight_scale_second": s2}
+    m = pkg.checkpoint.load_vendor_linear(t, base, G, device=dev)
+    xb = pkg.synth.activations(5, K, seed=3)
+    y = m(bf16_bits_tensor(xb).to(dev))
+    torch.cuda.synchronize()
+    q, s = ow.quant_act_per_token(xb)
+    y32, mag = ow.gemm_fp32(q, s, codes.numpy(), s2.float().numpy(), G, return_abs=True)
+    check_output(tensor_bf16_bits(y), y32, mag, K // G, "vendor linear")
+
+
+def test_midgroup_checkpoint_linear(pkg, dev):
+    """An mg_kgeom_v1 export loaded into MidGroupW4A8Linear, against the oracle."""
+    say("mg_kgeom_v1 linear")
+    w = torch.randn((320, 2049), generator=torch.Generator().manual_seed(10)) * 0.04
+    base = "model.layers.3.mlp.down_proj"
+    out = pkg.checkpoint.export_midgroup({f"{base}.weight": w}, 1024)
+    m = pkg.checkpoint.load_midgroup_linear(out, base, K=2049, device=dev)
+    xb = pkg.synth.activations(7, 2049, seed=4)
+    y = m(bf16_bits_tensor(xb).to(dev))
+    torch.cuda.synchronize()
+    codes, sc, zr, _ = ow.quantize_weight_asym(w.to(torch.bfloat16).float().numpy(), 1024)
+    q, s = ow.quant_act_midgroup(xb, 1024)
+    y32, mag = ow.gemm_midgroup_fp32(q, s, codes, sc, zr, 1024, return_abs=True)
+    check_output(tensor_bf16_bits(y), y32, mag, 3, "mg_kgeom_v1 linear")

@@ -94,3 +94,50 @@ def test_midgroup_fake_kernels_give_shapes(pkg):
         gn = torch.empty((2, 256), dtype=torch.bfloat16, device="cuda")
         y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_s, a_k, w_q, gn, gn.int(), gn, 1057)
         assert y.shape == (16, 256) and y.dtype == torch.bfloat16
+
+
+
+def _vendor_pack_n(codes: torch.Tensor) -> torch.Tensor:
+    """Test-side packer: two int4 per byte along N, low nibble = even row."""
+    c = codes.to(torch.int16) & 0xF
+    return (c[0::2] | (c[1::2] << 4)).to(torch.uint8).view(torch.int8)
+
+
+def test_vendor_w4a8_dynamic_conversion(pkg):
+    g = torch.Generator().manual_seed(7)
+    N, K, G = 64, 512, 128
+    codes = torch.randint(-8, 8, (N, K), dtype=torch.int8, generator=g)
+    s2 = (torch.rand((N, K // G), generator=g) * 0.01 + 0.001).to(torch.float16)
+    base = "model.layers.0.mlp.down_proj"
+    t = {f"{base}.weight": _vendor_pack_n(codes), f"{base}.weight_scale": torch.full((N, 1), 2.0),
+         f"{base}.weight_offset": torch.zeros((N, 1)), f"{base}.weight_scale_second": s2,
+         f"{base}.weight_offset_second": torch.zeros((N, K // G), dtype=torch.float16),
+         f"{base}.scale_bias": torch.zeros((N, 16))}
+    assert torch.equal(pkg.checkpoint.vendor_unpack_n(t[f"{base}.weight"]), codes)
+    w_q, w_scale, n, k = pkg.checkpoint.vendor_to_grouped(t, base, G)
+    assert (n, k) == (N, K)
+    assert torch.equal(pkg.packing.unpack_int4(w_q), codes)
+    assert torch.equal(w_scale, (2.0 * s2.float()).to(torch.float16).T)
+    t[f"{base}.weight_offset"] = torch.ones((N, 1))
+    with pytest.raises(ValueError, match="weight_offset"):
+        pkg.checkpoint.vendor_to_grouped(t, base, G)
+
+
+def test_midgroup_export_and_load_roundtrip(pkg, tmp_path):
+    g = torch.Generator().manual_seed(8)
+    src = {"model.layers.0.self_attn.o_proj.weight": torch.randn((96, 1057), generator=g) * 0.05,
+           "model.norm.weight": torch.ones(1057)}
+    out = pkg.checkpoint.export_midgroup(src, 1024)
+    base = "model.layers.0.self_attn.o_proj"
+    assert set(out) == {f"{base}.{s}" for s in pkg.checkpoint.MIDGROUP_SUFFIXES} | {"model.norm.weight"}
+    wq, ws, wk, wz = pkg.packing.quantize_weight_asym(src[f"{base}.weight"].to(torch.bfloat16), 1024)
+    assert torch.equal(out[f"{base}.weight_packed"], wq) and torch.equal(out[f"{base}.weight_scale"], ws.T)
+    assert out[f"{base}.weight_ksum"].shape == (96, 2) and out[f"{base}.weight_zero"].dtype == torch.bfloat16
+    from safetensors.torch import save_file
+    save_file(out, str(tmp_path / "model-00001.safetensors"), metadata={"format": "pt"})
+    out = pkg.checkpoint.load_safetensors(str(tmp_path / "model-00001.safetensors"))
+    m = pkg.checkpoint.load_midgroup_linear(out, base, K=1057, device="cpu")
+    assert torch.equal(m.weight_packed, wq) and torch.equal(m._gn[0], ws)
+    with pytest.raises(ValueError):
+        pkg.checkpoint.load_midgroup_linear(out, base, K=1100, device="cpu")
+    assert pkg.checkpoint.quant_config(1024)["packed_layout"] == "mg_kgeom_v1"
