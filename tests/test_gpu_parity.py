@@ -165,6 +165,9 @@ GEMM_CASES = [
     (2, 160, 2560, 640, "bf16"),     # decode, 10 slabs per group (not a power-of-two multiple of 128)
     (5, 96, 3072, 256, "f16"),       # decode, two tiles per group
     (64, 7168, 5120, 128, "f16"),    # qkv decode, M=64
+    (17, 336, 1536, 192, "f16"),     # two 16-row groups, the second with one row; 11 column groups
+    (40, 1000, 2048, 64, "bf16"),    # three row groups, ragged N
+    (50, 200, 3072, 320, "f16"),     # row groups with groups ending on either slab
     (65, 384, 1024, 128, "bf16"),    # first prefill-path M
     (128, 256, 1024, 1024, "f16"),
     (300, 1000, 2048, 128, "bf16"),  # ragged M and N tiles

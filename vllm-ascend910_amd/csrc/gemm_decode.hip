@@ -50,6 +50,8 @@ struct DecodeParams {
     int gshift;        // GM 1: log2(tiles per group)
     int unit;          // tiles per K-split unit (group and tile aligned)
     int units;         // ceil(KT / unit)
+    int cgroups;       // column groups (workgroups per row group)
+    int rgroups;       // row groups of 16 * MT rows
     uint32_t a_bytes, w_bytes, s_bytes;
 };
 
@@ -83,10 +85,25 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kw = blockDim.x >> 6;
     constexpr int CG = SWIGLU ? CPW / 2 : CPW;   // column blocks per output group
-    const int nb0 = blockIdx.x * CG;
+    // Workgroup -> (column group, row group).  With several row groups the
+    // ones that share a column group get consecutive ids of one XCD (ids are
+    // dispatched round-robin over the 8 XCDs), so they run together and read
+    // the weights through the same L2; ids past the column groups exit.
+    int cgi = static_cast<int>(blockIdx.x), rgi = 0;
+    if (p.rgroups > 1) {
+        const int i = static_cast<int>(blockIdx.x) >> 3;
+        const int j = i / p.rgroups;
+        cgi = (j << 3) + static_cast<int>(blockIdx.x & 7);
+        rgi = i - j * p.rgroups;
+        if (cgi >= p.cgroups) return;
+    }
+    const int nb0 = cgi * CG;
     auto block_of = [&](int c) { return (SWIGLU && c >= CG) ? nb0 + (c - CG) + p.up_nb : nb0 + c; };
     const int rowq = 4 * (lane >> 4);  // first output row of this lane in a 16-row tile
     const int colq = lane & 15;        // A row / output column of this lane in a 16-block
+    // Rows [m0, m0 + R) of the activations (more than R rows are split over
+    // row groups that share the column blocks).
+    const int m0 = rgi * R;
 
     // This wave's tile range [ta, tb).
     const int ua = (wave * p.units) / kw;
@@ -108,7 +125,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         // rows past M start past the buffer end; a slab past K meets zero weights
-        const uint32_t row = static_cast<uint32_t>(mt * 16 + colq);
+        const uint32_t row = static_cast<uint32_t>(m0 + mt * 16 + colq);
         const uint32_t o = row < static_cast<uint32_t>(p.M) ? row * static_cast<uint32_t>(p.lda) + (lane >> 4) * 16u : kOOB;
         ao[mt][0] = o;         // slab 0 of tile 0
         ao[mt][1] = o + 64u;   // slab 1 (kOOB + 64 stays out of range)
@@ -178,7 +195,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
                     const int col = block_of(c) * 16 + colq;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int row = mt * 16 + rowq + i;
+                        const int row = m0 + mt * 16 + rowq + i;
                         if (own && row < p.M && col < p.N && g < p.NG)
                             p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[mt][c][i] >> 4;
                     }
@@ -263,24 +280,24 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
             const int row = e / CH;
             const int cc = e - row * CH;
             const int col = nb0 * 16 + cc;
-            if (row >= p.M || col >= p.up_nb * 16) continue;
+            if (m0 + row >= p.M || col >= p.up_nb * 16) continue;
             float sg = red[row * C + cc], su = red[row * C + CH + cc];
             for (int w = 1; w < kw; ++w) {
                 sg += red[w * R * C + row * C + cc];
                 su += red[w * R * C + row * C + CH + cc];
             }
-            const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
-            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(swiglu_bf16_bits(sg * ts, su * ts));
+            const float ts = bf16_bits_to_f32(p.a_scale[m0 + row]) * 0.0625f;
+            p.Y[static_cast<int64_t>(m0 + row) * p.ldy + col] = static_cast<uint16_t>(swiglu_bf16_bits(sg * ts, su * ts));
         }
     } else {
         for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
             const int row = e / C;
             const int col = nb0 * 16 + (e - row * C);
-            if (row >= p.M || col >= p.N) continue;
+            if (m0 + row >= p.M || col >= p.N) continue;
             float sum = red[e];
             for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
-            const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
-            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
+            const float ts = bf16_bits_to_f32(p.a_scale[m0 + row]) * 0.0625f;
+            p.Y[static_cast<int64_t>(m0 + row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
         }
     }
 }
@@ -309,10 +326,14 @@ hipError_t launch_g(const DecodeParams& p, int kw, bool sbf16, hipStream_t strea
         const int w = std::max(1, std::min(kw, KWM));
         constexpr int CG = SWIGLU ? CPW / 2 : CPW;
         const int nbg = SWIGLU ? p.up_nb : p.NB;
-        const dim3 grid(static_cast<unsigned>((nbg + CG - 1) / CG)), block(64 * w);
+        DecodeParams q = p;
+        q.cgroups = (nbg + CG - 1) / CG;
+        q.rgroups = (p.M + 16 * MT - 1) / (16 * MT);
+        const int64_t nwg = q.rgroups > 1 ? int64_t{8} * ((q.cgroups + 7) / 8) * q.rgroups : q.cgroups;
+        const dim3 grid(static_cast<unsigned>(nwg)), block(64 * w);
         const size_t lds = static_cast<size_t>(w) * 16 * MT * 16 * CPW * sizeof(float);
-        if (sbf16) gemm_decode_kernel<MT, CPW, KWM, D, GM, true, DUMP, SWIGLU><<<grid, block, lds, stream>>>(p);
-        else gemm_decode_kernel<MT, CPW, KWM, D, GM, false, DUMP, SWIGLU><<<grid, block, lds, stream>>>(p);
+        if (sbf16) gemm_decode_kernel<MT, CPW, KWM, D, GM, true, DUMP, SWIGLU><<<grid, block, lds, stream>>>(q);
+        else gemm_decode_kernel<MT, CPW, KWM, D, GM, false, DUMP, SWIGLU><<<grid, block, lds, stream>>>(q);
         return hipGetLastError();
     }
 }
@@ -340,7 +361,8 @@ hipError_t launch_v(const DecodeParams& p, int kw, bool sbf16, hipStream_t strea
 // even CPW.
 template <int MODE>
 hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool sbf16, hipStream_t s) {
-    const int mt = (p.M + 15) / 16;
+    // c.MT > 0: workgroups of 16 * c.MT rows, gridDim.y of them
+    const int mt = c.MT > 0 ? std::min(c.MT, (p.M + 15) / 16) : (p.M + 15) / 16;
     if constexpr (MODE != 2) {
         if (mt == 1 && c.D == 8 && c.CPW == 1) return launch_v<1, 1, 8, MODE>(p, c.KW, sbf16, s);
         if (mt == 1 && c.D == 4 && c.CPW == 1) return launch_v<1, 1, 4, MODE>(p, c.KW, sbf16, s);
@@ -398,21 +420,21 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int64_t NB = geom::col_blocks(N);
     DecodeConfig c{4, 2, 4};
     const int64_t wgs = (NB + 1) / 2;
-    if (mt <= 2) {
-        // Wide N already gives >= 1024 workgroups; otherwise split K so that
-        // each wave holds about one ring (4 tiles) of its range -- but long K
-        // (>= 128 tiles) streams better with fewer, longer waves the more
-        // activation rows ride along.
-        if (wgs >= 1024) {
-            c.KW = M <= 2 ? 2 : 1;
-        } else {
-            const int cap = KT >= 128 ? (M <= 1 ? 8 : (M <= 4 ? 6 : 4)) : (mt == 1 ? 12 : 8);
-            c.KW = std::max(1, std::min(cap, (KT + 3) / 4));
-        }
-    } else if (wgs >= 1024) {
-        c = DecodeConfig{2, 4, 1};
+    if (wgs >= 1024) {
+        // Wide N already gives >= 1024 workgroups of all rows.
+        if (mt <= 2) c.KW = M <= 2 ? 2 : 1;
+        else c = DecodeConfig{2, 4, 1};
+    } else if (mt == 1 || (mt == 2 && KT >= 128)) {
+        // Split K so that each wave holds about one ring (4 tiles) of its
+        // range -- but long K (>= 128 tiles) streams better with fewer, longer
+        // waves the more activation rows ride along.
+        const int cap = KT >= 128 ? (M <= 1 ? 8 : (M <= 4 ? 6 : 4)) : 12;
+        c.KW = std::max(1, std::min(cap, (KT + 3) / 4));
     } else {
-        c.KW = KT >= 128 ? 3 : 2;
+        // More than 16 rows on narrow N: 16-row workgroups (row groups that
+        // share each column group) of two waves, which keeps every wave's
+        // MFMA, fold and load work per tile small and puts more waves in flight.
+        c = DecodeConfig{4, 2, 2, 1};
     }
     return c;
 }

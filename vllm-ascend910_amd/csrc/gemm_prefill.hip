@@ -220,6 +220,24 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         load_a(kt + 2, ra[u & 1]);
         uint32_t scn[2][NSC];
         load_s(kt + 1, scn);
+        // A operands from LDS two slabs at a time: slabs 0-1 now (their
+        // latency hides behind the weight unpack), slabs 2-3 before slab 1's
+        // MFMAs.  The scheduling barrier keeps the first reads ahead of the
+        // unpack; reading slab by slab right before each MFMA pair exposes
+        // the LDS latency eight times per step.  Group stride 64 (a fold in
+        // mid-step) and the partial dump need those registers and read per
+        // slab.
+        constexpr bool PAIRS = GMODE != 0 && !DUMP;
+        const int8_t* ab = abase + buf * (kBM * kLS);
+        auto lds_a = [&](int rb, int s) { return *reinterpret_cast<const v4i*>(ab + rb * 32 * kLS + s * 32); };
+        v4i avs[4][2];
+        if constexpr (PAIRS) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) avs[s][rb] = lds_a(rb, s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         v4i bvs[4][2];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
@@ -231,8 +249,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
                 bvs[s][j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
             }
         load_w(u, kt + DW);
-        const int8_t* ab = abase + buf * (kBM * kLS);
-        auto lds_a = [&](int rb, int s) { return *reinterpret_cast<const v4i*>(ab + rb * 32 * kLS + s * 32); };
 
         // Slab-major: the four blocks' MFMA chains interleave, so no MFMA waits
         // on its predecessor's result.  A group ends after slab 1 or 3 (fixed
@@ -249,9 +265,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const bool fresh = GMODE == 0 ? (s == 0 || s == 2) : (GMODE == 1 && s == 0);
+            if (PAIRS && s == 1) {
+#pragma unroll
+                for (int s2 = 2; s2 < 4; ++s2)
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb) avs[s2][rb] = lds_a(rb, s2);
+            }
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
-                const v4i av = lds_a(rb, s);
+                const v4i av = PAIRS ? avs[s][rb] : lds_a(rb, s);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) P[rb][j] = mfma32(av, bvs[s][j], fresh ? zero16 : P[rb][j]);
             }

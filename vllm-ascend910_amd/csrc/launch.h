@@ -48,6 +48,7 @@ struct DecodeConfig {
     int D;
     int CPW;
     int KW;
+    int MT = 0;   // 16-row tiles per workgroup; 0 = all rows in one workgroup
 };
 DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream);
