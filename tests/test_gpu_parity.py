@@ -111,6 +111,25 @@ def test_quant_ties_zero_rows_and_strided_input(dev):
     assert torch.equal(a_q2, a_q) and torch.equal(a_s2, a_s)
 
 
+@pytest.mark.parametrize("K", [512, 27648])
+def test_quant_tiny_and_boundary_scales(pkg, dev, K):
+    """Rows whose scale is subnormal, at the 2^-125 edge of the reciprocal path,
+    or whose elements are subnormal: byte-exact against the oracle's divide."""
+    say(f"quant tiny scales K={K}")
+    rng = np.random.default_rng(K)
+    amaxes = [1e-30, 2.0 ** -118, 2.0 ** -118 * 0.99, 127 * 2.0 ** -125, 1e-37, 3e-39, 1.0, 3e4]
+    rows = []
+    for a in amaxes:
+        v = rng.standard_normal(K).astype(np.float32)
+        v *= np.float32(a) / np.abs(v).max()
+        rows.append(ow.f32_to_bf16_bits(v))
+    xb = np.stack(rows)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xb).to(dev))
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    assert np.array_equal(tensor_bf16_bits(a_s), s_ref)
+    assert np.array_equal(a_q.cpu().numpy(), q_ref)
+
+
 def test_quant_empty(dev):
     a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(torch.empty((0, 256), dtype=torch.bfloat16, device=dev))
     assert a_q.shape == (0, 256) and a_s.shape == (0,)
@@ -240,7 +259,7 @@ def test_gemm_ragged_k(pkg, dev, M, N, K, G, sd):
 
 
 @pytest.mark.parametrize("K,G", [(1057, 1024), (100, 33), (1057, 96), (3456, 1024), (5000, 128), (35, 1024),
-                                 (1, 1024), (1001, 100)])
+                                 (1, 1024), (1001, 100), (20000, 1000)])
 def test_quant_padded_layout_byte_exact(pkg, dev, K, G):
     """Vector path (K % 8 == 0 and group % 8 == 0) and scalar path alike write
     the padded group layout with zeroed padding."""

@@ -128,6 +128,43 @@ def test_quant_tie_rows_match_rational_and_catch_reciprocal_multiply():
     assert not np.array_equal(q_bad, q)
 
 
+def reciprocal_quant(xf: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """numpy model of the GPU quantiser's arithmetic for a normal scale s:
+    t = rint(fp32(x * fp32(1/s))), the exact residual d = x - t*s (an fma on the
+    GPU, exact float64 here), and at |d| == s/2 the even neighbour."""
+    s = s.astype(np.float32)
+    r = (np.float32(1.0) / s).astype(np.float32)
+    t = np.rint((xf * r).astype(np.float32)).astype(np.float64)
+    d = xf.astype(np.float64) - t * s.astype(np.float64)
+    tie = (np.abs(d) == 0.5 * s.astype(np.float64)) & (np.mod(t, 2) != 0)
+    t = np.where(tie, t + np.sign(d), t)
+    return np.clip(t, -128, 127).astype(np.int8)
+
+
+def test_reciprocal_quant_equals_divide_exhaustively():
+    """The reciprocal-plus-half-way-test quantiser gives the IEEE divide's codes for
+    every bf16 x with |x| <= 127.25 s, every bf16 significand of s, at three scale
+    exponents (large, mid, and near the 2^-125 lower limit of that path), and on the
+    half-way tie rows where a bare reciprocal multiply fails."""
+    allx = ow.bf16_bits_to_f32(np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16))
+    allx = allx[np.isfinite(allx)]
+    bare_misses = 0
+    for e in (20, -40, -118):
+        for m in range(128, 256):
+            s = np.float32(m * 2.0 ** (e - 7))
+            x = allx[np.abs(allx) <= np.float32(127.25) * s]
+            div = np.clip(np.rint((x / s).astype(np.float32)), -128, 127).astype(np.int8)
+            assert np.array_equal(reciprocal_quant(x, np.full_like(x, s)), div), (e, m)
+            bare = np.clip(np.rint((x * (np.float32(1.0) / s)).astype(np.float32)), -128, 127).astype(np.int8)
+            bare_misses += int(np.count_nonzero(bare != div))
+    assert bare_misses > 0   # the half-way test is what makes the difference
+    from conftest import tie_rows
+    xb = tie_rows(48, 128, seed=4)
+    q, sb = ow.quant_act_per_token(xb)
+    sf = np.repeat(ow.bf16_bits_to_f32(sb)[:, None], 128, 1)
+    assert np.array_equal(reciprocal_quant(ow.bf16_bits_to_f32(xb), sf), q)
+
+
 # --------------------------------------------------------------- packing / geometry
 RAGGED_CASES = [(5120, 128), (27648, 128), (1057, 128), (1279, 256), (1025, 1024), (33, 64), (1, 64), (65, 64),
                 (63, 64), (2049, 512), (1023, 1024), (35, 32), (777, 96), (100, 33), (4096, 64)]

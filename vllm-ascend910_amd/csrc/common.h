@@ -81,6 +81,46 @@ __device__ __forceinline__ float scale_to_f32(uint32_t bits) {
     else return f16_bits_to_f32(bits);
 }
 
+// Per-token int8 quant of one element: clamp(rint(x / s), -128, 127) with
+// rint = round half to even and the IEEE fp32 quotient.
+__device__ __forceinline__ int quant_div(float x, float s) {
+    float q = rintf(x / s);
+    q = fminf(127.0f, fmaxf(-128.0f, q));
+    return static_cast<int>(q);
+}
+
+// The row's scale, its reciprocal and half of it.  With s normal (>= 2^-125
+// here) and |x| <= 127.25 s (s = bf16(amax / 127) is at least amax / 127
+// less one bf16 rounding), y = x * (1/s) lies within 2^-16 of the exact x/s,
+// and x/s -- a ratio of two 8-bit significands -- is either a half-integer or
+// at least 2^-10 from every half-integer.  So rint(y) is rint(x/s) except at
+// exact half-way cases, where the residual x - t*s (exact in an fma) is
+// +-s/2 and the even neighbour is taken.  Other scales (subnormal, infinite,
+// NaN) divide per element.
+struct RowScale {
+    float s, r, hs;
+    bool fast;
+};
+
+__device__ __forceinline__ RowScale row_scale(float s) {
+    RowScale q;
+    q.s = s;
+    q.fast = s >= 0x1p-125f && s <= 3.0e38f;
+    q.r = 1.0f / s;
+    q.hs = 0.5f * s;
+    return q;
+}
+
+template <bool FAST>
+__device__ __forceinline__ int quant_code(float x, const RowScale& q) {
+    if constexpr (!FAST) return quant_div(x, q.s);
+    const float t = rintf(x * q.r);
+    const float d = fmaf(-t, q.s, x);
+    int v = static_cast<int>(t);
+    if (fabsf(d) == q.hs && (v & 1)) v += d > 0.0f ? 1 : -1;
+    return min(127, max(-128, v));
+}
+
 // One packed dword of the repacked weight holds 8 int4 codes: byte j carries
 // code k+j in its low nibble and code k+4+j in its high nibble.  Moving each
 // nibble into the HIGH half of a byte gives int8 lanes equal to 16*code, with

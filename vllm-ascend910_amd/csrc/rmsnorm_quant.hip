@@ -12,6 +12,8 @@
 // vectorised mean, which moves r by at most an fp32 ulp.  Optionally writes s
 // (the updated residual stream) and h.  One workgroup per row, the row held in
 // registers (256 threads up to 8192 elements, 1024 threads up to 65536).
+#include <type_traits>
+
 #include "common.h"
 #include "kgeom.h"
 #include "launch.h"
@@ -67,11 +69,6 @@ __device__ __forceinline__ uint32_t block_max_u(uint32_t v, uint32_t* red) {
     return m;
 }
 
-__device__ __forceinline__ int quant1r(float x, float s) {
-    float q = rintf(x / s);
-    q = fminf(127.0f, fmaxf(-128.0f, q));
-    return static_cast<int>(q);
-}
 
 // VPT units of 8 elements per thread; K % 8 == 0, rows 16-byte aligned.
 template <int VPT, int NT, bool RES>
@@ -141,32 +138,38 @@ __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const RmsParams p) {
     amax = block_max_u<NT>(amax, redu);
     uint32_t sbits = f32_to_bf16_bits(bf16_bits_to_f32(amax) / 127.0f);
     if ((sbits & 0x7fffu) == 0u) sbits = kTinyRN;
-    const float sc = bf16_bits_to_f32(sbits);
+    const RowScale sc = row_scale(bf16_bits_to_f32(sbits));
     if (threadIdx.x == 0) p.a_scale[row] = static_cast<uint16_t>(sbits);
     int8_t* qr = p.a_q + row * p.lda;
+    // one uniform branch per row between the reciprocal and divide paths
+    auto emit = [&](auto fast) __attribute__((always_inline)) {
+        constexpr bool F = decltype(fast)::value;
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int idx = static_cast<int>(threadIdx.x) + i * NT;
-        if (idx >= nvec) continue;
-        const uint32_t* pa = reinterpret_cast<const uint32_t*>(&v[i]);
-        uint2 o;
-        uint32_t wd[2] = {0u, 0u};
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + i * NT;
+            if (idx >= nvec) continue;
+            const uint32_t* pa = reinterpret_cast<const uint32_t*>(&v[i]);
+            uint2 o;
+            uint32_t wd[2] = {0u, 0u};
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const int q0 = quant1r(__uint_as_float(pa[d] << 16), sc);
-            const int q1 = quant1r(__uint_as_float(pa[d] & 0xffff0000u), sc);
-            wd[d >> 1] |= ((static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8))
-                          << (16 * (d & 1));
+            for (int d = 0; d < 4; ++d) {
+                const int q0 = quant_code<F>(__uint_as_float(pa[d] << 16), sc);
+                const int q1 = quant_code<F>(__uint_as_float(pa[d] & 0xffff0000u), sc);
+                wd[d >> 1] |= ((static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8))
+                              << (16 * (d & 1));
+            }
+            o.x = wd[0];
+            o.y = wd[1];
+            int k0 = idx * 8;
+            if (p.pad) {
+                const int g = k0 / p.group;
+                k0 = g * p.stride + (k0 - g * p.group);
+            }
+            *reinterpret_cast<uint2*>(qr + k0) = o;
         }
-        o.x = wd[0];
-        o.y = wd[1];
-        int k0 = idx * 8;
-        if (p.pad) {
-            const int g = k0 / p.group;
-            k0 = g * p.stride + (k0 - g * p.group);
-        }
-        *reinterpret_cast<uint2*>(qr + k0) = o;
-    }
+    };
+    if (sc.fast) emit(std::true_type{});
+    else emit(std::false_type{});
     if (p.pad) {
         // zero the padding slots (real lengths are multiples of 8 here)
         const int kp = static_cast<int>(geom::kpad(p.K, p.group));
