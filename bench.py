@@ -151,8 +151,8 @@ def main():
             for p in PROJS:
                 K, N = synth.QWQ_SHAPES[p]
                 wt, st = weights[p][(len(DECODE_MS) * r + mi) % len(weights[p])]
-                a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(xs[(M, p)])
-                outs.append(torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP))
+                # quant + GEMM (one fused launch where w4a8_linear qualifies)
+                outs.append(torch.ops.npu.w4a8_linear(xs[(M, p)], wt, st, N, K, GROUP))
         return outs
 
     if args.pmc_probe:
@@ -267,16 +267,25 @@ def main():
                 for _ in range(T):
                     torch.ops.npu.w4a8_quant_pertoken(xs[(M, p)])
 
+            def linears(M=M, p=p, K=K, N=N):
+                for i in range(T):
+                    wt, st = weights[p][i % len(weights[p])]
+                    torch.ops.npu.w4a8_linear(xs[(M, p)], wt, st, N, K, GROUP)
+
             us = time_graph(gemms) / T
             qus = time_graph(quants) / T
+            lus = time_graph(linears) / T
+            x0 = xs[(M, p)]
+            fused = bool(pkg._abi.lib().w4a8_linear_fused(x0.data_ptr(), x0.stride(0), M, N, K, GROUP))
             b = gemm_bytes(M, N, K)
             tot_bytes += b
             tot_us += us
             shapes.append({"proj": p, "M": M, "N": N, "K": K, "gemm_us": round(us, 3),
                            "gemm_GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                           "TOPS": round(2 * M * N * K / us / 1e6, 2), "quant_us": round(qus, 3)})
+                           "TOPS": round(2 * M * N * K / us / 1e6, 2), "quant_us": round(qus, 3),
+                           "linear_us": round(lus, 3), "linear_fused": fused})
             log(f"  {p:13s} M={M:3d}: gemm {us:8.2f} us {b / us / 1e3:7.1f} GB/s ({b / us / 1e3 / HBM_PEAK_GBS:.1%})"
-                f"  quant {qus:6.2f} us")
+                f"  quant {qus:6.2f} us  linear {lus:7.2f} us{' (fused)' if fused else ''}")
     achieved = tot_bytes / tot_us / 1e3
     # HBM bytes per launch from the two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) recorded in
     # profiles/ (the command is in the summary), each scaled by a 256 MiB copy's reading.

@@ -136,6 +136,31 @@ int w4a8_gemm_swiglu(const void* a_q, int64_t lda, const void* a_scale, const vo
                      int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The whole W4A8 dynamic linear: per-token quant of bf16 x, then the GEMM,
+ *   x        bf16 [M, ldx], ldx >= K, 2-byte aligned
+ *   a_q      int8 [M, lda], a_scale bf16 [M]   receive the quantised
+ *            activations (as w4a8_quant_act with this group writes them)
+ *   the other arguments as for w4a8_gemm.
+ * Results are those of w4a8_quant_act followed by w4a8_gemm, bit for bit.
+ * For a single row (M == 1) on narrow N with an unpadded K (and x 16-byte
+ * aligned, ldx % 8 == 0) the quant runs inside the GEMM kernel, one launch
+ * instead of two.
+ * Replaces the reference linear method's quant-then-GEMM pair
+ * (npu_ops/python/midgroup_quant.py:163-177, apply: midgroup_quant_a then
+ * midgroup_w4a8_gemm) for the per-token symmetric path.
+ */
+int w4a8_linear(const void* x, int64_t ldx, const void* w_tiles, const void* s_tiles, int scale_dtype,
+                void* y, int64_t ldy, void* a_q, int64_t lda, void* a_scale, int64_t M, int64_t N,
+                int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * 1 when w4a8_linear with these arguments runs as one fused launch, 0 when it
+ * runs the quant and GEMM kernels (no counterpart in the reference: a query
+ * for tests and schedulers; x is only inspected for alignment).
+ */
+int w4a8_linear_fused(const void* x, int64_t ldx, int64_t M, int64_t N, int64_t K, int64_t group);
+
+/*
  * Parity hook: the same GEMM, which also writes every per-group int32 partial
  *   partials int32 [G, M, N],  partials[g][m][n] = P_g[m,n]
  * from the production kernel's own accumulators.  The reference computes the

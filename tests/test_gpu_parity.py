@@ -356,6 +356,87 @@ def test_w4a8_linear_module(pkg, dev):
     assert np.max(np.abs(got - y_ref) - 2 * ow.bf16_ulp(y_ref)) <= 0
 
 
+# w4a8_linear: quant + GEMM, fused into one kernel for small batches on narrow N.
+LINEAR_CASES = [
+    # (M, N, K, G, scale dtype, note)
+    (1, 7168, 5120, 128, "f16", "fused: qkv"),
+    (4, 5120, 5120, 128, "bf16", "two-kernel: o, four rows"),
+    (1, 5120, 5120, 128, "bf16", "fused: o"),
+    (2, 1024, 4096, 128, "bf16", "two-kernel: two rows"),
+    (1, 5120, 27648, 128, "f16", "fused: down, seven chunks per lane"),
+    (2, 5120, 27648, 128, "f16", "two-kernel: down, two rows"),
+    (1, 640, 4096, 64, "bf16", "fused: group stride 64"),
+    (1, 320, 6144, 512, "f16", "fused: groups of 4 tiles"),
+    (1, 480, 3200, 320, "bf16", "fused: groups ending on either slab"),
+    (1, 96, 1024, 1024, "f16", "fused: one group, one column group"),
+    (5, 512, 2048, 128, "f16", "two-kernel: five rows"),
+    (1, 55296, 1024, 128, "bf16", "two-kernel: wide N"),
+    (3, 256, 1057, 1024, "f16", "two-kernel: ragged K"),
+]
+
+
+def run_linear_abi(pkg, dev, x, w_tiles, s_tiles, N, K, G):
+    """w4a8_linear through the C ABI: (y, a_q, a_scale)."""
+    M = x.shape[0]
+    width = ow.kpad(K, G)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    a_q = torch.full((M, width), 99, dtype=torch.int8, device=dev)
+    a_s = torch.empty((M,), dtype=torch.bfloat16, device=dev)
+    lib = pkg._abi.lib()
+    st = lib.w4a8_linear(x.data_ptr(), x.stride(0), w_tiles.data_ptr(), s_tiles.data_ptr(),
+                         1 if s_tiles.dtype == torch.bfloat16 else 0, y.data_ptr(), N, a_q.data_ptr(), width,
+                         a_s.data_ptr(), M, N, K, G, None, 0, torch.cuda.current_stream(dev).cuda_stream)
+    pkg._abi.check(st, "w4a8_linear")
+    torch.cuda.synchronize()
+    return y, a_q, a_s
+
+
+@pytest.mark.parametrize("M,N,K,G,sd,note", LINEAR_CASES)
+def test_linear_equals_quant_then_gemm(pkg, dev, M, N, K, G, sd, note):
+    """w4a8_linear == w4a8_quant_act + w4a8_gemm bit for bit (y, a_q, a_scale), and y
+    within the output bar of the oracle."""
+    say(f"linear M={M} N={N} K={K} G={G} ({note})")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M * 31 + K, scale_dtype=sd)
+    x = bf16_bits_tensor(xb).to(dev)
+    w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+    fused = pkg._abi.lib().w4a8_linear_fused(x.data_ptr(), x.stride(0), M, N, K, G)
+    assert fused == (1 if note.startswith("fused") else 0), f"path {fused} for '{note}'"
+    y, a_q, a_s = run_linear_abi(pkg, dev, x, w_tiles, s_tiles, N, K, G)
+    a_q2, a_s2 = torch.ops.npu.w4a8_quant_pertoken(x, G)
+    y2 = torch.ops.npu.w4a8_gemm(a_q2, a_s2, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    assert torch.equal(a_q, a_q2), "quantised activations differ"
+    assert np.array_equal(tensor_bf16_bits(a_s), tensor_bf16_bits(a_s2))
+    assert np.array_equal(tensor_bf16_bits(y), tensor_bf16_bits(y2)), "y differs from quant + gemm"
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, return_abs=True)
+    check_output(tensor_bf16_bits(y), y32, mag, ow.num_groups(K, G), f"linear {note}")
+    # the torch op: same result
+    y3 = torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    assert np.array_equal(tensor_bf16_bits(y3), tensor_bf16_bits(y))
+
+
+def test_linear_unaligned_and_strided_input(pkg, dev):
+    """x rows not 16-byte aligned or ldx % 8 != 0 take the two-kernel path; a row-strided
+    aligned x takes the fused one; the results are the same."""
+    say("linear strided / unaligned x")
+    M, N, K, G = 1, 1024, 2048, 128
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=5)
+    w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+    x = bf16_bits_tensor(xb).to(dev)
+    y_ref, _, _ = run_linear_abi(pkg, dev, x, w_tiles, s_tiles, N, K, G)
+    for off, ld, fused in ((0, K + 64, 1), (1, K + 64, 0), (0, K + 4, 0)):
+        big = torch.zeros((M, ld + 8), dtype=torch.bfloat16, device=dev)
+        big[:, off:off + K] = x
+        xv = big[:, off:off + K]
+        assert pkg._abi.lib().w4a8_linear_fused(xv.data_ptr(), xv.stride(0), M, N, K, G) == fused
+        y, _, _ = run_linear_abi(pkg, dev, xv, w_tiles, s_tiles, N, K, G)
+        assert np.array_equal(tensor_bf16_bits(y), tensor_bf16_bits(y_ref)), (off, ld)
+
+
 def test_workspace_reuse_across_shapes(pkg, dev):
     """Regression: consecutive split-K calls of different shapes share one
     workspace; a small-N call's partials must not leave non-zero counters for a

@@ -15,7 +15,7 @@ from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "_lib" / "libw4a8_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1
@@ -32,6 +32,8 @@ SIGNATURES = {
     "w4a8_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "w4a8_gemm": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
     "w4a8_gemm_swiglu": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
+    "w4a8_linear_fused": (_I, [_VP, _I64, _I64, _I64, _I64, _I64]),
+    "w4a8_linear": (_I, [_VP, _I64, _VP, _VP, _I, _VP, _I64, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
     "w4a8_midgroup_quant_a": (_I, [_VP, _I64, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP]),
     "w4a8_midgroup_gemm": (_I, [_VP, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
                                 _VP]),

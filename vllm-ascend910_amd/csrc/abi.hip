@@ -121,7 +121,7 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 2; }
+int w4a8_abi_version(void) { return 3; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
@@ -182,6 +182,54 @@ int w4a8_gemm_swiglu(const void* a_q, int64_t lda, const void* a_scale, const vo
                      int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream) {
     return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, nullptr, M, N, K, group,
                     workspace, workspace_bytes, stream, true);
+}
+
+int w4a8_linear(const void* x, int64_t ldx, const void* w_tiles, const void* s_tiles, int scale_dtype,
+                void* y, int64_t ldy, void* a_q, int64_t lda, void* a_scale, int64_t M, int64_t N,
+                int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (int rc = check_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, M, N, K, group, workspace,
+                            workspace_bytes, false))
+        return rc;
+    if (M == 0) return W4A8_OK;
+    if (!x) return fail(W4A8_ERR_NULL, "x is NULL");
+    if (ldx < K) return fail(W4A8_ERR_SHAPE, "ldx=%lld must be >= K=%lld", ldx, K);
+    if (!aligned(x, 2)) return fail(W4A8_ERR_ALIGN, "x must be 2-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    GemmArgs a{};
+    a.a_q = static_cast<const int8_t*>(a_q);
+    a.lda = lda;
+    a.a_scale = static_cast<const uint16_t*>(a_scale);
+    a.w_tiles = static_cast<const uint8_t*>(w_tiles);
+    a.s_tiles = static_cast<const uint16_t*>(s_tiles);
+    a.scale_bf16 = scale_dtype == W4A8_DT_BF16;
+    a.y = static_cast<uint16_t*>(y);
+    a.ldy = ldy;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.group = group;
+    const auto* xb = static_cast<const uint16_t*>(x);
+    if (linear_fusable(a, xb, ldx))
+        return hip_status(launch_linear_fused(a, xb, ldx, static_cast<int8_t*>(a_q), lda, static_cast<uint16_t*>(a_scale), s),
+                          "w4a8_linear launch");
+    if (int rc = hip_status(launch_quant_act(xb, ldx, static_cast<int8_t*>(a_q), lda, static_cast<uint16_t*>(a_scale),
+                                             M, K, group, s),
+                            "w4a8_linear quant launch"))
+        return rc;
+    return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, nullptr, M, N, K, group, workspace,
+                    workspace_bytes, stream);
+}
+
+int w4a8_linear_fused(const void* x, int64_t ldx, int64_t M, int64_t N, int64_t K, int64_t group) {
+    if (M <= 0 || N <= 0 || K <= 0 || group <= 0 || M >= (1ll << 31) || N >= (1ll << 30) || K >= (1ll << 30) ||
+        group >= (1ll << 30))
+        return 0;
+    GemmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.group = group;
+    return linear_fusable(a, static_cast<const uint16_t*>(x), ldx) ? 1 : 0;
 }
 
 int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,

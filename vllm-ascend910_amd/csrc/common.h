@@ -81,6 +81,26 @@ __device__ __forceinline__ float scale_to_f32(uint32_t bits) {
     else return f16_bits_to_f32(bits);
 }
 
+constexpr uint32_t kBf16Tiny = 0x0080u;  // 2^-126, torch.finfo(torch.bfloat16).tiny
+
+// Per-token activation quant helpers (quant_act.hip semantics): the absmax
+// of bf16 rows is reduced on the 15 magnitude bits as integers.
+__device__ __forceinline__ uint32_t abs_bits_max2(uint32_t u) {
+    return max(u & 0x7fffu, (u >> 16) & 0x7fffu);
+}
+
+// Scale from the absmax bits; returns bf16 bits of the stored scale.
+__device__ __forceinline__ uint32_t scale_from_amax(uint32_t amax_bits) {
+    const float amax = bf16_bits_to_f32(amax_bits);
+    uint32_t s = f32_to_bf16_bits(amax / 127.0f);
+    if ((s & 0x7fffu) == 0u) s = kBf16Tiny;
+    return s;
+}
+
+__device__ __forceinline__ uint32_t abs_bits_max8(const uint4& v) {
+    return max(max(abs_bits_max2(v.x), abs_bits_max2(v.y)), max(abs_bits_max2(v.z), abs_bits_max2(v.w)));
+}
+
 // Per-token int8 quant of one element: clamp(rint(x / s), -128, 127) with
 // rint = round half to even and the IEEE fp32 quotient.
 __device__ __forceinline__ int quant_div(float x, float s) {
@@ -119,6 +139,14 @@ __device__ __forceinline__ int quant_code(float x, const RowScale& q) {
     int v = static_cast<int>(t);
     if (fabsf(d) == q.hs && (v & 1)) v += d > 0.0f ? 1 : -1;
     return min(127, max(-128, v));
+}
+
+// Two bf16 in one dword -> two int8 codes in the low 16 bits.
+template <bool FAST>
+__device__ __forceinline__ uint32_t quant2(uint32_t u, const RowScale& q) {
+    const int q0 = quant_code<FAST>(__uint_as_float(u << 16), q);
+    const int q1 = quant_code<FAST>(__uint_as_float(u & 0xffff0000u), q);
+    return (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8);
 }
 
 // One packed dword of the repacked weight holds 8 int4 codes: byte j carries

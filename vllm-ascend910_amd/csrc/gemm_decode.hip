@@ -53,6 +53,16 @@ struct DecodeParams {
     int cgroups;       // column groups (workgroups per row group)
     int rgroups;       // row groups of 16 * MT rows
     uint32_t a_bytes, w_bytes, s_bytes;
+    // Fused activation quant (QM > 0): bf16 rows X [M, ldx] are quantised per
+    // token inside the kernel into LDS (row stride lrs bytes); the workgroup of
+    // column group 0 also writes a_q [M, lda_out] and a_scale [M].
+    const uint16_t* X;
+    int64_t ldx;
+    int8_t* aq_out;
+    int64_t lda_out;
+    uint16_t* as_out;
+    int lrs;
+    int qcpr;          // 16-byte X chunks per row per lane (<= 8 / QM)
 };
 
 // Offset that every buffer here treats as out of range (reads return zero).
@@ -71,12 +81,22 @@ constexpr uint32_t kOOB = 0x80000000u;
 // SWIGLU: the workgroup's first CPW/2 column blocks are gate blocks and the
 // rest the matching up blocks (output column n = silu(y[:, n]) * y[:, n + N/2]);
 // every column accumulates exactly as in the plain GEMM.
-template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP, bool SWIGLU>
+// QM > 0: the activation quant is fused (M <= QM <= 4, MT = 1, unpadded K;
+// the launcher builds QM = 1 only):
+// each wave loads the bf16 rows of its own K range, the waves' absmax meet in
+// LDS, and each wave quantises its range into an LDS copy of A (the per-token
+// arithmetic of quant_act.hip) that its MFMAs then read; the weight ring is
+// already in flight meanwhile.
+template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP, bool SWIGLU, int QM = 0>
 __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodeParams p) {
     static_assert(!SWIGLU || (CPW % 2 == 0 && !DUMP), "SwiGLU pairs column blocks and dumps nothing");
+    static_assert(QM == 0 || (MT == 1 && QM <= 4 && !DUMP && !SWIGLU), "the fused quant serves at most 4 rows");
     constexpr int R = 16 * MT;
     constexpr int C = 16 * CPW;
-    // kw * R * C floats, sized at launch for the waves actually launched.
+    constexpr bool QF = QM > 0;
+    // kw * R * C floats of reduction, sized at launch for the waves launched;
+    // with QF followed by the quantised rows, a 64-byte zero block, the
+    // waves' absmax and the rows' scale bits.
     extern __shared__ float red[];
 
     const int lane = threadIdx.x & 63;
@@ -114,6 +134,12 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     // Per-lane offsets are fixed for the whole K loop; the tile's uniform
     // offset goes into the descriptor base (make_rsrc_at).
     uint32_t wo[CPW], so[CPW], ao[MT][2];
+    // QF: LDS regions (byte offsets from red) and this lane's A row address
+    const int lq_a = kw * R * C * 4;
+    const int lq_z = lq_a + QM * p.lrs;
+    const int lq_m = lq_z + 64;
+    const int lq_s = lq_m + kw * 16;
+    char* const lds = reinterpret_cast<char*>(red);
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
         // a column block past NB (odd NB, last workgroup) re-reads the last
@@ -153,11 +179,21 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     uint4 ab[DA][MT][2];
     uint32_t sb[D][CPW][NS];
     auto load_a = [&](int sa, int t) {
-        const auto ra = make_rsrc_at(p.A, static_cast<uint32_t>(min(t, p.KT - 1)) * 128u, p.a_bytes);
+        if constexpr (QF) {
+            // rows past M read the zero block; tiles past the range re-read
+            // the range's last tile (their weights are zero)
+            const int tt = min(t, tb - 1);
+            const bool real = colq < p.M;
+            const char* base = lds + (real ? lq_a + colq * p.lrs + tt * 128 : lq_z) + (lane >> 4) * 16;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+            for (int h = 0; h < 2; ++h) ab[sa][0][h] = *reinterpret_cast<const uint4*>(base + (real ? h * 64 : 0));
+        } else {
+            const auto ra = make_rsrc_at(p.A, static_cast<uint32_t>(min(t, p.KT - 1)) * 128u, p.a_bytes);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) ab[sa][mt][h] = buf_load16(ra, ao[mt][h]);
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) ab[sa][mt][h] = buf_load16(ra, ao[mt][h]);
+        }
     };
     auto load_slot = [&](int s, int t) {
         // tiles past this wave's range read zero weights (an empty descriptor)
@@ -256,9 +292,82 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
         }
     };
 
-    if (tb > ta) {
+    const bool busy = tb > ta;
+    // QF: this wave's real K range [k0, k1) of X in 16-byte chunks
+    // c = lane + 64 i, loaded ahead of the weight ring (loads return in
+    // order, so the quant below waits for X only).
+    constexpr int QI = QF ? 8 / QM : 1;
+    constexpr int QR = QF ? QM : 1;
+    const int k0 = ta * 128, k1 = min(tb * 128, p.K);
+    const int nch = max(0, (k1 - k0) >> 3);
+    uint4 xv[QR][QI];
+    if constexpr (QF) {
+#pragma unroll
+        for (int m = 0; m < QM; ++m)
+#pragma unroll
+            for (int i = 0; i < QI; ++i) {
+                const int c = lane + 64 * i;
+                const bool ok = m < p.M && i < p.qcpr && c < nch;
+                xv[m][i] = ok ? *reinterpret_cast<const uint4*>(p.X + m * p.ldx + k0 + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+            }
+    }
+    if (busy) {
 #pragma unroll
         for (int s = 0; s < D; ++s) load_slot(s, ta + s);
+    }
+    if constexpr (QF) {
+        uint32_t am[QM];
+#pragma unroll
+        for (int m = 0; m < QM; ++m) {
+            am[m] = 0u;
+#pragma unroll
+            for (int i = 0; i < QI; ++i) am[m] = max(am[m], abs_bits_max8(xv[m][i]));
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1)
+                am[m] = max(am[m], static_cast<uint32_t>(__shfl_xor(static_cast<int>(am[m]), off, 64)));
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < QM; ++m) reinterpret_cast<uint32_t*>(lds + lq_m)[wave * 4 + m] = am[m];
+        }
+        if (wave == 0 && lane < 16) reinterpret_cast<uint32_t*>(lds + lq_z)[lane] = 0u;
+        __syncthreads();
+        const bool writer = cgi == 0 && rgi == 0;   // one workgroup emits a_q / a_scale
+#pragma unroll
+        for (int m = 0; m < QM; ++m) {
+            if (m >= p.M) break;
+            // lane w < kw reads wave w's absmax, then a wave-wide max
+            uint32_t amax = lane < kw ? reinterpret_cast<const uint32_t*>(lds + lq_m)[lane * 4 + m] : 0u;
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1)
+                amax = max(amax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(amax), off, 64)));
+            amax = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(amax)));
+            const uint32_t sbits = scale_from_amax(amax);
+            if (wave == 0 && lane == 0) {
+                reinterpret_cast<uint32_t*>(lds + lq_s)[m] = sbits;
+                if (writer) p.as_out[m] = static_cast<uint16_t>(sbits);
+            }
+            const RowScale q = row_scale(bf16_bits_to_f32(sbits));
+            auto emit = [&](auto fast) __attribute__((always_inline)) {
+                constexpr bool F = decltype(fast)::value;
+#pragma unroll
+                for (int i = 0; i < QI; ++i) {
+                    const int c = lane + 64 * i;
+                    if (i < p.qcpr && c < nch) {
+                        const uint4 v = xv[m][i];
+                        uint2 o;
+                        o.x = quant2<F>(v.x, q) | (quant2<F>(v.y, q) << 16);
+                        o.y = quant2<F>(v.z, q) | (quant2<F>(v.w, q) << 16);
+                        *reinterpret_cast<uint2*>(lds + lq_a + m * p.lrs + k0 + 8 * c) = o;
+                        if (writer) *reinterpret_cast<uint2*>(p.aq_out + m * p.lda_out + k0 + 8 * c) = o;
+                    }
+                }
+            };
+            if (q.fast) emit(std::true_type{});
+            else emit(std::false_type{});
+        }
+    }
+    if (busy) {
 #pragma unroll
         for (int s = 0; s < DA; ++s) load_a(s, ta + s);
         const int iters = (tb - ta + D - 1) / D;
@@ -296,7 +405,8 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
             if (m0 + row >= p.M || col >= p.N) continue;
             float sum = red[e];
             for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
-            const float ts = bf16_bits_to_f32(p.a_scale[m0 + row]) * 0.0625f;
+            const uint32_t tsb = QF ? reinterpret_cast<const uint32_t*>(lds + lq_s)[row] : p.a_scale[m0 + row];
+            const float ts = bf16_bits_to_f32(tsb) * 0.0625f;
             p.Y[static_cast<int64_t>(m0 + row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
         }
     }
@@ -408,7 +518,76 @@ DecodeParams make_params(const GemmArgs& a) {
     return p;
 }
 
+// Fused quant + GEMM: MT = 1, CPW = 2, D = 4, plain epilogue.
+template <int GM, bool SBF16, int QM>
+hipError_t launch_fused_g(const DecodeParams& p, int kw, size_t lds, hipStream_t stream) {
+    constexpr int KWM = kwmax_for(1, 2);
+    gemm_decode_kernel<1, 2, KWM, 4, GM, SBF16, false, false, QM>
+        <<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
+    return hipGetLastError();
+}
+
+template <int QM>
+hipError_t launch_fused_q(const DecodeParams& p, int kw, size_t lds, bool sbf16, hipStream_t s) {
+    switch (group_mode(p.spg)) {
+        case 0: return sbf16 ? launch_fused_g<0, true, QM>(p, kw, lds, s) : launch_fused_g<0, false, QM>(p, kw, lds, s);
+        case 1: return sbf16 ? launch_fused_g<1, true, QM>(p, kw, lds, s) : launch_fused_g<1, false, QM>(p, kw, lds, s);
+        case 3: return sbf16 ? launch_fused_g<3, true, QM>(p, kw, lds, s) : launch_fused_g<3, false, QM>(p, kw, lds, s);
+        default: return sbf16 ? launch_fused_g<2, true, QM>(p, kw, lds, s) : launch_fused_g<2, false, QM>(p, kw, lds, s);
+    }
+}
+
+// The fused plan for a problem, or false when the two-kernel path applies.
+struct FusedPlan {
+    DecodeParams p;
+    int kw, qm;
+    size_t lds;
+};
+
+bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f) {
+    // Small batches on narrow N only: each workgroup quantises all M rows of
+    // its K range, so the quant work is repeated per column group -- cheap
+    // for a few hundred workgroups, not for the thousands of a wide N.
+    // (Measured on MI355X: one row saves 0.5-3 us per call over the quant
+    // kernel + GEMM pair; at 2-4 rows the per-workgroup quant costs more
+    // than the launch it saves.)
+    if (a.M != 1 || a.swiglu || a.partials || !geom::is_unpadded(a.K, a.group)) return false;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx % 8 != 0) return false;
+    const DecodeConfig c = decode_config(a.M, a.N, a.K, a.group);
+    if (c.D != 4 || c.CPW != 2 || c.MT != 0) return false;
+    f.p = make_params(a);
+    f.p.cgroups = (f.p.NB + 1) / 2;
+    f.p.rgroups = 1;
+    if (f.p.cgroups >= 1024) return false;
+    f.kw = std::max(1, std::min(c.KW, kwmax_for(1, 2)));
+    f.qm = 1;
+    const int tiles = f.p.unit * ((f.p.units + f.kw - 1) / f.kw);   // most tiles a wave owns
+    f.p.qcpr = (tiles + 3) / 4;                                     // 16-byte chunks per row per lane
+    if (f.p.qcpr > 8 / f.qm) return false;
+    f.p.lrs = f.p.KT * 128 + 16;   // 16-byte skew: the rows' reads fall on different banks
+    f.lds = static_cast<size_t>(f.kw) * 16 * 32 * 4 + static_cast<size_t>(f.qm) * f.p.lrs + 64 + f.kw * 16 + 16;
+    if (f.lds > 64 * 1024) return false;
+    f.p.X = x;
+    f.p.ldx = ldx;
+    return true;
+}
+
 }  // namespace
+
+bool linear_fusable(const GemmArgs& a, const uint16_t* x, int64_t ldx) {
+    FusedPlan f;
+    return plan_fused(a, x, ldx, f);
+}
+
+hipError_t launch_linear_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t lda,
+                               uint16_t* a_scale, hipStream_t stream) {
+    FusedPlan f;
+    if (!plan_fused(a, x, ldx, f)) return hipErrorInvalidValue;
+    f.p.aq_out = a_q;
+    f.p.lda_out = lda;
+    f.p.as_out = a_scale;
+    return launch_fused_q<1>(f.p, f.kw, f.lds, a.scale_bf16, stream);
+}
 
 int64_t decode_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
 

@@ -53,6 +53,15 @@ struct DecodeConfig {
 DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream);
 
+// Fused per-token quant + decode GEMM for one row on narrow N (unpadded K,
+// x 16-byte aligned with ldx % 8 == 0, and the decode heuristic's 2-block,
+// 4-deep plan).  The workgroup of column group 0 also
+// writes a_q / a_scale.  launch_linear_fused returns hipErrorInvalidValue when
+// linear_fusable is false.
+bool linear_fusable(const GemmArgs& a, const uint16_t* x, int64_t ldx);
+hipError_t launch_linear_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t lda,
+                               uint16_t* a_scale, hipStream_t stream);
+
 // Prefill path (M > kDecodeMaxM): MFMA bound, LDS-tiled.
 int64_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);

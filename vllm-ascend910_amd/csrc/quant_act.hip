@@ -34,11 +34,6 @@ namespace w4a8 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr uint32_t kBf16Tiny = 0x0080u;  // 2^-126, torch.finfo(torch.bfloat16).tiny
-
-__device__ __forceinline__ uint32_t abs_bits_max2(uint32_t u) {
-    return max(u & 0x7fffu, (u >> 16) & 0x7fffu);
-}
 
 // Block-wide max of a uint32 over NT threads.
 template <int NT>
@@ -52,26 +47,6 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
 #pragma unroll
     for (int w = 1; w < NT / 64; ++w) v = max(v, red[w]);
     return v;
-}
-
-// Scale from the absmax bits; returns bf16 bits of the stored scale.
-__device__ __forceinline__ uint32_t scale_from_amax(uint32_t amax_bits) {
-    const float amax = bf16_bits_to_f32(amax_bits);
-    uint32_t s = f32_to_bf16_bits(amax / 127.0f);
-    if ((s & 0x7fffu) == 0u) s = kBf16Tiny;
-    return s;
-}
-
-// Two bf16 in one dword -> two int8 codes in the low 16 bits.
-template <bool FAST>
-__device__ __forceinline__ uint32_t quant2(uint32_t u, const RowScale& q) {
-    const int q0 = quant_code<FAST>(__uint_as_float(u << 16), q);
-    const int q1 = quant_code<FAST>(__uint_as_float(u & 0xffff0000u), q);
-    return (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8);
-}
-
-__device__ __forceinline__ uint32_t abs_bits_max8(const uint4& v) {
-    return max(max(abs_bits_max2(v.x), abs_bits_max2(v.y)), max(abs_bits_max2(v.z), abs_bits_max2(v.w)));
 }
 
 // Padded group layout of one row.

@@ -10,7 +10,7 @@ embeddings, RMSNorm) on this build's ops:
 * RMSNorm, the residual add and the activation quant run as one kernel
   (``torch.ops.npu.w4a8_rmsnorm_quant``) in front of qkv and gate_up;
 * gate_up runs with the fused SwiGLU epilogue (``w4a8_gemm_swiglu``);
-* o and down take ``w4a8_quant_pertoken`` activations;
+* o and down run ``w4a8_linear`` (quant + GEMM, one launch for a single row);
 * attention stays on PyTorch-ROCm in bf16, written with contiguous batched
   products only: the K cache is stored transposed ``[B, KVH, D, L]`` and the
   query heads of one KV head form the rows of one product, so grouped-query
@@ -74,6 +74,11 @@ class _Linear:
 
     def __call__(self, a_q: torch.Tensor, a_s: torch.Tensor) -> torch.Tensor:
         y = torch.ops.npu.w4a8_gemm(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+        return y + self.bias if self.bias is not None else y
+
+    def linear(self, x: torch.Tensor) -> torch.Tensor:
+        """quant + GEMM of bf16 x (one launch for a single row)."""
+        y = torch.ops.npu.w4a8_linear(x, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
         return y + self.bias if self.bias is not None else y
 
     def swiglu(self, a_q: torch.Tensor, a_s: torch.Tensor) -> torch.Tensor:
@@ -154,12 +159,10 @@ class W4A8Decoder:
     def _mlp_and_next(self, L: dict, s: torch.Tensor, a_attn: torch.Tensor):
         """o projection, residual, RMSNorm+quant, gate_up+SwiGLU, down; returns (stream, delta)."""
         c = self.cfg
-        aq, as_ = torch.ops.npu.w4a8_quant_pertoken(a_attn, c.group)
-        o = L["o"](aq, as_)
+        o = L["o"].linear(a_attn)
         aq2, as2, s2, _ = torch.ops.npu.w4a8_rmsnorm_quant(o, L["ln2"], c.rms_eps, s, c.group)
         h = L["gate_up"].swiglu(aq2, as2)
-        aq3, as3 = torch.ops.npu.w4a8_quant_pertoken(h, c.group)
-        return s2, L["down"](aq3, as3)
+        return s2, L["down"].linear(h)
 
     # ------------------------------------------------------------ prefill
     @torch.no_grad()

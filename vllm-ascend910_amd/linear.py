@@ -30,8 +30,7 @@ def linear(x: torch.Tensor, w_tiles: torch.Tensor, s_tiles: torch.Tensor, N: int
     """
     lead, K = x.shape[:-1], x.shape[-1]
     x2 = x.reshape(-1, K).to(torch.bfloat16).contiguous()
-    a_q, a_scale = torch.ops.npu.w4a8_quant_pertoken(x2, group)
-    y = torch.ops.npu.w4a8_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group)
+    y = torch.ops.npu.w4a8_linear(x2, w_tiles, s_tiles, N, K, group)
     if bias is not None:
         y = y + bias
     return y.reshape(*lead, N)

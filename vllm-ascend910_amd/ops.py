@@ -10,6 +10,7 @@ group-size-parameterised ops of this build:
     torch.ops.npu.w4a8_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> y
     torch.ops.npu.w4a8_gemm_partials(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> (y, partials)
     torch.ops.npu.w4a8_gemm_swiglu(a_q, a_scale, w_tiles, s_tiles, N, K, group) -> y [M, N/2]
+    torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, group) -> y   (quant + GEMM)
 
 and, with the reference's own names and schemas (group appended with the
 reference's fixed value as default), its mid-group compat pair:
@@ -44,6 +45,7 @@ _LIB.define("w4a8_gemm_partials(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tens
             "int N, int K, int group) -> (Tensor, Tensor)")
 _LIB.define("w4a8_gemm_swiglu(Tensor a_q, Tensor a_scale, Tensor w_tiles, Tensor s_tiles, "
             "int N, int K, int group) -> Tensor")
+_LIB.define("w4a8_linear(Tensor x, Tensor w_tiles, Tensor s_tiles, int N, int K, int group) -> Tensor")
 _LIB.define("w4a8_rmsnorm_quant(Tensor x, Tensor weight, float eps, Tensor? residual=None, int group=0, "
             "bool want_normed=False) -> (Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("midgroup_quant_a(Tensor x, int group=1024) -> Tensor[]")
@@ -225,6 +227,41 @@ def _gemm_partials_fake(a_q, a_scale, w_tiles, s_tiles, N, K, group):
     M = a_q.shape[0]
     return (a_q.new_empty((M, N), dtype=torch.bfloat16),
             a_q.new_empty((geo.num_groups(K, group), M, N), dtype=torch.int32))
+
+
+# ---------------------------------------------------------------- quant + GEMM
+@torch.library.impl(_LIB, "w4a8_linear", "CUDA")
+def _linear_cuda(x: torch.Tensor, w_tiles, s_tiles, N: int, K: int, group: int):
+    """The W4A8 dynamic linear of bf16 x [M, K]: w4a8_quant_pertoken(x, group) then
+    w4a8_gemm, bit for bit, with the quant fused into the GEMM kernel for a
+    single row (midgroup_quant.py:163-177 is the reference's pair of calls)."""
+    _require(x.dim() == 2 and x.dtype == torch.bfloat16, "w4a8_linear: x must be bfloat16 [M, K]")
+    _require(x.shape[1] == K, f"w4a8_linear: x has {x.shape[1]} columns, K={K}")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M = x.shape[0]
+    dev = x.device
+    width = geo.kpad(K, group)
+    a_q = torch.empty((M, width), dtype=torch.int8, device=dev)
+    a_scale = torch.empty((M,), dtype=torch.bfloat16, device=dev)
+    _check_gemm(a_q, a_scale, w_tiles, s_tiles, N, K, group)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    if M == 0:
+        return y
+    lib = _abi.lib()
+    need = lib.w4a8_gemm_workspace_bytes(M, N, K, group)
+    ws = _workspace(dev, need) if need > 0 else None
+    ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+    _abi.check(lib.w4a8_linear(x.data_ptr(), x.stride(0), w_tiles.data_ptr(), s_tiles.data_ptr(),
+                               _SCALE_DT[s_tiles.dtype], y.data_ptr(), N, a_q.data_ptr(), width,
+                               a_scale.data_ptr(), M, N, K, group, ws_ptr, ws_bytes, _stream(dev)),
+               "w4a8_linear")
+    return y
+
+
+@torch.library.register_fake("npu::w4a8_linear")
+def _linear_fake(x, w_tiles, s_tiles, N, K, group):
+    return x.new_empty((x.shape[0], N), dtype=torch.bfloat16)
 
 
 # ---------------------------------------------------------------- RMSNorm + quant
