@@ -231,23 +231,31 @@ def main():
     T = args.detail_launches
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
 
-    def time_graph(fn, reps=3):
-        with torch.cuda.stream(cap):
+    # Per-shape timings run on their own stream (warm-up launches and graph
+    # replays alike), so a kernel trace of this command separates them from
+    # the step graphs by stream; `--trace-summary` reports per stream.
+    shape_stream = torch.cuda.Stream(device=dev)
+
+    def time_graph(fn, reps=3, stream=None):
+        st = stream if stream is not None else shape_stream
+        with torch.cuda.stream(st):
             fn()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=cap):
             fn()
-        g.replay()
         torch.cuda.synchronize()
         times = []
-        for _ in range(reps):
-            e0, e1 = ev(), ev()
-            e0.record()
+        with torch.cuda.stream(st):
             g.replay()
-            e1.record()
-            e1.synchronize()
-            times.append(e0.elapsed_time(e1) * 1e3)   # us
+            for _ in range(reps):
+                e0, e1 = ev(), ev()
+                e0.record(st)
+                g.replay()
+                e1.record(st)
+                e1.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3)   # us
+        torch.cuda.synchronize()
         del g
         return sorted(times)[len(times) // 2]
 
@@ -274,7 +282,8 @@ def main():
 
             us = time_graph(gemms) / T
             qus = time_graph(quants) / T
-            lus = time_graph(linears) / T
+            # quant + GEMM through w4a8_linear, on the step's stream
+            lus = time_graph(linears, stream=torch.cuda.current_stream(dev)) / T
             x0 = xs[(M, p)]
             fused = bool(pkg._abi.lib().w4a8_linear_fused(x0.data_ptr(), x0.stride(0), M, N, K, GROUP))
             b = gemm_bytes(M, N, K)
@@ -475,19 +484,26 @@ def trace_summary(db):
     import collections
     import sqlite3
     rows = sqlite3.connect(db).execute(
-        "select name, duration, grid_x, grid_y, workgroup_x from kernels order by start").fetchall()
+        "select name, duration, grid_x, grid_y, workgroup_x, stream from kernels order by start").fetchall()
     by_name, by_shape = collections.defaultdict(list), collections.defaultdict(list)
-    for name, dur, gx, gy, wx in rows:
+    by_stream = collections.defaultdict(list)
+    for name, dur, gx, gy, wx, stream in rows:
         short = name.split("(")[0].split("<")[0].split("::")[-1]
         by_name[short].append(dur)
         by_shape[(short, gx, gy, wx)].append(dur)
+        by_stream[(short, stream)].append(dur)
     print("| kernel | calls | avg us | min us | max us | total ms |\n|---|---:|---:|---:|---:|---:|")
     for k, d in sorted(by_name.items(), key=lambda kv: -sum(kv[1])):
         print(f"| {k} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} | {min(d) / 1e3:.3f} | {max(d) / 1e3:.3f} | "
               f"{sum(d) / 1e6:.3f} |")
+    print("\nPer stream (the per-shape timings run on a stream of their own, each decode shape "
+          "the same number of times):\n\n| kernel | stream | calls | avg us |\n|---|---|---:|---:|")
+    for (k, st), d in sorted(by_stream.items()):
+        if k.startswith(("gemm_", "linear_", "quant_")):
+            print(f"| {k} | {st} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
     print("\n| kernel | grid x (threads) | grid y | workgroup | calls | avg us |\n|---|---:|---:|---:|---:|---:|")
     for (k, gx, gy, wx), d in sorted(by_shape.items()):
-        if k.startswith(("gemm_", "quant_")):
+        if k.startswith(("gemm_", "linear_", "quant_")):
             print(f"| {k} | {gx} | {gy} | {wx} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
 
 

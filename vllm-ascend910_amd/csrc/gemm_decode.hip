@@ -87,8 +87,8 @@ constexpr uint32_t kOOB = 0x80000000u;
 // LDS, and each wave quantises its range into an LDS copy of A (the per-token
 // arithmetic of quant_act.hip) that its MFMAs then read; the weight ring is
 // already in flight meanwhile.
-template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP, bool SWIGLU, int QM = 0>
-__global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodeParams p) {
+template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP, bool SWIGLU, int QM>
+__device__ __forceinline__ void decode_body(const DecodeParams& p) {
     static_assert(!SWIGLU || (CPW % 2 == 0 && !DUMP), "SwiGLU pairs column blocks and dumps nothing");
     static_assert(QM == 0 || (MT == 1 && QM <= 4 && !DUMP && !SWIGLU), "the fused quant serves at most 4 rows");
     constexpr int R = 16 * MT;
@@ -412,6 +412,17 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodePar
     }
 }
 
+template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP, bool SWIGLU>
+__global__ __launch_bounds__(64 * KWMAX) void gemm_decode_kernel(const DecodeParams p) {
+    decode_body<MT, CPW, KWMAX, D, GM, SBF16, DUMP, SWIGLU, 0>(p);
+}
+
+// The fused quant + GEMM of one row (its own name in kernel traces).
+template <int KWMAX, int GM, bool SBF16>
+__global__ __launch_bounds__(64 * KWMAX) void linear_decode_kernel(const DecodeParams p) {
+    decode_body<1, 2, KWMAX, 4, GM, SBF16, false, false, 1>(p);
+}
+
 int gcd_i(int a, int b) {
     while (b) {
         const int t = a % b;
@@ -518,22 +529,20 @@ DecodeParams make_params(const GemmArgs& a) {
     return p;
 }
 
-// Fused quant + GEMM: MT = 1, CPW = 2, D = 4, plain epilogue.
-template <int GM, bool SBF16, int QM>
+// Fused quant + GEMM: MT = 1, CPW = 2, D = 4, plain epilogue, one row.
+template <int GM, bool SBF16>
 hipError_t launch_fused_g(const DecodeParams& p, int kw, size_t lds, hipStream_t stream) {
     constexpr int KWM = kwmax_for(1, 2);
-    gemm_decode_kernel<1, 2, KWM, 4, GM, SBF16, false, false, QM>
-        <<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
+    linear_decode_kernel<KWM, GM, SBF16><<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
     return hipGetLastError();
 }
 
-template <int QM>
-hipError_t launch_fused_q(const DecodeParams& p, int kw, size_t lds, bool sbf16, hipStream_t s) {
+hipError_t launch_fused(const DecodeParams& p, int kw, size_t lds, bool sbf16, hipStream_t s) {
     switch (group_mode(p.spg)) {
-        case 0: return sbf16 ? launch_fused_g<0, true, QM>(p, kw, lds, s) : launch_fused_g<0, false, QM>(p, kw, lds, s);
-        case 1: return sbf16 ? launch_fused_g<1, true, QM>(p, kw, lds, s) : launch_fused_g<1, false, QM>(p, kw, lds, s);
-        case 3: return sbf16 ? launch_fused_g<3, true, QM>(p, kw, lds, s) : launch_fused_g<3, false, QM>(p, kw, lds, s);
-        default: return sbf16 ? launch_fused_g<2, true, QM>(p, kw, lds, s) : launch_fused_g<2, false, QM>(p, kw, lds, s);
+        case 0: return sbf16 ? launch_fused_g<0, true>(p, kw, lds, s) : launch_fused_g<0, false>(p, kw, lds, s);
+        case 1: return sbf16 ? launch_fused_g<1, true>(p, kw, lds, s) : launch_fused_g<1, false>(p, kw, lds, s);
+        case 3: return sbf16 ? launch_fused_g<3, true>(p, kw, lds, s) : launch_fused_g<3, false>(p, kw, lds, s);
+        default: return sbf16 ? launch_fused_g<2, true>(p, kw, lds, s) : launch_fused_g<2, false>(p, kw, lds, s);
     }
 }
 
@@ -586,7 +595,7 @@ hipError_t launch_linear_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx
     f.p.aq_out = a_q;
     f.p.lda_out = lda;
     f.p.as_out = a_scale;
-    return launch_fused_q<1>(f.p, f.kw, f.lds, a.scale_bf16, stream);
+    return launch_fused(f.p, f.kw, f.lds, a.scale_bf16, stream);
 }
 
 int64_t decode_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
