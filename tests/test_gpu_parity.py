@@ -300,6 +300,37 @@ def test_gemm_qwq_prefill_column_sample(pkg, dev, proj):
     check_output(tensor_bf16_bits(y)[:, cols], y32, mag, ow.num_groups(K, 128), f"{proj} M{M}")
 
 
+@pytest.mark.parametrize("proj", ["qkv_proj", "down_proj"])
+def test_gemm_qwq_prefill_16384_sample(pkg, dev, proj):
+    """configs[2]'s largest batch, M=16384, at full shape; the oracle runs on 96 sampled
+    rows x 160 sampled columns (per-token rows and output columns are independent)."""
+    synth = pkg.synth
+    K, N = synth.QWQ_SHAPES[proj]
+    M, G = 16384, 128
+    say(f"qwq prefill {proj} M={M} (sampled check)")
+    x = synth.activations_device(M, K, seed=11, device=dev)
+    w = synth.weight_codes_uniform(N, K, 12)
+    sb = synth.group_scales(N, ow.num_groups(K, G), 13, "f16")
+    ws32 = synth.scale_bits_to_f32(sb, "f16")
+    w_scale = torch.from_numpy(np.ascontiguousarray(sb.T).view(np.int16)).view(torch.float16)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(torch.from_numpy(ow.pack_grouped(w, G)).to(dev),
+                                                 w_scale.to(dev), K, G)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, G)
+    y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(5)
+    rows = np.sort(np.concatenate([rng.choice(M, 94, replace=False), [0, M - 1]]))
+    cols = np.sort(np.concatenate([rng.choice(N, 158, replace=False), [0, N - 1]]))
+    rt = torch.from_numpy(rows).to(dev)
+    xb = tensor_bf16_bits(x.index_select(0, rt))
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    assert np.array_equal(tensor_bf16_bits(a_s.index_select(0, rt)), s_ref)
+    assert np.array_equal(a_q.index_select(0, rt).cpu().numpy(), q_ref)
+    y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G, return_abs=True)
+    got = tensor_bf16_bits(y.index_select(0, rt))[:, cols]
+    check_output(got, y32, mag, ow.num_groups(K, G), f"{proj} M{M} sample")
+
+
 def test_gemm_deterministic_and_stress(pkg, dev):
     """Split-K partials are reduced in a fixed order: repeated launches give
     identical bits (the reference's --stress relaunch check, mg_harness.h:307-334)."""

@@ -32,6 +32,21 @@ def activations(M: int, K: int, seed: int, outlier_frac: float = 0.001, outlier_
     return f32_to_bf16_bits(x)
 
 
+def activations_device(M: int, K: int, seed: int, device, outlier_frac: float = 0.001,
+                       outlier_scale: float = 20.0):
+    """The distribution of ``activations`` drawn on the device (for prefill-sized
+    batches): a bf16 torch tensor [M, K], N(0,1) from a seeded device generator,
+    the same number of outlier channels (chosen from the numpy seed) scaled."""
+    import torch
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    x = torch.randn((M, K), dtype=torch.float32, device=device, generator=gen)
+    n_out = max(1, int(round(K * outlier_frac)))
+    ch = np.random.default_rng(seed).choice(K, size=n_out, replace=False)
+    x[:, torch.from_numpy(ch).to(device)] *= outlier_scale
+    return x.to(torch.bfloat16)
+
+
 def weight_codes_uniform(N: int, K: int, seed: int) -> np.ndarray:
     """int8 [N, K] codes uniform in [-8, 7]."""
     return np.random.default_rng(seed).integers(-8, 8, size=(N, K), dtype=np.int8)
