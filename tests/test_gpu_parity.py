@@ -184,6 +184,7 @@ GEMM_CASES = [
     (2, 160, 2560, 640, "bf16"),     # decode, 10 slabs per group (not a power-of-two multiple of 128)
     (5, 96, 3072, 256, "f16"),       # decode, two tiles per group
     (64, 7168, 5120, 128, "f16"),    # qkv decode, M=64
+    (12, 32768, 1024, 128, "bf16"),  # wide N past 8 rows: four column blocks per workgroup
     (17, 336, 1536, 192, "f16"),     # two 16-row groups, the second with one row; 11 column groups
     (40, 1000, 2048, 64, "bf16"),    # three row groups, ragged N
     (50, 200, 3072, 320, "f16"),     # row groups with groups ending on either slab
@@ -507,6 +508,7 @@ def run_swiglu_pair(dev, xb, w, w_scale, N, K, G):
 
 SWIGLU_CASES = [
     # (M, I, K, G, scale dtype): merged gate/up weight of N = 2*I rows
+    (16, 16384, 512, 128, "f16"),     # wide N past 8 rows: four column blocks per workgroup
     (1, 512, 1024, 128, "f16"),
     (4, 1024, 2048, 64, "bf16"),
     (33, 256, 1024, 256, "bf16"),

@@ -434,7 +434,7 @@ int gcd_i(int a, int b) {
 
 // Most waves per workgroup a variant is built for (its register budget: the
 // 64-row, 4-block variant needs 256 VGPRs at 2 waves per SIMD).
-constexpr int kwmax_for(int mt, int cpw) { return mt == 1 ? 12 : (mt == 2 || cpw <= 2 ? 8 : 4); }
+constexpr int kwmax_for(int mt, int cpw) { return mt == 1 ? (cpw >= 4 ? 8 : 12) : (mt == 2 || cpw <= 2 ? 8 : 4); }
 
 // MODE: 0 = plain, 1 = plain with partial dump, 2 = SwiGLU epilogue.
 template <int MT, int CPW, int D, int GM, int MODE>
@@ -490,6 +490,8 @@ hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool sbf16, hi
         if (mt == 2 && c.D == 4 && c.CPW == 1) return launch_v<2, 1, 4, MODE>(p, c.KW, sbf16, s);
     }
     if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 1 && c.D == 4 && c.CPW == 4) return launch_v<1, 4, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 1 && c.D == 2 && c.CPW == 4) return launch_v<1, 4, 2, MODE>(p, c.KW, sbf16, s);
     if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, MODE>(p, c.KW, sbf16, s);
@@ -609,8 +611,11 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     DecodeConfig c{4, 2, 4};
     const int64_t wgs = (NB + 1) / 2;
     if (wgs >= 1024) {
-        // Wide N already gives >= 1024 workgroups of all rows.
-        if (mt <= 2) c.KW = M <= 2 ? 2 : 1;
+        // Wide N already gives >= 1024 workgroups of all rows.  Past 8 rows
+        // the activations every workgroup reads weigh as much as its weights:
+        // four column blocks per workgroup halve that traffic.
+        if (mt == 1 && M > 8) c = DecodeConfig{2, 4, 1};
+        else if (mt <= 2) c.KW = M <= 2 ? 2 : 1;
         else c = DecodeConfig{2, 4, 1};
     } else if (mt == 1 || (mt == 2 && KT >= 128)) {
         // Split K so that each wave holds about one ring (4 tiles) of its
