@@ -469,6 +469,54 @@ def test_linear_unaligned_and_strided_input(pkg, dev):
         assert np.array_equal(tensor_bf16_bits(y), tensor_bf16_bits(y_ref)), (off, ld)
 
 
+def test_vllm_plugin_methods_apply(pkg, dev):
+    """Both quant methods end to end -- create_weights, load the checkpoint tensors,
+    process_weights_after_loading, apply -- bit-equal to the modules they mirror."""
+    say("vllm plugin methods")
+    vp = pkg.vllm_plugin
+    K, N = 1600, 384
+    torch.manual_seed(3)
+    w = (torch.randn(N, K) * 0.05).to(torch.bfloat16)
+    x = torch.randn(2, 3, K, dtype=torch.bfloat16).to(dev)
+    bias = (torch.randn(N) * 0.1).to(torch.bfloat16).to(dev)
+
+    # per-token, group 64 (an unpadded layout), fp16 scales
+    G = 64
+    w_q, w_scale = pkg.packing.quantize_weight(w, G, torch.float16)
+    layer = torch.nn.Module()
+    m = vp.PerTokenW4A8Config(group_size=G, scale_dtype="float16").get_quant_method(layer, "l.0.o_proj")
+    m.create_weights(layer, K, [N], K, N, torch.bfloat16)
+    with torch.no_grad():
+        layer.weight_packed.copy_(w_q)
+        layer.weight_scale.copy_(w_scale.t())
+    layer.to(dev)
+    m.process_weights_after_loading(layer)
+    y = m.apply(layer, x, bias)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q.to(dev), w_scale.to(dev), K, G)
+    y_ref = pkg.linear(x, w_tiles, s_tiles, N, G, bias)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 3, N)
+    assert np.array_equal(tensor_bf16_bits(y.reshape(-1, N)), tensor_bf16_bits(y_ref.reshape(-1, N)))
+
+    # mid-group, the reference's group 1024 with a short last group (1600 = 1024 + 576)
+    G = 1024
+    wq, ws, wk, wz = pkg.packing.quantize_weight_asym(w, G)     # scales [G, N]
+    layer = torch.nn.Module()
+    m = vp.MidGroupW4A8Config(group_size=G).get_quant_method(layer, "l.0.down_proj")
+    m.create_weights(layer, K, [N], K, N, torch.bfloat16)
+    with torch.no_grad():
+        layer.weight_packed.copy_(wq)
+        layer.weight_scale.copy_(ws.t())
+        layer.weight_zero.copy_(wz.t())
+        layer.weight_ksum.copy_(wk.t())
+    layer.to(dev)
+    m.process_weights_after_loading(layer)
+    y = m.apply(layer, x, bias)
+    y_ref = pkg.midgroup_linear(x, wq.to(dev), ws.to(dev), wk.to(dev), wz.to(dev), G) + bias
+    torch.cuda.synchronize()
+    assert np.array_equal(tensor_bf16_bits(y.reshape(-1, N)), tensor_bf16_bits(y_ref.reshape(-1, N)))
+
+
 def test_workspace_reuse_across_shapes(pkg, dev):
     """Regression: consecutive split-K calls of different shapes share one
     workspace; a small-N call's partials must not leave non-zero counters for a

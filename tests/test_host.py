@@ -141,3 +141,47 @@ def test_midgroup_export_and_load_roundtrip(pkg, tmp_path):
     with pytest.raises(ValueError):
         pkg.checkpoint.load_midgroup_linear(out, base, K=1100, device="cpu")
     assert pkg.checkpoint.quant_config(1024)["packed_layout"] == "mg_kgeom_v1"
+
+
+# ------------------------------------------------------------------ vLLM-style linear methods
+def test_vllm_plugin_configs_and_weights(pkg):
+    """The quant-method contract without vLLM: config parsing, the parameters
+    create_weights registers (checkpoint layout, output_dim 0, loader), the
+    row-parallel refusal and the load-time transpose of the mid-group tensors."""
+    vp = pkg.vllm_plugin
+    cfg = vp.MidGroupW4A8Config.from_config({"quant_method": "midgroup_w4a8", "group_size": 1024, "sym": False})
+    assert cfg.get_name() == "midgroup_w4a8" and cfg.group_size == 1024 and cfg.quant_description == {}
+    assert cfg.get_supported_act_dtypes() == [torch.bfloat16]
+    assert cfg.get_quant_method(torch.nn.Module(), "model.lm_head") is None
+    m = cfg.get_quant_method(torch.nn.Module(), "model.layers.0.self_attn.o_proj")
+    layer = torch.nn.Module()
+    loader = object()
+    m.create_weights(layer, 3456, [256, 128], 3456, 384, torch.bfloat16, weight_loader=loader)
+    G = 4                      # 3456 = 3 full groups + a short one of 384
+    assert tuple(layer.weight_packed.shape) == (384, pkg.geometry.kpad(3456, 1024) // 2)
+    assert pkg.geometry.kpad(3456, 1024) == 3 * 1024 + 384
+    for name, dt in (("weight_scale", torch.bfloat16), ("weight_zero", torch.bfloat16), ("weight_ksum", torch.int32)):
+        t = getattr(layer, name)
+        assert tuple(t.shape) == (384, G) and t.dtype == dt and t.output_dim == 0 and t.weight_loader is loader
+        assert not t.requires_grad
+    with torch.no_grad():
+        layer.weight_scale.copy_(torch.arange(384 * G, dtype=torch.float32).reshape(384, G).to(torch.bfloat16))
+    ref = layer.weight_scale.detach().clone()
+    m.process_weights_after_loading(layer)
+    assert tuple(layer.weight_scale.shape) == (G, 384) and torch.equal(layer.weight_scale, ref.t())
+    with pytest.raises(ValueError, match="K-sharded"):
+        m.create_weights(torch.nn.Module(), 2560, [5120], 5120, 5120, torch.bfloat16)
+
+    pt = vp.PerTokenW4A8Config.from_config({"quant_method": "w4a8_pertoken", "group_size": 128,
+                                             "scale_dtype": "bfloat16"})
+    assert pt.get_name() == "w4a8_pertoken" and pt.scale_dtype == "bfloat16"
+    layer2 = torch.nn.Module()
+    pt.get_quant_method(layer2, "model.layers.0.mlp.down_proj").create_weights(
+        layer2, 5120, [1024], 5120, 1024, torch.bfloat16)
+    assert tuple(layer2.weight_packed.shape) == (1024, 2560) and layer2.weight_scale.dtype == torch.bfloat16
+    assert tuple(layer2.weight_scale.shape) == (1024, 40)
+    with pytest.raises(ValueError):
+        vp.PerTokenW4A8Config(scale_dtype="float32")
+    if not vp.HAVE_VLLM:
+        with pytest.raises(ImportError):
+            vp.register()

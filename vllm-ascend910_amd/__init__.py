@@ -9,9 +9,9 @@ itself is loaded on first use (``_abi.lib()``) and must have been built.
 The directory name is not a Python identifier, so the package is imported as
 ``vllm_ascend910_amd`` through ``__graft_entry__.package()``.
 """
-from . import checkpoint, decoder, geometry, packing, synth  # noqa: F401
+from . import checkpoint, decoder, geometry, packing, synth, vllm_plugin  # noqa: F401
 from . import ops  # noqa: F401
 from .linear import MidGroupW4A8Linear, W4A8Linear, linear, linear_swiglu, midgroup_linear  # noqa: F401
 
 __all__ = ["W4A8Linear", "MidGroupW4A8Linear", "linear", "linear_swiglu", "midgroup_linear", "geometry",
-           "packing", "ops", "synth", "decoder", "checkpoint"]
+           "packing", "ops", "synth", "decoder", "checkpoint", "vllm_plugin"]

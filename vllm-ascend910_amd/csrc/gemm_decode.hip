@@ -85,8 +85,8 @@ constexpr uint32_t kOOB = 0x80000000u;
 // the launcher builds QM = 1 only):
 // each wave loads the bf16 rows of its own K range, the waves' absmax meet in
 // LDS, and each wave quantises its range into an LDS copy of A (the per-token
-// arithmetic of quant_act.hip) that its MFMAs then read; the weight ring is
-// already in flight meanwhile.
+// arithmetic of quant_act.hip) that its MFMAs then read; the row loads are
+// issued ahead of the weight ring, which streams meanwhile.
 template <int MT, int CPW, int KWMAX, int D, int GM, bool SBF16, bool DUMP, bool SWIGLU, int QM>
 __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     static_assert(!SWIGLU || (CPW % 2 == 0 && !DUMP), "SwiGLU pairs column blocks and dumps nothing");
