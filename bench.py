@@ -198,6 +198,7 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
+    clocks = gpu_clocks()   # right after the timed region (the clocks ramp down when idle)
     value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
     log(f"bench: {ms_per_step:.4f} ms/step, {value:.1f} GB/s over {bytes_per_step / 1e6:.1f} MB/step")
 
@@ -310,6 +311,8 @@ def main():
         "traffic_source": str(traffic_src.relative_to(ROOT)) if traffic is not None else None,
     }
     result["decode_shapes"] = shapes
+    result["gpu_clocks"] = {"after_timed_region": clocks,
+                            "note": "rocm-smi reading; the peaks above are MI355X's published figures (2.4 GHz)"}
 
     # ---------------------------------------------------------------- prefill
     prefill = []
@@ -328,7 +331,8 @@ def main():
             us = time_graph(gemms) / Tp
             tops = 2 * M * N * K / us / 1e6
             prefill.append({"proj": p, "M": M, "gemm_us": round(us, 2), "TOPS": round(tops, 1),
-                            "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)})
+                            "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+                            "GBs": round(gemm_bytes(M, N, K) / us / 1e3, 1)})
             log(f"  prefill {p:13s} M={M:5d}: {us:9.1f} us {tops:7.1f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)")
             del x, a_q, a_s
     result["prefill_shapes"] = prefill
@@ -610,18 +614,41 @@ def cpu_baseline(pkg, dev, seconds):
             q, s = ow.quant_act_per_token(xb)
             ow.gemm_fp32(q, s, w, ws32, GROUP)
         what = "numpy restatement (oracle/w4a8.py) of the reference torch CPU path, configs[0]"
-    run()
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        run()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 10000:
-            break
+    def timed(fn, budget):
+        fn()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or reps >= 10000:
+                return reps, el
+
+    reps, el = timed(run, seconds)
     sec = el / reps
-    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{what}; {reps} runs in {el:.1f} s, {sec * 1e3:.2f} ms per linear",
-            "us_per_linear": round(sec * 1e6, 1), "parity_vs_gpu": parity}
+    out = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+           "sample": f"{what}; {reps} runs in {el:.1f} s, {sec * 1e3:.2f} ms per linear",
+           "us_per_linear": round(sec * 1e6, 1), "parity_vs_gpu": parity}
+    if kind == "reference":
+        # the numpy restatement of the same path, for comparison (numpy's own threading)
+        def port():
+            q, s = ow.quant_act_per_token(xb)
+            ow.gemm_fp32(q, s, w, ws32, GROUP)
+        preps, pel = timed(port, max(1.0, seconds / 4))
+        out["port"] = {"us_per_linear": round(pel / preps * 1e6, 1), "GBs": round(nbytes / (pel / preps) / 1e9, 3),
+                       "sample": f"oracle/w4a8.py numpy restatement, {preps} runs in {pel:.1f} s"}
+    return out
+
+
+def gpu_clocks():
+    """The GPU's current clock readings from rocm-smi (run as a child process), or None."""
+    import subprocess
+    try:
+        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True, text=True, timeout=30)
+        card = next(iter(json.loads(r.stdout).values()))
+        return {k.rstrip(":"): v for k, v in card.items() if "clk" in k.lower() and "speed" in k.lower()}
+    except Exception:   # tool missing or output not JSON: the clocks are informational only
+        return None
 
 
 if __name__ == "__main__":
