@@ -303,7 +303,7 @@ def main():
     if traffic_src.exists():
         traffic = round(json.loads(traffic_src.read_text())["avg_traffic_bytes"])
     result["roofline"] = {
-        "kernel": "gemm_decode_kernel (decode W4A8 GEMM, all 16 configs[1] shapes, cold)",
+        "kernel": "decode W4A8 GEMM: gemm_decode_kernel, gemm_wide_kernel for gate_up M=64 (all 16 configs[1] shapes, cold)",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
         "per_launch_bytes_avg": round(tot_bytes / len(shapes)), "launch_us_avg": round(tot_us / len(shapes), 3),
@@ -509,6 +509,12 @@ def trace_summary(db):
     for (k, st), d in sorted(by_stream.items()):
         if k.startswith(("gemm_", "linear_", "quant_")):
             print(f"| {k} | {st} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
+    both = collections.defaultdict(list)
+    for (k, st), d in by_stream.items():
+        if k in ("gemm_decode_kernel", "gemm_wide_kernel"):
+            both[st] += d
+    for st, d in sorted(both.items()):
+        print(f"| decode GEMM (gemm_decode_kernel + gemm_wide_kernel) | {st} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
     print("\n| kernel | grid x (threads) | grid y | workgroup | calls | avg us |\n|---|---:|---:|---:|---:|---:|")
     for (k, gx, gy, wx), d in sorted(by_shape.items()):
         if k.startswith(("gemm_", "linear_", "quant_")):
@@ -531,8 +537,9 @@ def pmc_summary(fetch_db, write_db, out_json=None):
     cal_kib = 256 * 1024
     ff = cal_kib / [v for n, v in fetch if is_copy(n)][-1]
     fw = cal_kib / [v for n, v in write if is_copy(n)][-1]
-    gf = [v for n, v in fetch if "gemm_decode_kernel" in n][-16:]
-    gw = [v for n, v in write if "gemm_decode_kernel" in n][-16:]
+    is_gemm = lambda n: "gemm_decode_kernel" in n or "gemm_wide_kernel" in n   # noqa: E731
+    gf = [v for n, v in fetch if is_gemm(n)][-16:]
+    gw = [v for n, v in write if is_gemm(n)][-16:]
     shapes = [(M, p) for M in DECODE_MS for p in PROJS]
     import __graft_entry__ as ge
     synth = ge.package().synth

@@ -185,6 +185,10 @@ GEMM_CASES = [
     (5, 96, 3072, 256, "f16"),       # decode, two tiles per group
     (64, 7168, 5120, 128, "f16"),    # qkv decode, M=64
     (12, 32768, 1024, 128, "bf16"),  # wide N past 8 rows: four column blocks per workgroup
+    (40, 32768, 1024, 128, "f16"),   # wide N past 16 rows: activations shared through LDS
+    (48, 32768, 1024, 64, "bf16"),   # the same, group stride 64
+    (20, 33000, 1920, 320, "f16"),   # the same, groups ending on either slab, ragged column groups
+    (64, 32768, 3072, 512, "bf16"),  # the same, groups of four tiles
     (17, 336, 1536, 192, "f16"),     # two 16-row groups, the second with one row; 11 column groups
     (40, 1000, 2048, 64, "bf16"),    # three row groups, ragged N
     (50, 200, 3072, 320, "f16"),     # row groups with groups ending on either slab
@@ -330,6 +334,28 @@ def test_gemm_qwq_prefill_16384_sample(pkg, dev, proj):
     y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G, return_abs=True)
     got = tensor_bf16_bits(y.index_select(0, rt))[:, cols]
     check_output(got, y32, mag, ow.num_groups(K, G), f"{proj} M{M} sample")
+
+
+def test_gemm_every_decode_row_count(pkg, dev):
+    """Every M from 1 to 64 on a wide (2048 column groups) and a narrow N: each picks a
+    built kernel variant (a missing one is a launch error) and matches the oracle on a
+    column sample."""
+    K, G = 512, 128
+    cols_rng = np.random.default_rng(9)
+    for N in (32768, 1000):
+        xb_all, w, ws32, w_scale = make_problem(pkg, 64, N, K, G, seed=N)
+        w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+        w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+        cols = np.sort(cols_rng.choice(N, 48, replace=False))
+        for M in range(1, 65):
+            say(f"decode rows M={M} N={N}")
+            xb = xb_all[:M]
+            a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xb).to(dev), G)
+            y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+            torch.cuda.synchronize()
+            q_ref, s_ref = ow.quant_act_per_token(xb)
+            y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G, return_abs=True)
+            check_output(tensor_bf16_bits(y)[:, cols], y32, mag, ow.num_groups(K, G), f"M{M} N{N}")
 
 
 def test_gemm_deterministic_and_stress(pkg, dev):
@@ -557,6 +583,7 @@ def run_swiglu_pair(dev, xb, w, w_scale, N, K, G):
 SWIGLU_CASES = [
     # (M, I, K, G, scale dtype): merged gate/up weight of N = 2*I rows
     (16, 16384, 512, 128, "f16"),     # wide N past 8 rows: four column blocks per workgroup
+    (33, 16384, 1024, 128, "bf16"),   # wide N past 16 rows: activations shared through LDS
     (1, 512, 1024, 128, "f16"),
     (4, 1024, 2048, 64, "bf16"),
     (33, 256, 1024, 256, "bf16"),

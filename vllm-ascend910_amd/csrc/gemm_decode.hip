@@ -565,7 +565,7 @@ bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f)
     if (a.M != 1 || a.swiglu || a.partials || !geom::is_unpadded(a.K, a.group)) return false;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx % 8 != 0) return false;
     const DecodeConfig c = decode_config(a.M, a.N, a.K, a.group);
-    if (c.D != 4 || c.CPW != 2 || c.MT != 0) return false;
+    if (c.D != 4 || c.CPW != 2 || c.MT != 0 || c.WIDE) return false;
     f.p = make_params(a);
     f.p.cgroups = (f.p.NB + 1) / 2;
     f.p.rgroups = 1;
@@ -615,8 +615,8 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
         // the activations every workgroup reads weigh as much as its weights:
         // four column blocks per workgroup halve that traffic.
         if (mt == 1 && M > 8) c = DecodeConfig{2, 4, 1};
-        else if (mt <= 2) c.KW = M <= 2 ? 2 : 1;
-        else c = DecodeConfig{2, 4, 1};
+        else if (mt == 1) c.KW = M <= 2 ? 2 : 1;
+        else c = DecodeConfig{2, 2, 1, 0, 1};   // > 16 rows: activations shared through LDS
     } else if (mt == 1 || (mt == 2 && KT >= 128)) {
         // Split K so that each wave holds about one ring (4 tiles) of its
         // range -- but long K (>= 128 tiles) streams better with fewer, longer
@@ -633,6 +633,7 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
 }
 
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream) {
+    if (cfg.WIDE) return launch_gemm_wide(a, 4, cfg.CPW, 1, stream);
     const DecodeParams p = make_params(a);
     if (a.swiglu) return dispatch<2>(p, cfg, a.scale_bf16, stream);
     return a.partials ? dispatch<1>(p, cfg, a.scale_bf16, stream) : dispatch<0>(p, cfg, a.scale_bf16, stream);
