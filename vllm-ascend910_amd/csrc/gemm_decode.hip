@@ -633,7 +633,7 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
 }
 
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream) {
-    if (cfg.WIDE) return launch_gemm_wide(a, 4, cfg.CPW, 1, stream);
+    if (cfg.WIDE) return launch_gemm_wide(a, stream);
     const DecodeParams p = make_params(a);
     if (a.swiglu) return dispatch<2>(p, cfg, a.scale_bf16, stream);
     return a.partials ? dispatch<1>(p, cfg, a.scale_bf16, stream) : dispatch<0>(p, cfg, a.scale_bf16, stream);

@@ -6,13 +6,14 @@
 // end).  The decode kernel gives every wave all rows and its own K range, so
 // every workgroup streams the whole activation block from L2 for its few
 // column blocks: at 64 rows on gate_up that is twice the weight bytes.  Here a
-// workgroup of kWN x KS waves covers kWN * 4 column blocks; the kWN waves of
-// one K split walk the same tiles and share each 64-row activation tile,
-// staged once into LDS (double-buffered, one barrier per tile) and read from
-// there as MFMA operands.  Weights stream straight to registers in a 2-deep
-// ring as in the decode kernel.  With two K splits the second split's
-// accumulators are added to the first's through LDS at the end, in a fixed
-// order, so results are deterministic.
+// workgroup of kWN column waves covers kWN * kCPW column blocks and walks all
+// of K; its waves share each 64-row activation tile, staged once into LDS
+// (double-buffered, one barrier per tile) and read from there as MFMA
+// operands, while the weights stream straight to registers in a 2-deep ring
+// as in the decode kernel.  The accumulation order per output is the decode
+// kernel's with one K wave, so the sums are bit-identical to it.  (Measured
+// on the QwQ-32B shapes: on narrow N -- a few dozen workgroups -- adding K
+// splits reduced through LDS did not reach the decode kernel's row groups.)
 #include <type_traits>
 
 #include "common.h"
@@ -39,37 +40,33 @@ struct WideParams {
     int32_t* P;        // optional partial dump [NG, M, N]
     int M, N, KT, NG, NB;
     int up_nb;         // SWIGLU: column blocks per half
-    int nslab, spg, gshift, unit, units;
+    int nslab, spg, gshift;
     uint32_t a_bytes, w_bytes, s_bytes;
 };
 
 // GM: the group modes of gemm_decode.hip (0: stride 64, 3: stride 128,
 // 1: stride 128 * 2^gshift, 2: any other stride).
-// kWN column waves per K split, kCPW 16-column blocks per wave, KS K splits.
-template <int kWN, int kCPW, int KS, int GM, bool SBF16, bool DUMP, bool SWIGLU>
-__global__ __launch_bounds__(64 * kWN * KS) void gemm_wide_kernel(const WideParams p) {
+// kWN column waves, kCPW 16-column blocks per wave.
+template <int kWN, int kCPW, int GM, bool SBF16, bool DUMP, bool SWIGLU>
+__global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p) {
     static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
     constexpr int CG = SWIGLU ? kCPW / 2 : kCPW;   // output column blocks per wave
     constexpr int NS = (GM == 1 || GM == 3) ? 1 : 2;
-    // two staged activation tiles per K split; the epilogue reuses the space
-    __shared__ __attribute__((aligned(16))) int8_t la[KS][2][kATile];
+    // two staged activation tiles
+    __shared__ __attribute__((aligned(16))) int8_t la[2][kATile];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave % kWN, ks = wave / kWN;
+    const int wn = wave;
     const int rowq = 4 * (lane >> 4);
     const int colq = lane & 15;
 
     const int nb0 = (static_cast<int>(blockIdx.x) * kWN + wn) * CG;
     auto block_of = [&](int c) { return (SWIGLU && c >= CG) ? nb0 + (c - CG) + p.up_nb : nb0 + c; };
 
-    // This K split's tile range [ta, tb); every split runs nit iterations
-    // (tiles past tb hold zero weights) so that the barriers line up.
-    const int ua = (ks * p.units) / KS, ub = ((ks + 1) * p.units) / KS;
-    const int ta = ua * p.unit;
-    const int tb = min(p.KT, ub * p.unit);
-    const int nit = ((p.units + KS - 1) / KS) * p.unit;
+    // All of K: tiles [0, KT).
+    const int ta = 0, tb = p.KT, nit = p.KT;
 
     uint32_t wo[kCPW], so[kCPW];
 #pragma unroll
@@ -78,8 +75,8 @@ __global__ __launch_bounds__(64 * kWN * KS) void gemm_wide_kernel(const WidePara
         wo[c] = nb * static_cast<uint32_t>(p.KT) * 1024u + lane * 16u;
         so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + colq) * 2u;
     }
-    // Staging: the split's 64 rows x 128 K = 512 units of 16 bytes, NU per
-    // lane of its kWN waves; rows past M read zero.
+    // Staging: 64 rows x 128 K = 512 units of 16 bytes, NU per lane; rows
+    // past M read zero.
     constexpr int NU = 512 / (64 * kWN);
     static_assert(NU * 64 * kWN == 512, "kWN must divide 8");
     uint32_t sg[NU];
@@ -102,15 +99,14 @@ __global__ __launch_bounds__(64 * kWN * KS) void gemm_wide_kernel(const WidePara
 
     uint4 ra[2][NU];
     auto stage_load = [&](int t, uint4 (&r)[NU]) {
-        // tiles past the split's range stage its last tile again (zero weights meet it)
-        const int tt = min(t, max(tb - 1, ta));
-        const auto rs = make_rsrc_at(p.A, static_cast<uint32_t>(min(tt, p.KT - 1)) * 128u, p.a_bytes);
+        // tiles past the end stage the last tile again (nothing reads them)
+        const auto rs = make_rsrc_at(p.A, static_cast<uint32_t>(min(t, p.KT - 1)) * 128u, p.a_bytes);
 #pragma unroll
         for (int j = 0; j < NU; ++j) r[j] = buf_load16(rs, sg[j]);
     };
     auto stage_store = [&](int buf, const uint4 (&r)[NU]) {
 #pragma unroll
-        for (int j = 0; j < NU; ++j) *reinterpret_cast<uint4*>(&la[ks][buf][sl[j]]) = r[j];
+        for (int j = 0; j < NU; ++j) *reinterpret_cast<uint4*>(&la[buf][sl[j]]) = r[j];
     };
 
     uint4 wb[kD][kCPW];
@@ -181,7 +177,7 @@ __global__ __launch_bounds__(64 * kWN * KS) void gemm_wide_kernel(const WidePara
 #pragma unroll
         for (int c = 0; c < kCPW; ++c) unpack_tile_lane(wb[u][c], b[c][0], b[c][1]);
         load_slot(u, t + kD);
-        const int8_t* ab = &la[ks][u][0] + colq * kALS + (lane >> 4) * 16;
+        const int8_t* ab = &la[u][0] + colq * kALS + (lane >> 4) * 16;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const bool fresh = GM == 0 || (GM == 3 && h == 0);
@@ -215,36 +211,7 @@ __global__ __launch_bounds__(64 * kWN * KS) void gemm_wide_kernel(const WidePara
     }
     if (i < nit) step(i, 0);
 
-    // ---- K-split reduction (second split into the first, fixed order) and epilogue
-    if constexpr (KS == 2) {
-        constexpr int C = 16 * kCPW;
-        float* red = reinterpret_cast<float*>(&la[0][0][0]);   // kWN x 32 rows x C columns per half
-        static_assert(kWN * 32 * C * 4 <= static_cast<int>(sizeof(la)), "reduction does not fit the staging space");
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            if (ks == 1) {
-#pragma unroll
-                for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-                    for (int c = 0; c < kCPW; ++c)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            red[(wn * 32 + m2 * 16 + rowq + q) * C + c * 16 + colq] = acc[2 * half + m2][c][q];
-            }
-            __syncthreads();
-            if (ks == 0) {
-#pragma unroll
-                for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-                    for (int c = 0; c < kCPW; ++c)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            acc[2 * half + m2][c][q] += red[(wn * 32 + m2 * 16 + rowq + q) * C + c * 16 + colq];
-            }
-            __syncthreads();
-        }
-        if (ks != 0) return;
-    }
+    // ---- epilogue: token scale, bf16 (or the SwiGLU pair)
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
@@ -279,38 +246,30 @@ int group_mode_of(int spg) {
     return 2;
 }
 
-template <int WN, int CPW, int KS, int GM, bool DUMP, bool SWIGLU>
-hipError_t launch_ks(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
-    const dim3 grid(static_cast<unsigned>(cgroups)), block(64 * WN * KS);
-    if (sbf16) gemm_wide_kernel<WN, CPW, KS, GM, true, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
-    else gemm_wide_kernel<WN, CPW, KS, GM, false, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
+constexpr int kWaves = 4;   // column waves per workgroup
+constexpr int kBlocks = 2;  // column blocks per wave
+
+template <int GM, bool DUMP, bool SWIGLU>
+hipError_t launch_g(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(cgroups)), block(64 * kWaves);
+    if (sbf16) gemm_wide_kernel<kWaves, kBlocks, GM, true, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
+    else gemm_wide_kernel<kWaves, kBlocks, GM, false, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
     return hipGetLastError();
 }
 
-template <int WN, int CPW, int KS, bool DUMP, bool SWIGLU>
+template <bool DUMP, bool SWIGLU>
 hipError_t launch_gm(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
     switch (group_mode_of(p.spg)) {
-        case 0: return launch_ks<WN, CPW, KS, 0, DUMP, SWIGLU>(p, cgroups, sbf16, s);
-        case 1: return launch_ks<WN, CPW, KS, 1, DUMP, SWIGLU>(p, cgroups, sbf16, s);
-        case 3: return launch_ks<WN, CPW, KS, 3, DUMP, SWIGLU>(p, cgroups, sbf16, s);
-        default: return launch_ks<WN, CPW, KS, 2, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 0: return launch_g<0, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 1: return launch_g<1, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 3: return launch_g<3, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        default: return launch_g<2, DUMP, SWIGLU>(p, cgroups, sbf16, s);
     }
-}
-
-template <int WN, int CPW, int KS>
-hipError_t launch_mode(const WideParams& p, int cgroups, bool sbf16, bool dump, bool swiglu, hipStream_t s) {
-    if constexpr (CPW % 2 == 0) {
-        if (swiglu) return launch_gm<WN, CPW, KS, false, true>(p, cgroups, sbf16, s);
-    } else {
-        if (swiglu) return hipErrorInvalidValue;
-    }
-    return dump ? launch_gm<WN, CPW, KS, true, false>(p, cgroups, sbf16, s)
-                : launch_gm<WN, CPW, KS, false, false>(p, cgroups, sbf16, s);
 }
 
 }  // namespace
 
-hipError_t launch_gemm_wide(const GemmArgs& a, int wn, int cpw, int ks, hipStream_t stream) {
+hipError_t launch_gemm_wide(const GemmArgs& a, hipStream_t stream) {
     if (a.M <= 0 || a.M > 16 * kMT) return hipErrorInvalidValue;
     WideParams p{};
     p.A = a.a_q;
@@ -334,26 +293,12 @@ hipError_t launch_gemm_wide(const GemmArgs& a, int wn, int cpw, int ks, hipStrea
     p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + geom::kpad(a.K, a.group));
     p.w_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.KT) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.NG) * 16 * 2);
-    // K-split units fall on tile and group boundaries (as in the decode kernel)
-    int g2 = 2, s2 = p.spg;
-    while (s2) {
-        const int t = g2 % s2;
-        g2 = s2;
-        s2 = t;
-    }
-    p.unit = (2 * p.spg / g2) / 2;
-    p.units = (p.KT + p.unit - 1) / p.unit;
-    const int blocks_per_wg = wn * cpw;
-    const int64_t cg = a.swiglu ? geom::ceil_div(p.up_nb, blocks_per_wg / 2) : geom::ceil_div(p.NB, blocks_per_wg);
-    const bool dump = a.partials != nullptr;
+    const int per_wg = kWaves * kBlocks;
+    const int64_t cg = a.swiglu ? geom::ceil_div(p.up_nb, per_wg / 2) : geom::ceil_div(p.NB, per_wg);
     const int c = static_cast<int>(cg);
-    const bool b = a.scale_bf16, sw = a.swiglu;
-    if (ks == 1 && wn == 4 && cpw == 1) return launch_mode<4, 1, 1>(p, c, b, dump, sw, stream);
-    if (ks == 1 && wn == 4 && cpw == 2) return launch_mode<4, 2, 1>(p, c, b, dump, sw, stream);
-    if (ks == 1 && wn == 8 && cpw == 2) return launch_mode<8, 2, 1>(p, c, b, dump, sw, stream);
-    if (ks == 1 && wn == 8 && cpw == 1) return launch_mode<8, 1, 1>(p, c, b, dump, sw, stream);
-    if (ks == 1 && wn == 4 && cpw == 4) return launch_mode<4, 4, 1>(p, c, b, dump, sw, stream);
-    return hipErrorInvalidValue;
+    if (a.swiglu) return launch_gm<false, true>(p, c, a.scale_bf16, stream);
+    return a.partials ? launch_gm<true, false>(p, c, a.scale_bf16, stream)
+                      : launch_gm<false, false>(p, c, a.scale_bf16, stream);
 }
 
 }  // namespace w4a8

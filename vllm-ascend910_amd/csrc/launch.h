@@ -49,15 +49,14 @@ struct DecodeConfig {
     int CPW;
     int KW;
     int MT = 0;     // 16-row tiles per workgroup; 0 = all rows in one workgroup
-    int WIDE = 0;   // 1: the LDS-shared-activation kernel (gemm_wide.hip), 4 waves x CPW blocks
+    int WIDE = 0;   // 1: the LDS-shared-activation kernel (gemm_wide.hip); D/CPW/KW unused
 };
 DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream);
 
 // Decode GEMM for 16 < M <= 64 with the activations shared through LDS by
-// the wn column waves of a workgroup (cpw column blocks per wave, ks K splits
-// per workgroup; the built combinations are listed in gemm_wide.hip).
-hipError_t launch_gemm_wide(const GemmArgs& a, int wn, int cpw, int ks, hipStream_t stream);
+// the column waves of a workgroup (gemm_wide.hip).
+hipError_t launch_gemm_wide(const GemmArgs& a, hipStream_t stream);
 
 // Fused per-token quant + decode GEMM for one row on narrow N (unpadded K,
 // x 16-byte aligned with ldx % 8 == 0, and the decode heuristic's 2-block,
