@@ -93,11 +93,13 @@ int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_t
                 void* s_tiles, int64_t N, int64_t K, int64_t group, void* stream);
 
 /*
- * Workspace bytes the GEMM needs for (M, N, K, group); 0 when none, which is
- * every shape in this build (decode reduces its K split inside a workgroup,
- * prefill does not split K).  The workspace arguments of w4a8_gemm stay so
- * that a kernel needing scratch can be added without changing the ABI; a
- * caller passes the size this function returns (NULL/0 for 0).
+ * Workspace bytes the GEMM needs for (M, N, K, group); 0 when none.  Only
+ * decode shapes past 8 rows on narrow N (under 2047 column blocks of 16)
+ * with long K (at least 128 tiles of 128) use one: their K is split over
+ * workgroups whose fp32 sums, [splits, M, ceil(N/16)*16], a second kernel
+ * adds in split order.  A caller passes at least the size this function
+ * returns (NULL/0 for 0), 256-byte aligned; calls that overlap in time need
+ * workspaces of their own.  Prefill does not split K.
  */
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 

@@ -189,6 +189,10 @@ GEMM_CASES = [
     (48, 32768, 1024, 64, "bf16"),   # the same, group stride 64
     (20, 33000, 1920, 320, "f16"),   # the same, groups ending on either slab, ragged column groups
     (64, 32768, 3072, 512, "bf16"),  # the same, groups of four tiles
+    (20, 1000, 16384, 128, "f16"),   # narrow N, long K past 8 rows: K split over 16 workgroups, ragged N
+    (40, 512, 16384, 320, "bf16"),   # the same, split on 5-tile group-aligned units
+    (64, 256, 16384, 256, "f16"),    # the same, 64 rows, two tiles per group
+    (9, 2048, 16384, 64, "bf16"),    # the same, one row tile, group stride 64
     (17, 336, 1536, 192, "f16"),     # two 16-row groups, the second with one row; 11 column groups
     (40, 1000, 2048, 64, "bf16"),    # three row groups, ragged N
     (50, 200, 3072, 320, "f16"),     # row groups with groups ending on either slab
@@ -337,25 +341,25 @@ def test_gemm_qwq_prefill_16384_sample(pkg, dev, proj):
 
 
 def test_gemm_every_decode_row_count(pkg, dev):
-    """Every M from 1 to 64 on a wide (2048 column groups) and a narrow N: each picks a
-    built kernel variant (a missing one is a launch error) and matches the oracle on a
-    column sample."""
-    K, G = 512, 128
+    """Every M from 1 to 64 on a wide (2048 column groups) and a narrow N, and on a
+    narrow N with long K: each picks a built kernel variant (a missing one is a launch
+    error) and matches the oracle on a column sample."""
+    G = 128
     cols_rng = np.random.default_rng(9)
-    for N in (32768, 1000):
+    for N, K in ((32768, 512), (1000, 512), (1000, 16384)):
         xb_all, w, ws32, w_scale = make_problem(pkg, 64, N, K, G, seed=N)
         w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
         w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
         cols = np.sort(cols_rng.choice(N, 48, replace=False))
         for M in range(1, 65):
-            say(f"decode rows M={M} N={N}")
+            say(f"decode rows M={M} N={N} K={K}")
             xb = xb_all[:M]
             a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xb).to(dev), G)
             y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
             torch.cuda.synchronize()
             q_ref, s_ref = ow.quant_act_per_token(xb)
             y32, mag = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G, return_abs=True)
-            check_output(tensor_bf16_bits(y)[:, cols], y32, mag, ow.num_groups(K, G), f"M{M} N{N}")
+            check_output(tensor_bf16_bits(y)[:, cols], y32, mag, ow.num_groups(K, G), f"M{M} N{N} K{K}")
 
 
 def test_gemm_deterministic_and_stress(pkg, dev):
@@ -547,7 +551,8 @@ def test_workspace_reuse_across_shapes(pkg, dev):
     """Regression: consecutive split-K calls of different shapes share one
     workspace; a small-N call's partials must not leave non-zero counters for a
     later wide-N call."""
-    cases = [(16, 256, 4096, 128), (1, 32768, 1024, 128), (8, 1024, 8192, 256), (1, 32768, 1024, 128)]
+    cases = [(16, 256, 4096, 128), (1, 32768, 1024, 128), (8, 1024, 8192, 256), (1, 32768, 1024, 128),
+             (24, 1000, 16384, 128), (12, 512, 16384, 128), (24, 1000, 16384, 128)]
     for i, (M, N, K, G) in enumerate(cases):
         say(f"workspace reuse step {i}: M={M} N={N} K={K} G={G}")
         xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=40 + i)
@@ -584,6 +589,8 @@ SWIGLU_CASES = [
     # (M, I, K, G, scale dtype): merged gate/up weight of N = 2*I rows
     (16, 16384, 512, 128, "f16"),     # wide N past 8 rows: four column blocks per workgroup
     (33, 16384, 1024, 128, "bf16"),   # wide N past 16 rows: activations shared through LDS
+    (24, 16384, 512, 128, "bf16"),    # the same, two row tiles
+    (24, 1024, 16384, 128, "f16"),    # narrow N, long K: no SwiGLU pairs in the K-split layout
     (1, 512, 1024, 128, "f16"),
     (4, 1024, 2048, 64, "bf16"),
     (33, 256, 1024, 256, "bf16"),

@@ -490,12 +490,9 @@ hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool sbf16, hi
         if (mt == 2 && c.D == 4 && c.CPW == 1) return launch_v<2, 1, 4, MODE>(p, c.KW, sbf16, s);
     }
     if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, MODE>(p, c.KW, sbf16, s);
-    if (mt == 1 && c.D == 4 && c.CPW == 4) return launch_v<1, 4, 4, MODE>(p, c.KW, sbf16, s);
-    if (mt == 1 && c.D == 2 && c.CPW == 4) return launch_v<1, 4, 2, MODE>(p, c.KW, sbf16, s);
     if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, MODE>(p, c.KW, sbf16, s);
-    if (mt == 4 && c.D == 2 && c.CPW == 4) return launch_v<4, 4, 2, MODE>(p, c.KW, sbf16, s);
     return hipErrorInvalidValue;
 }
 
@@ -600,23 +597,19 @@ hipError_t launch_linear_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx
     return launch_fused(f.p, f.kw, f.lds, a.scale_bf16, stream);
 }
 
-int64_t decode_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
+namespace {
 
-DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
-    // Picked from a sweep over ring depth, column blocks per workgroup and
-    // waves per workgroup on MI355X at the QwQ-32B projection shapes.
+// The decode kernel's own plans (no wide layout): every shape has one.
+DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int mt = static_cast<int>((M + 15) / 16);
     const int KT = static_cast<int>(geom::k_tiles(K, group));
     const int64_t NB = geom::col_blocks(N);
     DecodeConfig c{4, 2, 4};
     const int64_t wgs = (NB + 1) / 2;
     if (wgs >= 1024) {
-        // Wide N already gives >= 1024 workgroups of all rows.  Past 8 rows
-        // the activations every workgroup reads weigh as much as its weights:
-        // four column blocks per workgroup halve that traffic.
-        if (mt == 1 && M > 8) c = DecodeConfig{2, 4, 1};
-        else if (mt == 1) c.KW = M <= 2 ? 2 : 1;
-        else c = DecodeConfig{2, 2, 1, 0, 1};   // > 16 rows: activations shared through LDS
+        // Wide N already gives >= 1024 workgroups of all rows.
+        if (mt == 1) c.KW = M <= 2 ? 2 : 1;
+        else c = DecodeConfig{4, 2, 1};
     } else if (mt == 1 || (mt == 2 && KT >= 128)) {
         // Split K so that each wave holds about one ring (4 tiles) of its
         // range -- but long K (>= 128 tiles) streams better with fewer, longer
@@ -632,8 +625,46 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     return c;
 }
 
+}  // namespace
+
+DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
+    // Picked from sweeps over ring depths, column blocks per workgroup, waves
+    // per workgroup and K splits on MI355X at the QwQ-32B projection shapes.
+    const int mt = static_cast<int>((M + 15) / 16);
+    const int KT = static_cast<int>(geom::k_tiles(K, group));
+    const int64_t NB = geom::col_blocks(N);
+    const int64_t wgs = (NB + 1) / 2;
+    DecodeConfig c{4, 2, 1};
+    if (M > 8 && wgs >= 1024) {
+        // Wide N past 8 rows: the activations each decode workgroup reads
+        // weigh as much as its weights; four column waves share them in LDS.
+        c.WIDE = mt == 1 ? kWide1x2 : (mt == 2 ? kWide2x2 : kWide4x2);
+        return c;
+    }
+    if (M > 8 && KT >= 128) {
+        // Narrow N, long K, past 8 rows: the same sharing with one column
+        // block per wave, K split over workgroups to reach ~640 of them
+        // (at least 8 tiles each).
+        c.WIDE = mt == 1 ? kWide1x1 : (mt == 2 ? kWide2x1 : kWide4x1);
+        const int64_t cg = (NB + 3) / 4;
+        const int64_t s = std::min<int64_t>({(640 + cg / 2) / cg, int64_t{16}, KT / 8});
+        c.SPLITS = static_cast<int>(std::max<int64_t>(s, 1));
+        return c;
+    }
+    return rows_config(M, N, K, group);
+}
+
+int64_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
+    const DecodeConfig c = decode_config(M, N, K, group);
+    return c.WIDE && c.SPLITS > 1 ? wide_workspace_bytes(M, N, K, group, c.SPLITS) : 0;
+}
+
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream) {
-    if (cfg.WIDE) return launch_gemm_wide(a, stream);
+    if (cfg.WIDE) {
+        if (!a.swiglu || wide_layout_pairs(cfg.WIDE)) return launch_gemm_wide(a, cfg.WIDE, cfg.SPLITS, stream);
+        // the one-block layouts have no SwiGLU pairs: the decode kernel's plan
+        return launch_gemm_decode_cfg(a, rows_config(a.M, a.N, a.K, a.group), stream);
+    }
     const DecodeParams p = make_params(a);
     if (a.swiglu) return dispatch<2>(p, cfg, a.scale_bf16, stream);
     return a.partials ? dispatch<1>(p, cfg, a.scale_bf16, stream) : dispatch<0>(p, cfg, a.scale_bf16, stream);

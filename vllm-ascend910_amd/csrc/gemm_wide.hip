@@ -1,19 +1,25 @@
-// Decode-shaped W4A8 GEMM for 16 < M <= 64 rows on wide N, the activations
-// shared through LDS.
+// Decode-shaped W4A8 GEMM for 16 < M <= 64 rows, the activations shared
+// through LDS.
 //
 // Same arithmetic as gemm_decode.hip (exact int32 per group on
 // v_mfma_i32_16x16x64_i8, fp32 fold with the group scale, token scale at the
 // end).  The decode kernel gives every wave all rows and its own K range, so
 // every workgroup streams the whole activation block from L2 for its few
 // column blocks: at 64 rows on gate_up that is twice the weight bytes.  Here a
-// workgroup of kWN column waves covers kWN * kCPW column blocks and walks all
-// of K; its waves share each 64-row activation tile, staged once into LDS
+// workgroup of kWN column waves covers kWN * kCPW column blocks; its waves
+// share each activation tile (16 * kMT rows x 128 K), staged once into LDS
 // (double-buffered, one barrier per tile) and read from there as MFMA
-// operands, while the weights stream straight to registers in a 2-deep ring
-// as in the decode kernel.  The accumulation order per output is the decode
-// kernel's with one K wave, so the sums are bit-identical to it.  (Measured
-// on the QwQ-32B shapes: on narrow N -- a few dozen workgroups -- adding K
-// splits reduced through LDS did not reach the decode kernel's row groups.)
+// operands.  The staging loads run kRA tiles ahead in registers and the
+// weights stream straight to registers in a kD-deep ring.
+//
+// A workgroup walks one K range of a group-aligned split (blockIdx.y).  With
+// one split it writes bf16 directly and the accumulation order per output is
+// the decode kernel's with one K wave.  With several splits each workgroup
+// writes its fp32 sums (before the token scale) to the workspace and
+// wide_reduce_kernel adds the splits in index order, applies the token scale
+// and rounds to bf16 -- the order the decode kernel's in-workgroup K split
+// reduces its waves in.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -23,11 +29,9 @@
 namespace w4a8 {
 namespace {
 
-constexpr int kMT = 4;                 // 16-row tiles: 64 rows
-constexpr int kD = 2;                  // weight ring depth (tiles)
 constexpr int kALS = 128 + 16;         // LDS row stride of a staged activation tile (bytes)
-constexpr int kATile = 16 * kMT * kALS;  // one staged tile
 constexpr uint32_t kOOBW = 0x80000000u;
+constexpr int kWaves = 4;              // column waves per workgroup
 
 struct WideParams {
     const int8_t* A;
@@ -38,20 +42,36 @@ struct WideParams {
     uint16_t* Y;
     int64_t ldy;
     int32_t* P;        // optional partial dump [NG, M, N]
+    float* R;          // splits > 1: fp32 sums [splits, M, ldr]
+    int64_t ldr;       // NB * 16
     int M, N, KT, NG, NB;
     int up_nb;         // SWIGLU: column blocks per half
     int nslab, spg, gshift;
+    int unit, units, splits;   // K split: tiles per group-aligned unit, units, workgroups along K
     uint32_t a_bytes, w_bytes, s_bytes;
 };
 
+// f(integral_constant<int, J>) for J = B .. E-1, in order.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 // GM: the group modes of gemm_decode.hip (0: stride 64, 3: stride 128,
 // 1: stride 128 * 2^gshift, 2: any other stride).
-// kWN column waves, kCPW 16-column blocks per wave.
-template <int kWN, int kCPW, int GM, bool SBF16, bool DUMP, bool SWIGLU>
+// kMT 16-row tiles, kWN column waves, kCPW 16-column blocks per wave, kD
+// weight ring depth, kRA activation tiles in flight.
+template <int kMT, int kWN, int kCPW, int kD, int kRA, int GM, bool SBF16, bool DUMP, bool SWIGLU>
 __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p) {
     static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
     constexpr int CG = SWIGLU ? kCPW / 2 : kCPW;   // output column blocks per wave
     constexpr int NS = (GM == 1 || GM == 3) ? 1 : 2;
+    constexpr int U = kD > kRA ? kD : kRA;           // unroll: every ring slot index is static
+    static_assert(U % kD == 0 && U % kRA == 0 && U % 2 == 0, "ring depths must divide the unroll");
+    constexpr int kATile = 16 * kMT * kALS;
     // two staged activation tiles
     __shared__ __attribute__((aligned(16))) int8_t la[2][kATile];
 
@@ -65,8 +85,14 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     const int nb0 = (static_cast<int>(blockIdx.x) * kWN + wn) * CG;
     auto block_of = [&](int c) { return (SWIGLU && c >= CG) ? nb0 + (c - CG) + p.up_nb : nb0 + c; };
 
-    // All of K: tiles [0, KT).
-    const int ta = 0, tb = p.KT, nit = p.KT;
+    // This workgroup's K range [ta, tb): group-aligned units split evenly
+    // (the host keeps splits <= units, so every range is non-empty).
+    const int ks = static_cast<int>(blockIdx.y);
+    const int ua = (ks * p.units) / p.splits;
+    const int ub = ((ks + 1) * p.units) / p.splits;
+    const int ta = ua * p.unit;
+    const int tb = min(p.KT, ub * p.unit);
+    const int nit = tb - ta;
 
     uint32_t wo[kCPW], so[kCPW];
 #pragma unroll
@@ -75,15 +101,19 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
         wo[c] = nb * static_cast<uint32_t>(p.KT) * 1024u + lane * 16u;
         so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + colq) * 2u;
     }
-    // Staging: 64 rows x 128 K = 512 units of 16 bytes, NU per lane; rows
-    // past M read zero.
-    constexpr int NU = 512 / (64 * kWN);
-    static_assert(NU * 64 * kWN == 512, "kWN must divide 8");
+    // Staging: 16 * kMT rows x 128 K = 128 * kMT units of 16 bytes, NU per
+    // lane; rows past M read zero.  With fewer units than lanes (one row
+    // tile) the waves past the units stage nothing (a wave-uniform test).
+    constexpr int kUnits = 128 * kMT;
+    constexpr int NU = (kUnits + 64 * kWN - 1) / (64 * kWN);
+    static_assert(NU * 64 * kWN == kUnits || (NU == 1 && kUnits % 64 == 0), "staging units per wave");
+    constexpr bool kAllStage = kUnits >= 64 * kWN;
+    const bool stager = kAllStage || wn * 64 < kUnits;
     uint32_t sg[NU];
     int sl[NU];
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
-        const int u = lane + 64 * (wn + kWN * j);
+        const int u = kAllStage ? lane + 64 * (wn + kWN * j) : min(lane + 64 * wn, kUnits - 1);
         const int r = u >> 3, c16 = (u & 7) * 16;
         sg[j] = r < p.M ? static_cast<uint32_t>(r) * static_cast<uint32_t>(p.lda) + c16 : kOOBW;
         sl[j] = r * kALS + c16;
@@ -97,14 +127,16 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
         return min(g, p.NG - 1);
     };
 
-    uint4 ra[2][NU];
+    uint4 ra[kRA][NU];
     auto stage_load = [&](int t, uint4 (&r)[NU]) {
+        if (!kAllStage && !stager) return;
         // tiles past the end stage the last tile again (nothing reads them)
         const auto rs = make_rsrc_at(p.A, static_cast<uint32_t>(min(t, p.KT - 1)) * 128u, p.a_bytes);
 #pragma unroll
         for (int j = 0; j < NU; ++j) r[j] = buf_load16(rs, sg[j]);
     };
     auto stage_store = [&](int buf, const uint4 (&r)[NU]) {
+        if (!kAllStage && !stager) return;
 #pragma unroll
         for (int j = 0; j < NU; ++j) *reinterpret_cast<uint4*>(&la[buf][sl[j]]) = r[j];
     };
@@ -134,7 +166,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
             for (int i = 0; i < 4; ++i) acc[mt][c][i] = 0.0f;
         }
 
-    auto fold = [&](int g, bool own, const uint32_t (&sc)[kCPW][NS], int j) __attribute__((always_inline)) {
+    auto fold = [&](int g, const uint32_t (&sc)[kCPW][NS], int j) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < kCPW; ++c) {
             const float ws = scale_to_f32<SBF16>(sc[c][j]);
@@ -145,7 +177,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int row = mt * 16 + rowq + i;
-                        if (own && row < p.M && col < p.N && g < p.NG)
+                        if (row < p.M && col < p.N && g < p.NG)
                             p.P[(static_cast<int64_t>(g) * p.M + row) * p.N + col] = P[mt][c][i] >> 4;
                     }
                 }
@@ -156,28 +188,33 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
         }
     };
 
-    // ---- prologue: tile ta staged in buffer 0, ta+1 in registers, the ring in flight
+    // ---- prologue: tiles ta .. ta+kRA-1 in flight to the staging registers,
+    // the weight ring filled, tile ta staged in buffer 0
     stage_load(ta, ra[0]);
-    stage_load(ta + 1, ra[1]);
 #pragma unroll
     for (int s = 0; s < kD; ++s) load_slot(s, ta + s);
+#pragma unroll
+    for (int r = 1; r < kRA; ++r) stage_load(ta + r, ra[r]);
     stage_store(0, ra[0]);
     __syncthreads();
 
-    // One tile: u = iteration parity (the staging registers and the ring slot).
-    auto step = [&](int i, int u) __attribute__((always_inline)) {
+    // One tile t = ta + i; J = i mod U names the ring slots and the LDS buffer.
+    auto step = [&](int i, auto jc) __attribute__((always_inline)) {
+        constexpr int J = decltype(jc)::value;
+        constexpr int WS = J % kD;
         const int t = ta + i;
-        stage_load(t + 2, ra[u]);
+        // the staging slot of tile t is free again (tile t is in LDS)
+        stage_load(t + kRA, ra[J % kRA]);
         uint32_t sc[kCPW][NS];
 #pragma unroll
         for (int c = 0; c < kCPW; ++c)
 #pragma unroll
-            for (int j = 0; j < NS; ++j) sc[c][j] = sb[u][c][j];
+            for (int q = 0; q < NS; ++q) sc[c][q] = sb[WS][c][q];
         v4i b[kCPW][2];
 #pragma unroll
-        for (int c = 0; c < kCPW; ++c) unpack_tile_lane(wb[u][c], b[c][0], b[c][1]);
-        load_slot(u, t + kD);
-        const int8_t* ab = &la[u][0] + colq * kALS + (lane >> 4) * 16;
+        for (int c = 0; c < kCPW; ++c) unpack_tile_lane(wb[WS][c], b[c][0], b[c][1]);
+        load_slot(WS, t + kD);
+        const int8_t* ab = &la[J & 1][0] + colq * kALS + (lane >> 4) * 16;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const bool fresh = GM == 0 || (GM == 3 && h == 0);
@@ -188,38 +225,36 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
                 for (int c = 0; c < kCPW; ++c) P[mt][c] = mfma16(a, b[c][h], fresh ? v4i{0, 0, 0, 0} : P[mt][c]);
             }
             if constexpr (GM == 0) {
-                fold(2 * t + h, t < tb, sc, h);
+                fold(2 * t + h, sc, h);
             } else if constexpr (GM == 3) {
-                if (h == 1) fold(t, t < tb, sc, 0);
+                if (h == 1) fold(t, sc, 0);
             } else if constexpr (GM == 1) {
-                if (h == 1 && (((t + 1) & ((1 << p.gshift) - 1)) == 0 || t == p.KT - 1))
-                    fold(t >> p.gshift, t < tb, sc, 0);
+                if (h == 1 && (((t + 1) & ((1 << p.gshift) - 1)) == 0 || t == p.KT - 1)) fold(t >> p.gshift, sc, 0);
             } else {
                 const int sgi = 2 * t + h;
-                if (sgi < p.nslab && (((sgi + 1) % p.spg) == 0 || sgi == p.nslab - 1))
-                    fold(sgi / p.spg, t < tb, sc, h);
+                if (sgi < p.nslab && (((sgi + 1) % p.spg) == 0 || sgi == p.nslab - 1)) fold(sgi / p.spg, sc, h);
             }
         }
         // tile t+1 into the other buffer (free: every wave finished tile t-1)
-        stage_store(u ^ 1, ra[u ^ 1]);
+        stage_store((J + 1) & 1, ra[(J + 1) % kRA]);
         __syncthreads();
     };
     int i = 0;
-    for (; i + 2 <= nit; i += 2) {
-        step(i, 0);
-        step(i + 1, 1);
-    }
-    if (i < nit) step(i, 0);
+    for (; i + U <= nit; i += U) static_for<0, U>([&](auto jc) { step(i + decltype(jc)::value, jc); });
+    static_for<0, U - 1>([&](auto jc) {
+        if (i + decltype(jc)::value < nit) step(i + decltype(jc)::value, jc);
+    });
 
-    // ---- epilogue: token scale, bf16 (or the SwiGLU pair)
+    // ---- epilogue: token scale, bf16 (or the SwiGLU pair); fp32 sums to
+    // the workspace when K is split
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int row = mt * 16 + rowq + q;
             if (row >= p.M) continue;
-            const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
             if constexpr (SWIGLU) {
+                const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
 #pragma unroll
                 for (int c = 0; c < CG; ++c) {
                     const int col = block_of(c) * 16 + colq;
@@ -227,7 +262,15 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
                         p.Y[static_cast<int64_t>(row) * p.ldy + col] =
                             static_cast<uint16_t>(swiglu_bf16_bits(acc[mt][c][q] * ts, acc[mt][c + CG][q] * ts));
                 }
+            } else if (p.splits > 1) {
+                float* r = p.R + (static_cast<int64_t>(ks) * p.M + row) * p.ldr;
+#pragma unroll
+                for (int c = 0; c < kCPW; ++c) {
+                    const int col = block_of(c) * 16 + colq;
+                    if (col < p.N) r[col] = acc[mt][c][q];
+                }
             } else {
+                const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
 #pragma unroll
                 for (int c = 0; c < kCPW; ++c) {
                     const int col = block_of(c) * 16 + colq;
@@ -239,6 +282,41 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
         }
 }
 
+// y[m, n] = bf16((R[0, m, n] + R[1, m, n] + ...) * token scale), four
+// columns per thread; R rows are ldr (a multiple of 16) floats apart and
+// columns from N to ldr are never written.
+__global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restrict__ R, int64_t ldr,
+                                                          const uint16_t* a_scale, uint16_t* Y, int64_t ldy, int M,
+                                                          int N, int splits) {
+    const int n4 = static_cast<int>(ldr >> 2);
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= static_cast<int64_t>(M) * n4) return;
+    const int row = static_cast<int>(idx / n4);
+    const int col = static_cast<int>(idx - static_cast<int64_t>(row) * n4) * 4;
+    if (col >= N) return;
+    const int64_t plane = static_cast<int64_t>(M) * ldr;
+    const float* r = R + static_cast<int64_t>(row) * ldr + col;
+    float4 s = *reinterpret_cast<const float4*>(r);
+    for (int k = 1; k < splits; ++k) {
+        const float4 v = *reinterpret_cast<const float4*>(r + k * plane);
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+    }
+    const float ts = bf16_bits_to_f32(a_scale[row]) * 0.0625f;
+    const uint32_t lo = f32_to_bf16_bits(s.x * ts) | (f32_to_bf16_bits(s.y * ts) << 16);
+    const uint32_t hi = f32_to_bf16_bits(s.z * ts) | (f32_to_bf16_bits(s.w * ts) << 16);
+    uint16_t* y = Y + static_cast<int64_t>(row) * ldy + col;
+    if (col + 4 <= N && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) {
+        *reinterpret_cast<uint2*>(y) = make_uint2(lo, hi);
+    } else {
+        const uint16_t v[4] = {static_cast<uint16_t>(lo), static_cast<uint16_t>(lo >> 16), static_cast<uint16_t>(hi),
+                               static_cast<uint16_t>(hi >> 16)};
+        for (int c = 0; c < 4 && col + c < N; ++c) y[c] = v[c];
+    }
+}
+
 int group_mode_of(int spg) {
     if (spg == 1) return 0;
     if (spg == 2) return 3;
@@ -246,31 +324,36 @@ int group_mode_of(int spg) {
     return 2;
 }
 
-constexpr int kWaves = 4;   // column waves per workgroup
-constexpr int kBlocks = 2;  // column blocks per wave
+int gcd_w(int a, int b) {
+    while (b) {
+        const int t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
+}
 
-template <int GM, bool DUMP, bool SWIGLU>
+template <int kMT, int kCPW, int kD, int kRA, int GM, bool DUMP, bool SWIGLU>
 hipError_t launch_g(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
-    const dim3 grid(static_cast<unsigned>(cgroups)), block(64 * kWaves);
-    if (sbf16) gemm_wide_kernel<kWaves, kBlocks, GM, true, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
-    else gemm_wide_kernel<kWaves, kBlocks, GM, false, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
+    const dim3 grid(static_cast<unsigned>(cgroups), static_cast<unsigned>(p.splits)), block(64 * kWaves);
+    if (sbf16) gemm_wide_kernel<kMT, kWaves, kCPW, kD, kRA, GM, true, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
+    else gemm_wide_kernel<kMT, kWaves, kCPW, kD, kRA, GM, false, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
     return hipGetLastError();
 }
 
-template <bool DUMP, bool SWIGLU>
+template <int kMT, int kCPW, int kD, int kRA, bool DUMP, bool SWIGLU>
 hipError_t launch_gm(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
     switch (group_mode_of(p.spg)) {
-        case 0: return launch_g<0, DUMP, SWIGLU>(p, cgroups, sbf16, s);
-        case 1: return launch_g<1, DUMP, SWIGLU>(p, cgroups, sbf16, s);
-        case 3: return launch_g<3, DUMP, SWIGLU>(p, cgroups, sbf16, s);
-        default: return launch_g<2, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 0: return launch_g<kMT, kCPW, kD, kRA, 0, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 1: return launch_g<kMT, kCPW, kD, kRA, 1, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 3: return launch_g<kMT, kCPW, kD, kRA, 3, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        default: return launch_g<kMT, kCPW, kD, kRA, 2, DUMP, SWIGLU>(p, cgroups, sbf16, s);
     }
 }
 
-}  // namespace
-
-hipError_t launch_gemm_wide(const GemmArgs& a, hipStream_t stream) {
-    if (a.M <= 0 || a.M > 16 * kMT) return hipErrorInvalidValue;
+// Parameters of one call; splits is clamped to the group-aligned units (and
+// to 1 for the SwiGLU epilogue, which needs the whole sum).
+WideParams make_wide_params(const GemmArgs& a, int splits) {
     WideParams p{};
     p.A = a.a_q;
     p.lda = a.lda;
@@ -290,15 +373,75 @@ hipError_t launch_gemm_wide(const GemmArgs& a, hipStream_t stream) {
     p.spg = static_cast<int>(geom::group_stride(a.group) / 64);
     p.gshift = 0;
     while ((2 << p.gshift) < p.spg) ++p.gshift;
+    p.unit = (2 * p.spg / gcd_w(2, p.spg)) / 2;   // lcm(2, spg) slabs, in tiles
+    p.units = (p.KT + p.unit - 1) / p.unit;
+    p.splits = a.swiglu ? 1 : std::max(1, std::min(splits, p.units));
+    p.ldr = static_cast<int64_t>(p.NB) * 16;
     p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + geom::kpad(a.K, a.group));
     p.w_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.KT) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.NG) * 16 * 2);
-    const int per_wg = kWaves * kBlocks;
+    return p;
+}
+
+int64_t split_bytes(const WideParams& p) {
+    return p.splits > 1 ? static_cast<int64_t>(p.splits) * p.M * p.ldr * 4 : 0;
+}
+
+// One call with an explicit layout: kMT row tiles, kCPW column blocks per
+// wave, ring depths kD / kRA, p.splits workgroups along K.
+template <int kMT, int kCPW, int kD, int kRA>
+hipError_t launch_wide_v(const GemmArgs& a, WideParams p, hipStream_t stream) {
+    if (a.M <= 0 || a.M > 16 * kMT) return hipErrorInvalidValue;
+    if (a.swiglu && kCPW % 2 != 0) return hipErrorInvalidValue;
+    const int64_t need = split_bytes(p);
+    if (need > 0) {
+        if (a.workspace == nullptr || a.workspace_bytes < need) return hipErrorInvalidValue;
+        p.R = static_cast<float*>(a.workspace);
+    }
+    const int per_wg = kWaves * kCPW;
     const int64_t cg = a.swiglu ? geom::ceil_div(p.up_nb, per_wg / 2) : geom::ceil_div(p.NB, per_wg);
     const int c = static_cast<int>(cg);
-    if (a.swiglu) return launch_gm<false, true>(p, c, a.scale_bf16, stream);
-    return a.partials ? launch_gm<true, false>(p, c, a.scale_bf16, stream)
-                      : launch_gm<false, false>(p, c, a.scale_bf16, stream);
+    hipError_t e;
+    if (a.swiglu) {
+        if constexpr (kCPW % 2 == 0) e = launch_gm<kMT, kCPW, kD, kRA, false, true>(p, c, a.scale_bf16, stream);
+        else return hipErrorInvalidValue;
+    } else if (a.partials) e = launch_gm<kMT, kCPW, kD, kRA, true, false>(p, c, a.scale_bf16, stream);
+    else e = launch_gm<kMT, kCPW, kD, kRA, false, false>(p, c, a.scale_bf16, stream);
+    if (e != hipSuccess || p.splits == 1) return e;
+    const int64_t n = static_cast<int64_t>(p.M) * (p.ldr / 4);
+    wide_reduce_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy,
+                                                                                   p.M, p.N, p.splits);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// The layouts launch_gemm_wide builds: (row tiles, column blocks per wave,
+// weight ring, activation ring), measured best for their row counts on
+// MI355X at the QwQ-32B shapes.
+hipError_t launch_gemm_wide(const GemmArgs& a, int layout, int splits, hipStream_t stream) {
+    const WideParams p = make_wide_params(a, splits);
+    switch (layout) {
+        case kWide1x2: return launch_wide_v<1, 2, 2, 4>(a, p, stream);
+        case kWide2x2: return launch_wide_v<2, 2, 2, 2>(a, p, stream);
+        case kWide4x2: return launch_wide_v<4, 2, 2, 4>(a, p, stream);
+        case kWide1x1: return launch_wide_v<1, 1, 4, 4>(a, p, stream);
+        case kWide2x1: return launch_wide_v<2, 1, 4, 4>(a, p, stream);
+        case kWide4x1: return launch_wide_v<4, 1, 2, 2>(a, p, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool wide_layout_pairs(int layout) { return layout == kWide1x2 || layout == kWide2x2 || layout == kWide4x2; }
+
+int64_t wide_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int splits) {
+    GemmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.group = group;
+    a.lda = geom::kpad(K, group);
+    return split_bytes(make_wide_params(a, splits));
 }
 
 }  // namespace w4a8

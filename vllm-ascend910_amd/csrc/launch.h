@@ -48,15 +48,29 @@ struct DecodeConfig {
     int D;
     int CPW;
     int KW;
-    int MT = 0;     // 16-row tiles per workgroup; 0 = all rows in one workgroup
-    int WIDE = 0;   // 1: the LDS-shared-activation kernel (gemm_wide.hip); D/CPW/KW unused
+    int MT = 0;       // 16-row tiles per workgroup; 0 = all rows in one workgroup
+    int WIDE = 0;     // a WideLayout: the LDS-shared-activation kernel (gemm_wide.hip); D/CPW/KW/MT unused
+    int SPLITS = 1;   // WIDE: workgroups along K (fp32 sums in the workspace, reduced by a second kernel)
 };
 DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream);
 
-// Decode GEMM for 16 < M <= 64 with the activations shared through LDS by
-// the column waves of a workgroup (gemm_wide.hip).
-hipError_t launch_gemm_wide(const GemmArgs& a, hipStream_t stream);
+// Decode GEMM with the activations shared through LDS by the four column
+// waves of a workgroup (gemm_wide.hip).  Layouts: 16-row tiles x 16-column
+// blocks per wave; the x2 layouts also build the SwiGLU epilogue.
+enum WideLayout : int {
+    kWideNone = 0,
+    kWide1x2 = 1,   // up to 16 rows
+    kWide2x2 = 2,   // up to 32 rows
+    kWide4x2 = 3,   // up to 64 rows
+    kWide1x1 = 4,
+    kWide2x1 = 5,
+    kWide4x1 = 6,
+};
+hipError_t launch_gemm_wide(const GemmArgs& a, int layout, int splits, hipStream_t stream);
+bool wide_layout_pairs(int layout);
+// Workspace of a call with `splits` K splits (0 for one split).
+int64_t wide_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int splits);
 
 // Fused per-token quant + decode GEMM for one row on narrow N (unpadded K,
 // x 16-byte aligned with ldx % 8 == 0, and the decode heuristic's 2-block,

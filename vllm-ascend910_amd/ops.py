@@ -67,7 +67,7 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
 
 
 # One workspace per (device, stream), allocated only when the library asks
-# for one (no shape does at present); it only grows.  Concurrent calls on one
+# for one (decode shapes that split K over workgroups); it only grows.  Concurrent calls on one
 # stream are stream-ordered, so sharing per stream is safe.
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
 
