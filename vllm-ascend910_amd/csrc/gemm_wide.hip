@@ -214,15 +214,23 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
 #pragma unroll
         for (int c = 0; c < kCPW; ++c) unpack_tile_lane(wb[WS][c], b[c][0], b[c][1]);
         load_slot(WS, t + kD);
+        // Every A operand of the tile read from LDS before the first MFMA
+        // (left to itself the compiler reads the second half one operand at
+        // a time, each read waited for before its MFMAs).
         const int8_t* ab = &la[J & 1][0] + colq * kALS + (lane >> 4) * 16;
+        v4i av[2][kMT];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int mt = 0; mt < kMT; ++mt) av[h][mt] = *reinterpret_cast<const v4i*>(ab + mt * 16 * kALS + h * 64);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const bool fresh = GM == 0 || (GM == 3 && h == 0);
 #pragma unroll
             for (int mt = 0; mt < kMT; ++mt) {
-                const v4i a = *reinterpret_cast<const v4i*>(ab + mt * 16 * kALS + h * 64);
 #pragma unroll
-                for (int c = 0; c < kCPW; ++c) P[mt][c] = mfma16(a, b[c][h], fresh ? v4i{0, 0, 0, 0} : P[mt][c]);
+                for (int c = 0; c < kCPW; ++c)
+                    P[mt][c] = mfma16(av[h][mt], b[c][h], fresh ? v4i{0, 0, 0, 0} : P[mt][c]);
             }
             if constexpr (GM == 0) {
                 fold(2 * t + h, sc, h);
