@@ -303,7 +303,9 @@ def main():
     if traffic_src.exists():
         traffic = round(json.loads(traffic_src.read_text())["avg_traffic_bytes"])
     result["roofline"] = {
-        "kernel": "decode W4A8 GEMM: gemm_decode_kernel, gemm_wide_kernel for gate_up M=64 (all 16 configs[1] shapes, cold)",
+        "kernel": ("decode W4A8 GEMM per call: gemm_decode_kernel; gemm_wide_kernel for gate_up and down at M=16 "
+                   "and 64, down followed by wide_reduce_kernel (K split over 8 workgroups) -- all 16 configs[1] "
+                   "shapes, cold"),
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
         "per_launch_bytes_avg": round(tot_bytes / len(shapes)), "launch_us_avg": round(tot_us / len(shapes), 3),
@@ -507,17 +509,22 @@ def trace_summary(db):
     print("\nPer stream (the per-shape timings run on a stream of their own, each decode shape "
           "the same number of times):\n\n| kernel | stream | calls | avg us |\n|---|---|---:|---:|")
     for (k, st), d in sorted(by_stream.items()):
-        if k.startswith(("gemm_", "linear_", "quant_")):
+        if k.startswith(("gemm_", "linear_", "quant_", "wide_")):
             print(f"| {k} | {st} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
-    both = collections.defaultdict(list)
+    # One decode GEMM call = one gemm_decode_kernel or gemm_wide_kernel
+    # dispatch, plus a wide_reduce_kernel when it splits K over workgroups.
+    calls, total = collections.Counter(), collections.Counter()
     for (k, st), d in by_stream.items():
         if k in ("gemm_decode_kernel", "gemm_wide_kernel"):
-            both[st] += d
-    for st, d in sorted(both.items()):
-        print(f"| decode GEMM (gemm_decode_kernel + gemm_wide_kernel) | {st} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
+            calls[st] += len(d)
+        if k in ("gemm_decode_kernel", "gemm_wide_kernel", "wide_reduce_kernel"):
+            total[st] += sum(d)
+    for st in sorted(calls):
+        print(f"| decode GEMM per call (gemm_decode_kernel / gemm_wide_kernel + wide_reduce_kernel) | {st} | "
+              f"{calls[st]} | {total[st] / calls[st] / 1e3:.3f} |")
     print("\n| kernel | grid x (threads) | grid y | workgroup | calls | avg us |\n|---|---:|---:|---:|---:|---:|")
     for (k, gx, gy, wx), d in sorted(by_shape.items()):
-        if k.startswith(("gemm_", "linear_", "quant_")):
+        if k.startswith(("gemm_", "linear_", "quant_", "wide_")):
             print(f"| {k} | {gx} | {gy} | {wx} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
 
 
@@ -537,9 +544,18 @@ def pmc_summary(fetch_db, write_db, out_json=None):
     cal_kib = 256 * 1024
     ff = cal_kib / [v for n, v in fetch if is_copy(n)][-1]
     fw = cal_kib / [v for n, v in write if is_copy(n)][-1]
-    is_gemm = lambda n: "gemm_decode_kernel" in n or "gemm_wide_kernel" in n   # noqa: E731
-    gf = [v for n, v in fetch if is_gemm(n)][-16:]
-    gw = [v for n, v in write if is_gemm(n)][-16:]
+    def per_call(events):
+        # a call = its gemm_decode_kernel / gemm_wide_kernel dispatch plus the
+        # wide_reduce_kernel that follows it when K is split over workgroups
+        out = []
+        for n, v in events:
+            if "gemm_decode_kernel" in n or "gemm_wide_kernel" in n:
+                out.append(v)
+            elif "wide_reduce_kernel" in n and out:
+                out[-1] += v
+        return out[-16:]
+
+    gf, gw = per_call(fetch), per_call(write)
     shapes = [(M, p) for M in DECODE_MS for p in PROJS]
     import __graft_entry__ as ge
     synth = ge.package().synth
