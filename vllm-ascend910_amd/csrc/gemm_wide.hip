@@ -32,6 +32,7 @@ namespace {
 constexpr int kALS = 128 + 16;         // LDS row stride of a staged activation tile (bytes)
 constexpr uint32_t kOOBW = 0x80000000u;
 constexpr int kWaves = 4;              // column waves per workgroup
+constexpr int kMaxSplits = 16;         // K splits over workgroups, at most
 
 struct WideParams {
     const int8_t* A;
@@ -304,13 +305,21 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
     if (col >= N) return;
     const int64_t plane = static_cast<int64_t>(M) * ldr;
     const float* r = R + static_cast<int64_t>(row) * ldr + col;
-    float4 s = *reinterpret_cast<const float4*>(r);
-    for (int k = 1; k < splits; ++k) {
-        const float4 v = *reinterpret_cast<const float4*>(r + k * plane);
-        s.x += v.x;
-        s.y += v.y;
-        s.z += v.z;
-        s.w += v.w;
+    // all loads first (one memory latency, not one per split), then the sum
+    // in split order
+    float4 v[kMaxSplits];
+#pragma unroll
+    for (int k = 0; k < kMaxSplits; ++k)
+        v[k] = k < splits ? *reinterpret_cast<const float4*>(r + k * plane) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 s = v[0];
+#pragma unroll
+    for (int k = 1; k < kMaxSplits; ++k) {
+        if (k < splits) {
+            s.x += v[k].x;
+            s.y += v[k].y;
+            s.z += v[k].z;
+            s.w += v[k].w;
+        }
     }
     const float ts = bf16_bits_to_f32(a_scale[row]) * 0.0625f;
     const uint32_t lo = f32_to_bf16_bits(s.x * ts) | (f32_to_bf16_bits(s.y * ts) << 16);
@@ -383,7 +392,7 @@ WideParams make_wide_params(const GemmArgs& a, int splits) {
     while ((2 << p.gshift) < p.spg) ++p.gshift;
     p.unit = (2 * p.spg / gcd_w(2, p.spg)) / 2;   // lcm(2, spg) slabs, in tiles
     p.units = (p.KT + p.unit - 1) / p.unit;
-    p.splits = a.swiglu ? 1 : std::max(1, std::min(splits, p.units));
+    p.splits = a.swiglu ? 1 : std::max(1, std::min({splits, p.units, kMaxSplits}));
     p.ldr = static_cast<int64_t>(p.NB) * 16;
     p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + geom::kpad(a.K, a.group));
     p.w_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.KT) * geom::kTileBytes);
