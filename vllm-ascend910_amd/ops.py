@@ -77,7 +77,8 @@ def _workspace(dev: torch.device, need: int) -> torch.Tensor:
            torch.cuda.current_stream(dev).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+        # no clearing needed: the split GEMM writes every sum the reduce reads
+        ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
     return ws
 
