@@ -562,6 +562,50 @@ def test_workspace_reuse_across_shapes(pkg, dev):
         check_output(tensor_bf16_bits(y), y32, mag, ow.num_groups(K, G), f"reuse step {i}")
 
 
+def test_split_k_gemm_in_a_graph(pkg, dev):
+    """A call that splits K over workgroups (two kernels and a workspace) captured in a
+    HIP graph: every replay, with eager GEMMs of other shapes on the same stream in
+    between, equals the eager result bit for bit; so does a graph of w4a8_linear."""
+    M, N, K, G = 24, 1000, 16384, 128
+    say(f"split-K graph M={M} N={N} K={K} G={G}")
+    assert pkg._abi.lib().w4a8_gemm_workspace_bytes(M, N, K, G) > 0
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=77)
+    w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+    x = bf16_bits_tensor(xb).to(dev)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, G)
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        eager = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+        eager_lin = torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+        y_lin = torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, G)
+    # a shape between the replays that splits K with a larger workspace: the stream's
+    # workspace grows, and the one the graph captured must stay allocated
+    lib = pkg._abi.lib()
+    assert lib.w4a8_gemm_workspace_bytes(64, 2048, 16384, 256) > lib.w4a8_gemm_workspace_bytes(M, N, K, G)
+    xo, wo, _, wso = make_problem(pkg, 64, 2048, 16384, 256, seed=78)
+    wt2, st2 = torch.ops.npu.w4a8_repack(torch.from_numpy(ow.pack_grouped(wo, 256)).to(dev), wso.to(dev), 16384, 256)
+    aq2, as2 = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xo).to(dev), 256)
+    for r in range(4):
+        with torch.cuda.stream(s):
+            y.zero_()
+            y_lin.zero_()
+            g.replay()
+            other = torch.ops.npu.w4a8_gemm(aq2, as2, wt2, st2, 2048, 16384, 256)
+            junk = torch.full((1 << 22,), 7, dtype=torch.int32, device=dev)   # reuses freed memory, if any
+        torch.cuda.synchronize()
+        del other, junk
+        assert torch.equal(y, eager), f"replay {r}: split-K GEMM differs from eager"
+        assert torch.equal(y_lin, eager_lin), f"replay {r}: linear differs from eager"
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    y32, mag = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, return_abs=True)
+    check_output(tensor_bf16_bits(eager), y32, mag, ow.num_groups(K, G), "split-K eager")
+
+
 # ------------------------------------------------------------------ SwiGLU epilogue
 def check_swiglu(got_bits: np.ndarray, exp_bits: np.ndarray, min_equal: float, tag: str) -> None:
     """Every output within one bf16 ulp of the expected SwiGLU value and at least

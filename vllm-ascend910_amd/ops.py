@@ -70,6 +70,10 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
 # for one (decode shapes that split K over workgroups); it only grows.  Concurrent calls on one
 # stream are stream-ordered, so sharing per stream is safe.
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+# Workspaces replaced by a larger one stay allocated: a captured HIP graph
+# keeps the address it was captured with, so that memory must never return
+# to the caching allocator.
+_RETIRED: list = []
 
 
 def _workspace(dev: torch.device, need: int) -> torch.Tensor:
@@ -77,6 +81,8 @@ def _workspace(dev: torch.device, need: int) -> torch.Tensor:
            torch.cuda.current_stream(dev).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
+        if ws is not None:
+            _RETIRED.append(ws)
         # no clearing needed: the split GEMM writes every sum the reduce reads
         ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
