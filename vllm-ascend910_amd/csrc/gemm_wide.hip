@@ -1,5 +1,6 @@
-// Decode-shaped W4A8 GEMM for 16 < M <= 64 rows, the activations shared
-// through LDS.
+// Decode-shaped W4A8 GEMM for up to 64 rows with the activations shared
+// through LDS (the decode heuristic sends it 9-64 rows on wide N, and on
+// narrow N with long K).
 //
 // Same arithmetic as gemm_decode.hip (exact int32 per group on
 // v_mfma_i32_16x16x64_i8, fp32 fold with the group scale, token scale at the
