@@ -338,6 +338,9 @@ def main():
             log(f"  prefill {p:13s} M={M:5d}: {us:9.1f} us {tops:7.1f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)")
             del x, a_q, a_s
     result["prefill_shapes"] = prefill
+    if prefill:
+        # right after the MFMA-bound prefill loop: the clock that kernel ran at
+        result["gpu_clocks"]["after_prefill"] = gpu_clocks()
 
     # ---------------------------------------------------------------- mid-group variants
     if args.config4:
