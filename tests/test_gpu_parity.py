@@ -548,9 +548,9 @@ def test_vllm_plugin_methods_apply(pkg, dev):
 
 
 def test_workspace_reuse_across_shapes(pkg, dev):
-    """Regression: consecutive split-K calls of different shapes share one
-    workspace; a small-N call's partials must not leave non-zero counters for a
-    later wide-N call."""
+    """Consecutive calls of different shapes, some splitting K over workgroups
+    (fp32 sums in the stream's one workspace, which grows between them), each
+    match the oracle: no call reads what an earlier one left there."""
     cases = [(16, 256, 4096, 128), (1, 32768, 1024, 128), (8, 1024, 8192, 256), (1, 32768, 1024, 128),
              (24, 1000, 16384, 128), (12, 512, 16384, 128), (24, 1000, 16384, 128)]
     for i, (M, N, K, G) in enumerate(cases):
