@@ -44,7 +44,8 @@ enum w4a8_status {
 /* Scale dtype codes. */
 enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
 
-/* Library ABI version (bumped on any signature change). */
+/* Library ABI version (bumped on any signature or contract change: 4 = the
+ * first build whose GEMM asks a workspace of some decode shapes). */
 int w4a8_abi_version(void);
 
 /* Message for the calling thread's last failed call ("" if none). */

@@ -15,7 +15,7 @@ from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "_lib" / "libw4a8_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1

@@ -121,7 +121,7 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 3; }
+int w4a8_abi_version(void) { return 4; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
