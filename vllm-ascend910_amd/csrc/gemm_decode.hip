@@ -124,6 +124,15 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     // Rows [m0, m0 + R) of the activations (more than R rows are split over
     // row groups that share the column blocks).
     const int m0 = rgi * R;
+    // Token scales of this workgroup's rows: requested here, parked in LDS
+    // just before the epilogue's barrier (a load issued in the epilogue would
+    // add a memory round trip to the tail of every call).
+    __shared__ uint32_t tsc[R];
+    uint32_t ts_bits = 0;
+    if constexpr (!QF) {
+        if (static_cast<int>(threadIdx.x) < R && m0 + static_cast<int>(threadIdx.x) < p.M)
+            ts_bits = p.a_scale[m0 + threadIdx.x];
+    }
 
     // This wave's tile range [ta, tb).
     const int ua = (wave * p.units) / kw;
@@ -382,6 +391,9 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
         for (int c = 0; c < CPW; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i) red[wave * R * C + (mt * 16 + rowq + i) * C + c * 16 + colq] = acc[mt][c][i];
+    if constexpr (!QF) {
+        if (static_cast<int>(threadIdx.x) < R) tsc[threadIdx.x] = ts_bits;
+    }
     __syncthreads();
     if constexpr (SWIGLU) {
         constexpr int CH = C / 2;
@@ -395,7 +407,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
                 sg += red[w * R * C + row * C + cc];
                 su += red[w * R * C + row * C + CH + cc];
             }
-            const float ts = bf16_bits_to_f32(p.a_scale[m0 + row]) * 0.0625f;
+            const float ts = bf16_bits_to_f32(tsc[row]) * 0.0625f;
             p.Y[static_cast<int64_t>(m0 + row) * p.ldy + col] = static_cast<uint16_t>(swiglu_bf16_bits(sg * ts, su * ts));
         }
     } else {
@@ -405,7 +417,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
             if (m0 + row >= p.M || col >= p.N) continue;
             float sum = red[e];
             for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
-            const uint32_t tsb = QF ? reinterpret_cast<const uint32_t*>(lds + lq_s)[row] : p.a_scale[m0 + row];
+            const uint32_t tsb = QF ? reinterpret_cast<const uint32_t*>(lds + lq_s)[row] : tsc[row];
             const float ts = bf16_bits_to_f32(tsb) * 0.0625f;
             p.Y[static_cast<int64_t>(m0 + row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
         }

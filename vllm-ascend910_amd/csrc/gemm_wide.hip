@@ -87,6 +87,13 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     const int nb0 = (static_cast<int>(blockIdx.x) * kWN + wn) * CG;
     auto block_of = [&](int c) { return (SWIGLU && c >= CG) ? nb0 + (c - CG) + p.up_nb : nb0 + c; };
 
+    // Token scales of the rows: requested here, parked in LDS after the K
+    // loop (loads issued in the epilogue would add a memory round trip to
+    // the tail of every call).
+    __shared__ uint32_t tsc[16 * kMT];
+    uint32_t ts_bits = 0;
+    if (tid < 16 * kMT && tid < p.M) ts_bits = p.a_scale[tid];
+
     // This workgroup's K range [ta, tb): group-aligned units split evenly
     // (the host keeps splits <= units, so every range is non-empty).
     const int ks = static_cast<int>(blockIdx.y);
@@ -257,6 +264,8 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
 
     // ---- epilogue: token scale, bf16 (or the SwiGLU pair); fp32 sums to
     // the workspace when K is split
+    if (tid < 16 * kMT) tsc[tid] = ts_bits;
+    __syncthreads();
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
@@ -264,7 +273,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
             const int row = mt * 16 + rowq + q;
             if (row >= p.M) continue;
             if constexpr (SWIGLU) {
-                const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
+                const float ts = bf16_bits_to_f32(tsc[row]) * 0.0625f;
 #pragma unroll
                 for (int c = 0; c < CG; ++c) {
                     const int col = block_of(c) * 16 + colq;
@@ -280,7 +289,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
                     if (col < p.N) r[col] = acc[mt][c][q];
                 }
             } else {
-                const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
+                const float ts = bf16_bits_to_f32(tsc[row]) * 0.0625f;
 #pragma unroll
                 for (int c = 0; c < kCPW; ++c) {
                     const int col = block_of(c) * 16 + colq;
@@ -304,6 +313,7 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
     const int row = static_cast<int>(idx / n4);
     const int col = static_cast<int>(idx - static_cast<int64_t>(row) * n4) * 4;
     if (col >= N) return;
+    const uint32_t tsb = a_scale[row];   // requested with the sums, not after them
     const int64_t plane = static_cast<int64_t>(M) * ldr;
     const float* r = R + static_cast<int64_t>(row) * ldr + col;
     // all loads first (one memory latency, not one per split), then the sum
@@ -322,7 +332,7 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
             s.w += v[k].w;
         }
     }
-    const float ts = bf16_bits_to_f32(a_scale[row]) * 0.0625f;
+    const float ts = bf16_bits_to_f32(tsb) * 0.0625f;
     const uint32_t lo = f32_to_bf16_bits(s.x * ts) | (f32_to_bf16_bits(s.y * ts) << 16);
     const uint32_t hi = f32_to_bf16_bits(s.z * ts) | (f32_to_bf16_bits(s.w * ts) << 16);
     uint16_t* y = Y + static_cast<int64_t>(row) * ldy + col;
