@@ -193,6 +193,8 @@ GEMM_CASES = [
     (40, 512, 16384, 320, "bf16"),   # the same, split on 5-tile group-aligned units
     (64, 256, 16384, 256, "f16"),    # the same, 64 rows, two tiles per group
     (9, 2048, 16384, 64, "bf16"),    # the same, one row tile, group stride 64
+    (20, 16, 16400, 128, "bf16"),    # the same, one column block over 16 splits, a 16-element last group
+    (11, 300, 20000, 1024, "f16"),   # the same, group 1024: 8-tile split units, a short last group
     (17, 336, 1536, 192, "f16"),     # two 16-row groups, the second with one row; 11 column groups
     (40, 1000, 2048, 64, "bf16"),    # three row groups, ragged N
     (50, 200, 3072, 320, "f16"),     # row groups with groups ending on either slab
