@@ -502,6 +502,7 @@ hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool sbf16, hi
         if (mt == 2 && c.D == 4 && c.CPW == 1) return launch_v<2, 1, 4, MODE>(p, c.KW, sbf16, s);
     }
     if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 1 && c.D == 2 && c.CPW == 4) return launch_v<1, 4, 2, MODE>(p, c.KW, sbf16, s);
     if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, MODE>(p, c.KW, sbf16, s);
@@ -635,15 +636,15 @@ DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
         // waves (four past 8 rows).
         const int cap = KT >= 128 ? (M <= 8 ? 6 : 4) : 12;
         c.KW = std::max(1, std::min(cap, (KT + 3) / 4));
-    } else if (M <= 22) {
-        // 17-22 rows: one workgroup of all rows and six waves still beats
-        // the row groups (qkv/o at 17 rows: 9.9 / 9.4 against 10.7 / 10.3 us)
-        c.KW = 6;
     } else {
-        // More than 16 rows on narrow N: 16-row workgroups (row groups that
-        // share each column group) of two waves, which keeps every wave's
-        // MFMA, fold and load work per tile small and puts more waves in flight.
-        c = DecodeConfig{4, 2, 2, 1};
+        // More than 16 rows on narrow N with short K: 16-row workgroups (row
+        // groups that share each column group), which keeps every wave's
+        // MFMA, fold and load work per tile small and puts more waves in
+        // flight; four column blocks each, so every workgroup's activation
+        // rows serve twice the columns of a two-block group (the L2 reads of A
+        // bound these shapes: qkv M=64 17.5 -> 14.3 us), and six waves up to
+        // 28 rows, four past them.
+        c = DecodeConfig{2, 4, M <= 28 ? 6 : 4, 1};
     }
     return c;
 }
