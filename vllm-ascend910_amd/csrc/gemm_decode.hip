@@ -504,6 +504,7 @@ hipError_t dispatch(const DecodeParams& p, const DecodeConfig& c, bool sbf16, hi
     if (mt == 1 && c.D == 4 && c.CPW == 2) return launch_v<1, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 1 && c.D == 2 && c.CPW == 4) return launch_v<1, 4, 2, MODE>(p, c.KW, sbf16, s);
     if (mt == 2 && c.D == 4 && c.CPW == 2) return launch_v<2, 2, 4, MODE>(p, c.KW, sbf16, s);
+    if (mt == 2 && c.D == 2 && c.CPW == 4) return launch_v<2, 4, 2, MODE>(p, c.KW, sbf16, s);
     if (mt == 3 && c.D == 4 && c.CPW == 2) return launch_v<3, 2, 4, MODE>(p, c.KW, sbf16, s);
     if (mt == 4 && c.D == 4 && c.CPW == 2) return launch_v<4, 2, 4, MODE>(p, c.KW, sbf16, s);
     return hipErrorInvalidValue;
@@ -619,6 +620,8 @@ hipError_t launch_linear_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx
 
 namespace {
 
+constexpr int64_t kCUs = 256;   // MI355X compute units
+
 // The decode kernel's own plans (no wide layout): every shape has one.
 DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int mt = static_cast<int>((M + 15) / 16);
@@ -637,14 +640,18 @@ DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
         const int cap = KT >= 128 ? (M <= 8 ? 6 : 4) : 12;
         c.KW = std::max(1, std::min(cap, (KT + 3) / 4));
     } else {
-        // More than 16 rows on narrow N with short K: 16-row workgroups (row
-        // groups that share each column group), which keeps every wave's
-        // MFMA, fold and load work per tile small and puts more waves in
-        // flight; four column blocks each, so every workgroup's activation
-        // rows serve twice the columns of a two-block group (the L2 reads of A
-        // bound these shapes: qkv M=64 17.5 -> 14.3 us), and six waves up to
-        // 28 rows, four past them.
-        c = DecodeConfig{2, 4, M <= 28 ? 6 : 4, 1};
+        // More than 16 rows on narrow N with short K: row groups that share
+        // each column group, four column blocks each, so every workgroup's
+        // activation rows serve twice the columns of a two-block group (the
+        // L2 reads of A bound these shapes: qkv M=64 17.5 -> 14.3 us).
+        // 16-row groups (six waves up to 28 rows, four past) while they fit
+        // the CUs in one round; past that 32-row groups of four waves, which
+        // read each column group's weights half as often (qkv M=64 14.3 ->
+        // 13.5 us, o M=64 14.1 -> 13.1 us; o M=48 stays at 10 us on 240
+        // 16-row workgroups against 12.6 us).
+        const int64_t cg = (NB + 3) / 4;
+        if (cg * ((M + 15) / 16) <= kCUs) c = DecodeConfig{2, 4, M <= 28 ? 6 : 4, 1};
+        else c = DecodeConfig{2, 4, 4, 2};
     }
     return c;
 }
