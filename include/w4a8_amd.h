@@ -145,9 +145,9 @@ int w4a8_gemm_swiglu(const void* a_q, int64_t lda, const void* a_scale, const vo
  *            activations (as w4a8_quant_act with this group writes them)
  *   the other arguments as for w4a8_gemm.
  * Results are those of w4a8_quant_act followed by w4a8_gemm, bit for bit.
- * For a single row (M == 1) on narrow N with an unpadded K (and x 16-byte
- * aligned, ldx % 8 == 0) the quant runs inside the GEMM kernel, one launch
- * instead of two.
+ * For a single row (M == 1) with an unpadded K (and x 16-byte aligned,
+ * ldx % 8 == 0) whose K split fits the fused prologue, the quant runs inside
+ * the GEMM kernel on the GEMM's own split, one launch instead of two.
  * Replaces the reference linear method's quant-then-GEMM pair
  * (npu_ops/python/midgroup_quant.py:163-177, apply: midgroup_quant_a then
  * midgroup_w4a8_gemm) for the per-token symmetric path.

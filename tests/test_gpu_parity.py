@@ -427,14 +427,15 @@ LINEAR_CASES = [
     (4, 5120, 5120, 128, "bf16", "two-kernel: o, four rows"),
     (1, 5120, 5120, 128, "bf16", "fused: o"),
     (2, 1024, 4096, 128, "bf16", "two-kernel: two rows"),
-    (1, 5120, 27648, 128, "f16", "fused: down, seven chunks per lane (eight waves, two more than the GEMM)"),
+    (1, 5120, 27648, 128, "f16", "fused: down, seven chunks per lane (eight waves)"),
     (2, 5120, 27648, 128, "f16", "two-kernel: down, two rows"),
     (1, 640, 4096, 64, "bf16", "fused: group stride 64"),
     (1, 320, 6144, 512, "f16", "fused: groups of 4 tiles"),
     (1, 480, 3200, 320, "bf16", "fused: groups ending on either slab"),
     (1, 96, 1024, 1024, "f16", "fused: one group, one column group"),
     (5, 512, 2048, 128, "f16", "two-kernel: five rows"),
-    (1, 55296, 1024, 128, "bf16", "two-kernel: wide N"),
+    (1, 55296, 1024, 128, "bf16", "fused: wide N (two waves per column group)"),
+    (1, 55296, 5120, 128, "f16", "fused: gate_up"),
     (3, 256, 1057, 1024, "f16", "two-kernel: ragged K"),
 ]
 

@@ -567,12 +567,11 @@ struct FusedPlan {
 };
 
 bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f) {
-    // Small batches on narrow N only: each workgroup quantises all M rows of
-    // its K range, so the quant work is repeated per column group -- cheap
-    // for a few hundred workgroups, not for the thousands of a wide N.
-    // (Measured on MI355X: one row saves 0.5-3 us per call over the quant
-    // kernel + GEMM pair; at 2-4 rows the per-workgroup quant costs more
-    // than the launch it saves.)
+    // One row only: each workgroup quantises the rows of its K range, so the
+    // quant work is repeated per column group.  (Measured on MI355X: one row
+    // saves 0.5-3 us per call over the quant kernel + GEMM pair on narrow N
+    // and ~2 us on gate_up's 1728 column groups; at 2-4 rows the
+    // per-workgroup quant costs more than the launch it saves.)
     if (a.M != 1 || a.swiglu || a.partials || !geom::is_unpadded(a.K, a.group)) return false;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx % 8 != 0) return false;
     const DecodeConfig c = decode_config(a.M, a.N, a.K, a.group);
@@ -580,18 +579,13 @@ bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f)
     f.p = make_params(a);
     f.p.cgroups = (f.p.NB + 1) / 2;
     f.p.rgroups = 1;
-    if (f.p.cgroups >= 1024) return false;
     f.qm = 1;
-    // 16-byte chunks per row per lane of a wave's K range (its most tiles);
-    // the prologue holds at most 8 / qm, so the plan takes more waves than
-    // the GEMM's heuristic when a wave's range would not fit
-    auto qcpr_of = [&](int w) { return (f.p.unit * ((f.p.units + w - 1) / w) + 3) / 4; };
-    // Each wave quantises its K range before its first MFMA, so long K
-    // (>= 128 tiles) fuses best with eight short waves (down_proj: 20.7 us
-    // against 21.4 us at seven) where the GEMM alone prefers six.
-    f.kw = std::max(1, std::min(f.p.KT >= 128 ? std::max(c.KW, 8) : c.KW, kwmax_for(1, 2)));
-    while (f.kw < kwmax_for(1, 2) && qcpr_of(f.kw) > 8 / f.qm) ++f.kw;
-    f.p.qcpr = qcpr_of(f.kw);
+    // The GEMM's own K split (same waves, same ranges, same reduction order),
+    // so the fused call equals quant + GEMM bit for bit.
+    f.kw = c.KW;
+    if (f.kw < 1 || f.kw > kwmax_for(1, 2)) return false;
+    const int tiles = f.p.unit * ((f.p.units + f.kw - 1) / f.kw);   // most tiles a wave owns
+    f.p.qcpr = (tiles + 3) / 4;                                     // 16-byte chunks per row per lane
     if (f.p.qcpr > 8 / f.qm) return false;
     f.p.lrs = f.p.KT * 128 + 16;   // 16-byte skew: the rows' reads fall on different banks
     f.lds = static_cast<size_t>(f.kw) * 16 * 32 * 4 + static_cast<size_t>(f.qm) * f.p.lrs + 64 + f.kw * 16 + 16;
@@ -630,14 +624,18 @@ DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     DecodeConfig c{4, 2, 4};
     const int64_t wgs = (NB + 1) / 2;
     if (wgs >= 1024) {
-        // Wide N already gives >= 1024 workgroups of all rows: one wave each.
-        if (mt == 1) c.KW = 1;
+        // Wide N already gives >= 1024 workgroups of all rows: one wave each
+        // -- two for a single row, whose fused-quant plan (the same split)
+        // needs a wave's K range to fit its prologue's registers.
+        if (mt == 1) c.KW = M == 1 ? 2 : 1;
         else c = DecodeConfig{4, 2, 1};
     } else if (mt == 1 || (mt == 2 && KT >= 128)) {
         // Split K so that each wave holds about one ring (4 tiles) of its
         // range -- but long K (>= 128 tiles) streams better with six longer
-        // waves (four past 8 rows).
-        const int cap = KT >= 128 ? (M <= 8 ? 6 : 4) : 12;
+        // waves (four past 8 rows); a single row takes eight, which its fused
+        // quant prologue prefers (down_proj linear 20.7 against 21.4 us at
+        // seven; that plan uses the GEMM's split).
+        const int cap = KT >= 128 ? (M == 1 ? 8 : (M <= 8 ? 6 : 4)) : 12;
         c.KW = std::max(1, std::min(cap, (KT + 3) / 4));
     } else {
         // More than 16 rows on narrow N with short K: row groups that share

@@ -72,9 +72,9 @@ bool wide_layout_pairs(int layout);
 // Workspace of a call with `splits` K splits (0 for one split).
 int64_t wide_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int splits);
 
-// Fused per-token quant + decode GEMM for one row on narrow N (unpadded K,
-// x 16-byte aligned with ldx % 8 == 0, and the decode heuristic's 2-block,
-// 4-deep plan).  The workgroup of column group 0 also
+// Fused per-token quant + decode GEMM for one row (unpadded K, x 16-byte
+// aligned with ldx % 8 == 0, and the decode heuristic's 2-block, 4-deep plan,
+// whose K split it keeps).  The workgroup of column group 0 also
 // writes a_q / a_scale.  launch_linear_fused returns hipErrorInvalidValue when
 // linear_fusable is false.
 bool linear_fusable(const GemmArgs& a, const uint16_t* x, int64_t ldx);
