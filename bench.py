@@ -304,7 +304,7 @@ def main():
         traffic = round(json.loads(traffic_src.read_text())["avg_traffic_bytes"])
     result["roofline"] = {
         "kernel": ("decode W4A8 GEMM per call: gemm_decode_kernel; gemm_wide_kernel for gate_up and down at M=16 "
-                   "and 64, down followed by wide_reduce_kernel (K split over 8 workgroups) -- all 16 configs[1] "
+                   "and 64, down followed by wide_reduce_kernel (K split over 12 / 6 workgroups) -- all 16 configs[1] "
                    "shapes, cold"),
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

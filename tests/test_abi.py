@@ -44,8 +44,9 @@ def test_version_and_sizes(lib):
     assert lib.w4a8_gemm_workspace_bytes(4096, 5120, 5120, 128) == 0
     assert lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128) == 0
     assert lib.w4a8_gemm_workspace_bytes(8, 5120, 27648, 128) == 0
-    assert lib.w4a8_gemm_workspace_bytes(64, 5120, 27648, 128) == 8 * 64 * 5120 * 4
-    assert lib.w4a8_gemm_workspace_bytes(12, 5120, 27648, 128) == 8 * 12 * 5120 * 4
+    assert lib.w4a8_gemm_workspace_bytes(64, 5120, 27648, 128) == 6 * 64 * 5120 * 4
+    assert lib.w4a8_gemm_workspace_bytes(24, 5120, 27648, 128) == 8 * 24 * 5120 * 4
+    assert lib.w4a8_gemm_workspace_bytes(12, 5120, 27648, 128) == 12 * 12 * 5120 * 4
     assert lib.w4a8_gemm_workspace_bytes(20, 1000, 16384, 128) == 16 * 20 * 1008 * 4
     assert lib.w4a8_gemm_workspace_bytes(64, 55296, 27648, 128) == 0   # wide N: no split
 
@@ -69,8 +70,8 @@ def _gemm(lib, **kw):
     (dict(lda=264), 4, "16-byte"),
     (dict(a_q=24), 4, "16-byte"),
     # a decode shape that splits K over workgroups needs its workspace
-    (dict(M=12, N=5120, K=27648, lda=27648, ldy=5120), 6, "workspace needs 1966080 bytes"),
-    (dict(M=12, N=5120, K=27648, lda=27648, ldy=5120, ws=256, wsb=1966079), 6, "workspace"),
+    (dict(M=12, N=5120, K=27648, lda=27648, ldy=5120), 6, "workspace needs 2949120 bytes"),
+    (dict(M=12, N=5120, K=27648, lda=27648, ldy=5120, ws=256, wsb=2949119), 6, "workspace"),
     (dict(M=12, N=5120, K=27648, lda=27648, ldy=5120, ws=272, wsb=1 << 21), 6, "256-byte aligned"),
 ])
 def test_gemm_rejects_bad_arguments(lib, kw, code, msg):

@@ -672,11 +672,14 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     }
     if (M > 8 && KT >= 128) {
         // Narrow N, long K, past 8 rows: the same sharing with one column
-        // block per wave, K split over workgroups to reach ~640 of them
-        // (at least 8 tiles each).
+        // block per wave, K split over workgroups (at least 8 tiles each):
+        // ~960 of them for the 16-row layout, ~640 for 32 rows, ~480 for 64
+        // (the lighter the workgroup, the more of them; down_proj: 12, 8 and
+        // 6 splits).
         c.WIDE = mt == 1 ? kWide1x1 : (mt == 2 ? kWide2x1 : kWide4x1);
         const int64_t cg = (NB + 3) / 4;
-        const int64_t s = std::min<int64_t>({(640 + cg / 2) / cg, int64_t{16}, KT / 8});
+        const int64_t target = mt == 1 ? 960 : (mt == 2 ? 640 : 480);
+        const int64_t s = std::min<int64_t>({(target + cg / 2) / cg, int64_t{16}, KT / 8});
         c.SPLITS = static_cast<int>(std::max<int64_t>(s, 1));
         return c;
     }
