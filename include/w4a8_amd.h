@@ -94,15 +94,26 @@ int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_t
                 void* s_tiles, int64_t N, int64_t K, int64_t group, void* stream);
 
 /*
- * Workspace bytes the GEMM needs for (M, N, K, group); 0 when none.  Only
- * decode shapes past 8 rows on narrow N (under 2047 column blocks of 16)
- * with long K (at least 128 tiles of 128) use one: their K is split over
- * workgroups whose fp32 sums, [splits, M, ceil(N/16)*16], a second kernel
- * adds in split order.  A caller passes at least the size this function
- * returns (NULL/0 for 0), 256-byte aligned; calls that overlap in time need
- * workspaces of their own.  Prefill does not split K.
+ * Workspace bytes the GEMM needs for (M, N, K, group) on the current device;
+ * 0 when none.  Only decode shapes past 8 rows on narrow N (fewer than four
+ * two-block column groups per compute unit: under 2047 column blocks of 16 on
+ * a 256-CU MI355X) with long K (at least 128 tiles of 128) use one: their K
+ * is split over workgroups whose fp32 sums, [splits, M, ceil(N/16)*16], a
+ * second kernel adds in split order.  A caller passes at least the size this
+ * function returns (NULL/0 for 0), 256-byte aligned; calls that overlap in
+ * time need workspaces of their own.  Prefill does not split K.
  */
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
+
+/*
+ * Rows per launch when w4a8_gemm splits a call of M rows at row stride lda
+ * into row chunks: M itself when one launch takes them all (the kernels
+ * address A with 32-bit offsets), 0 when the call is refused instead (64 rows
+ * or fewer at that stride, or a stride too large for even 256 rows).  No
+ * counterpart in the reference, whose host path has no such limit at its
+ * shapes; a query for callers and tests.
+ */
+int64_t w4a8_gemm_row_chunk(int64_t M, int64_t lda);
 
 /*
  * The grouped W4A8 GEMM with fused scale epilogue.
@@ -113,6 +124,9 @@ int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
  *   a_scale  bf16 [M]
  *   w_tiles, s_tiles            (from w4a8_repack; scale_dtype as repacked)
  *   y        bf16 [M, ldy]      output
+ * Calls whose activations exceed 32-bit offsets ((M + 128) * lda >= 2^31) run
+ * as several launches over row chunks (w4a8_gemm_row_chunk); the debug
+ * partial dump refuses such calls.
  * Replaces the reference GEMM, kernel npu_ops/kernel/midgroup_w4a8_gemm.inc:491-1169
  * bound by npu_ops/host/midgroup_w4a8_gemm.cpp:45-140 (run_midgroup_w4a8_gemm),
  * for symmetric weights and per-token activation scales.

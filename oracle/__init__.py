@@ -18,9 +18,13 @@ How each function is pinned (tests/test_oracle.py):
                             (oracle/_ref: gemm_ref.cpp PackInt4Grouped,
                             mg_kgeom.h) and exhaustive nibble round trips
   * group partials       -- brute-force int64 dot products
-  * fp32 GEMM / bf16 out -- the reference's ReferenceMidGroupGemm (oracle/_ref)
-                            and a float64 restatement of run_selftest.py's
-                            _exact_reference; golden vectors in tests/golden/
+  * fp32 GEMM / bf16 out -- the reference's ReferenceMidGroupGemm and
+                            ReferencePerchannelGemm (oracle/_ref) and a float64
+                            restatement of run_selftest.py's _exact_reference;
+                            tests/golden/reference_vectors.npz holds outputs of
+                            the reference's C++ (packing, plane split, ksums,
+                            geometry, the three GEMM orders) written by
+                            tests/golden/make_golden.py, checked on CPU and GPU
   * torch addcmul_ FMA   -- parity unpinned at the last fp32 bit (whether
     contraction             ATen fuses acc + partial*s is not fixed); covered by
                             the bf16 output tolerance instead

@@ -46,6 +46,8 @@ def lib() -> ctypes.CDLL:
         h.ref_split_planes_grouped.argtypes = [_P, _SZ, _U32, _U32, _P, _P]
         h.ref_midgroup_gemm.argtypes = [_P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32]
         h.ref_perchannel_gemm.argtypes = [_P, _P, _P, _P, _P, _U32, _U32, _U32]
+        h.ref_set_threads.argtypes = [ctypes.c_int]
+        h.ref_max_threads.restype = ctypes.c_int
         _lib = h
     return _lib
 
@@ -119,3 +121,39 @@ def midgroup_gemm(a_q: np.ndarray, a_scale_g: np.ndarray, w_codes: np.ndarray, w
     lib().ref_midgroup_gemm(_ptr(a_q), _ptr(a_scale_g), _ptr(w_codes), _ptr(w_scale_g),
                             None if wz is None else _ptr(wz), _ptr(y), M, N, K, group, M)
     return y
+
+
+def set_threads(n: int) -> int:
+    """Set the OpenMP team size of the reference's loops; returns the size now in effect."""
+    lib().ref_set_threads(int(n))
+    return int(lib().ref_max_threads())
+
+
+def perchannel_gemm(a_q: np.ndarray, a_scale: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray) -> np.ndarray:
+    """ReferencePerchannelGemm (gemm_ref.cpp:154-179): bf16 bits [M, N] of
+    bf16(float(sum_k a*w) * as[m] * ws[n]); a_scale [M], w_scale [N] bf16 bits."""
+    a_q = np.ascontiguousarray(a_q, np.int8)
+    w_codes = np.ascontiguousarray(w_codes, np.int8)
+    a_scale = np.ascontiguousarray(a_scale, np.uint16)
+    w_scale = np.ascontiguousarray(w_scale, np.uint16)
+    M, K = a_q.shape
+    N = w_codes.shape[0]
+    y = np.empty((M, N), np.uint16)
+    lib().ref_perchannel_gemm(_ptr(a_q), _ptr(a_scale), _ptr(w_codes), _ptr(w_scale), _ptr(y), M, N, K)
+    return y
+
+
+def num_groups(K: int, group: int) -> int:
+    return int(lib().ref_num_groups(K, group))
+
+
+def kpad(K: int, group: int) -> int:
+    return int(lib().ref_kpad(K, group))
+
+
+def group_offset(g: int, group: int) -> int:
+    return int(lib().ref_group_offset(g, group))
+
+
+def group_real(g: int, K: int, group: int) -> int:
+    return int(lib().ref_group_real(g, K, group))

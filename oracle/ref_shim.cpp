@@ -9,11 +9,18 @@
 #include <cstring>
 #include <vector>
 
+#include <omp.h>
+
 #include "bf16.h"
 #include "gemm_ref.h"
 #include "mg_kgeom.h"
 
 extern "C" {
+
+// OpenMP team size of the reference's parallel loops (for timing: the thread
+// count a baseline states is the one it ran with).
+void ref_set_threads(int n) { omp_set_num_threads(n); }
+int ref_max_threads(void) { return omp_get_max_threads(); }
 
 void ref_fp32_to_bf16(const float* x, uint16_t* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = FP32ToBF16(x[i]);

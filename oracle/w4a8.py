@@ -68,6 +68,11 @@ def group_pad(g: int, K: int, group: int) -> int:
     return -(-group_real(g, K, group) // GROUP_ALIGN) * GROUP_ALIGN
 
 
+def group_offset(g: int, group: int) -> int:
+    """Element offset of group g in a padded row (npu_ops/kernel/mg_kgeom.h:90-95)."""
+    return g * group_stride(group)
+
+
 def kpad(K: int, group: int) -> int:
     """npu_ops/kernel/mg_kgeom.h:98-102."""
     G = num_groups(K, group)
@@ -193,6 +198,9 @@ def group_partials(a_q: np.ndarray, w_codes: np.ndarray, group: int, exact_int64
     M, K = a_q.shape
     N = w_codes.shape[0]
     G = num_groups(K, group)
+    # the fp32 route is exact only while every |partial| stays below 2^24
+    # (|a| <= 128, |w| <= 8): longer groups (per-channel, group = K) take int64
+    exact_int64 = exact_int64 or 1024 * min(group, K) >= (1 << 24)
     out = np.empty((G, M, N), np.int64)
     for g in range(G):
         sl = slice(g * group, g * group + group_real(g, K, group))
@@ -254,6 +262,48 @@ def gemm_f64(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_s
     for g in range(G):
         acc += partials[g].astype(np.float64) * (a_s[:, None] * w_scale[:, g].astype(np.float64)[None, :])
     return acc
+
+
+def gemm_midgroup_f64(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_scale_bits: np.ndarray,
+                      w_zero_bits: Optional[np.ndarray], group: int,
+                      partials: Optional[np.ndarray] = None) -> np.ndarray:
+    """float64 value of ReferenceMidGroupGemm's definition (int4_cube_lab/host/gemm_ref.cpp:199-240):
+    sum_g I_g[m,n] * ws[g,n] * as[g,m] with I_g = sum_{k in g} A*(W - wz), exact int64."""
+    M = a_q.shape[0]
+    G = num_groups(a_q.shape[1], group)
+    if partials is None:
+        partials = group_partials_asym(a_q, w_codes, w_zero_bits, group)
+    acc = np.zeros((M, w_codes.shape[0]), np.float64)
+    for g in range(G):
+        acc += (partials[g].astype(np.float64) * bf16_bits_to_f32(w_scale_bits[g]).astype(np.float64)[None, :]
+                * bf16_bits_to_f32(a_scale_bits[g, :M]).astype(np.float64)[:, None])
+    return acc
+
+
+def output_bar(y_bits: np.ndarray, y32: np.ndarray, exact) -> Tuple[np.ndarray, int]:
+    """The bf16 output bar of the build's parity tests.
+
+    An output passes when |y - y32| <= 1 bf16 ulp of y32, the oracle's fp32
+    result (the north_star's max-abs bound).  One that does not -- where the
+    groups cancel, two fp32 summation orders can differ by more than an ulp of
+    the small result -- must lie within 1 bf16 ulp of the exact value instead:
+    ``exact(rows, cols)`` returns the float64 restatement (``gemm_f64``,
+    fakequant_lab/run_selftest.py:104-120) on the sorted unique rows x cols of
+    those outputs.  Returns (mask of outputs failing both, number of outputs
+    that needed the float64 value).
+    """
+    y = bf16_bits_to_f32(y_bits).astype(np.float64)
+    r = np.asarray(y32, np.float64)
+    first = np.abs(y - r) > bf16_ulp(r)
+    fail = np.zeros(y.shape, bool)
+    n_fb = int(first.sum())
+    if n_fb:
+        ri, ci = np.nonzero(first)
+        ur, uc = np.unique(ri), np.unique(ci)
+        e = np.asarray(exact(ur, uc), np.float64)
+        ev = e[np.searchsorted(ur, ri), np.searchsorted(uc, ci)]
+        fail[ri, ci] = np.abs(y[ri, ci] - ev) > bf16_ulp(ev)
+    return fail, n_fb
 
 
 # ------------------------------------------------------------------ RMSNorm (decoder layer)

@@ -100,3 +100,40 @@ def test_quant_and_repack_reject_bad_arguments(lib):
 def test_errors_raise_runtimeerror_from_python(pkg):
     with pytest.raises(RuntimeError, match="SHAPE"):
         pkg._abi.check(_gemm(pkg._abi.lib(), N=0), "w4a8_gemm")
+
+
+def test_row_chunk_arithmetic(lib):
+    """Calls whose activations exceed 32-bit offsets are split into row chunks: each
+    chunk fits the offset bound (rows + 128 past them), chunks are multiples of 128,
+    and a balanced split of M gives every chunk more than 64 rows (prefill launches)."""
+    for lda in (5120, 27648, 55296, 1 << 16, 1 << 20, 3 << 20):
+        for M in (1, 64, 65, 1000, 77000, 77700, 80000, 200000, 1 << 20):
+            c = lib.w4a8_gemm_row_chunk(M, lda)
+            if (M + 128) * lda < (1 << 31):
+                assert c == M
+                continue
+            if M <= 64:
+                assert c == 0
+                continue
+            if c == 0:
+                assert ((1 << 31) - 1) // lda - 128 < 256
+                continue
+            assert c % 128 == 0 and c >= 256 and (c + 128) * lda < (1 << 31)
+            n = -(-M // c)
+            bounds = [(M * i) // n for i in range(n + 1)]
+            sizes = [b - a for a, b in zip(bounds, bounds[1:])]
+            assert sum(sizes) == M and max(sizes) <= c and min(sizes) > 64
+    assert lib.w4a8_gemm_row_chunk(80000, 27648) == ((1 << 31) - 1) // 27648 - 128 - (((1 << 31) - 1) // 27648 - 128) % 128
+
+
+def test_offset_limits_are_refused_on_every_path(lib):
+    """Weights beyond 32-bit offsets are refused by the GEMM and by the fused
+    single-row linear alike (no launch, no silent wrap)."""
+    N, K, G = 1 << 19, 8192, 128
+    st = lib.w4a8_gemm(16, K, 16, 16, 16, 0, 16, N, 1, N, K, G, None, 0, None)
+    assert st == 5 and b"32-bit" in lib.w4a8_last_error()
+    st = lib.w4a8_linear(16, K, 16, 16, 0, 16, N, 16, K, 16, 1, N, K, G, None, 0, None)
+    assert st == 5 and b"32-bit" in lib.w4a8_last_error()
+    # 64 rows at a stride too large for one launch cannot be chunked
+    lda = (1 << 31) // 150 // 16 * 16
+    assert lib.w4a8_gemm(16, lda, 16, 16, 16, 0, 16, 64, 64, 64, 256, G, None, 0, None) == 5

@@ -159,3 +159,110 @@ def test_resize_then_capture_after_full_decode(pkg, dev):
     m2 = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=16, device=dev, seed=4)
     eager_out = m2.decode(m2.prefill(p2), 8, 8, graph=False)
     assert all(torch.equal(a, b) for a, b in zip(graph_out, eager_out))
+
+
+# ------------------------------------------------------------------ configs[4] at its real widths
+def _check_linear_calls(pkg, calls, n_cols=48):
+    """Every recorded W4A8 linear call of a forward against the oracle on sampled
+    output columns (all rows): the GEMMs and the quant+GEMM linears to the output
+    bar of the parity tests, the fused SwiGLU against silu(bf16 g) * bf16 u of the
+    oracle's gate/up outputs."""
+    import numpy as np
+    from conftest import tensor_bf16_bits
+    from oracle import w4a8 as ow
+    from test_gpu_parity import check_output, check_swiglu, exact_sym
+    rng = np.random.default_rng(0)
+    for i, (lin, kind, inp, out) in enumerate(calls):
+        N, K, G = lin.N, lin.K, lin.group
+        if kind == "linear":
+            q_ref, s_ref = ow.quant_act_per_token(tensor_bf16_bits(inp))
+        else:
+            a_q, a_s = inp
+            q_ref, s_ref = a_q.cpu().numpy()[:, :K], tensor_bf16_bits(a_s)
+        width = N // 2 if kind == "swiglu" else N
+        cols = np.sort(rng.choice(width, n_cols, replace=False))
+        both = np.concatenate([cols, cols + width]) if kind == "swiglu" else cols
+        w = lin.codes[torch.from_numpy(both).to(lin.codes.device)].cpu().numpy()
+        ws32 = lin.scales[:, torch.from_numpy(both).to(lin.scales.device)].float().cpu().numpy().T.copy()
+        y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G)
+        got = tensor_bf16_bits(out)[:, cols]
+        tag = f"call {i} {kind} M={q_ref.shape[0]} N={N} K={K}"
+        if kind == "swiglu":
+            # gate/up of the plain GEMM on the same operands against the oracle, and
+            # the fused epilogue against silu(g) * u of those bf16 values
+            gu = tensor_bf16_bits(torch.ops.npu.w4a8_gemm(a_q, a_s, lin.w_tiles, lin.s_tiles, N, K, G))[:, both]
+            check_output(gu, y32, tag + " gate/up", exact_sym(q_ref, s_ref, w, ws32, G))
+            check_swiglu(got, ow.silu_mul_bf16(gu[:, :n_cols], gu[:, n_cols:]), 0.999, tag)
+        else:
+            check_output(got, y32, tag, exact_sym(q_ref, s_ref, w, ws32, G))
+
+
+def test_qwq_width_layers_linears_match_oracle(pkg, dev, monkeypatch):
+    """configs[4]'s layer at QwQ-32B widths (hidden 5120, 40/8 heads, head_dim 128, FFN
+    27648, vocab 152064, group 128; two layers): every W4A8 linear inside a prefill of
+    2 x 64 tokens (prefill kernels, 128 rows) and inside two decode steps (decode
+    kernels, 2 rows) matches the oracle; graph replay equals eager decode; a decode
+    step after a prefill agrees with a longer prefill."""
+    D = pkg.decoder
+    cfg = D.DecoderConfig(layers=2)
+    say("decoder: QwQ-32B widths, 2 layers")
+    m = D.W4A8Decoder(cfg, batch=2, max_len=80, device=dev, seed=7, keep_weights=True)
+    calls = []
+    orig_call, orig_linear, orig_swiglu = D._Linear.__call__, D._Linear.linear, D._Linear.swiglu
+
+    def rec_call(self, a_q, a_s):
+        y = torch.ops.npu.w4a8_gemm(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+        calls.append((self, "gemm", (a_q.clone(), a_s.clone()), y.clone()))
+        return y + self.bias if self.bias is not None else y
+
+    def rec_linear(self, x):
+        y = torch.ops.npu.w4a8_linear(x, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+        calls.append((self, "linear", x.clone(), y.clone()))
+        return y + self.bias if self.bias is not None else y
+
+    def rec_swiglu(self, a_q, a_s):
+        y = orig_swiglu(self, a_q, a_s)
+        calls.append((self, "swiglu", (a_q.clone(), a_s.clone()), y.clone()))
+        return y
+
+    prompt = torch.randint(0, cfg.vocab, (2, 64), generator=torch.Generator().manual_seed(8)).to(dev)
+    monkeypatch.setattr(D._Linear, "__call__", rec_call)
+    monkeypatch.setattr(D._Linear, "linear", rec_linear)
+    monkeypatch.setattr(D._Linear, "swiglu", rec_swiglu)
+    first = m.prefill(prompt)
+    m.decode(first, 64, 2, graph=False)
+    torch.cuda.synchronize()
+    monkeypatch.setattr(D._Linear, "__call__", orig_call)
+    monkeypatch.setattr(D._Linear, "linear", orig_linear)
+    monkeypatch.setattr(D._Linear, "swiglu", orig_swiglu)
+    assert len(calls) == 3 * 4 * cfg.layers, len(calls)     # prefill + 2 decode steps, 4 linears per layer
+    say(f"  checking {len(calls)} linear calls against the oracle")
+    _check_linear_calls(pkg, calls)
+    del calls
+
+    # graph replay == eager decode (same kernels), every replay checked
+    k0 = [k.clone() for k in m.k_cache]
+    v0 = [v.clone() for v in m.v_cache]
+    eager = m.decode(first, 64, 4, graph=False)
+    eager_logits = m.last_logits.clone()
+    for k, kk in zip(m.k_cache, k0):
+        k.copy_(kk)
+    for v, vv in zip(m.v_cache, v0):
+        v.copy_(vv)
+    graph = m.decode(first, 64, 4, graph=True)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(graph, eager)), "graph decode differs from eager"
+    assert torch.equal(m.last_logits, eager_logits), "graph logits differ from eager"
+
+    # prefill/decode consistency at full width
+    for k, kk in zip(m.k_cache, k0):
+        k.copy_(kk)
+    for v, vv in zip(m.v_cache, v0):
+        v.copy_(vv)
+    m.decode(first, 64, 1, graph=False)
+    dec_logits = m.last_logits.float().clone()
+    m.resize(2, 80)
+    m.prefill(torch.cat([prompt, first[:, None]], dim=1))
+    rel = (dec_logits - m.last_logits.float()).norm() / m.last_logits.float().norm()
+    say(f"  prefill vs decode logits rel-L2 {rel:.5f}")
+    assert rel < 2e-2, f"rel-L2 {rel}"

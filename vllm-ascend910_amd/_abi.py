@@ -30,6 +30,7 @@ SIGNATURES = {
     "w4a8_repacked_scale_bytes": (_I64, [_I64, _I64, _I64]),
     "w4a8_repack": (_I, [_VP, _VP, _I, _VP, _VP, _I64, _I64, _I64, _VP]),
     "w4a8_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "w4a8_gemm_row_chunk": (_I64, [_I64, _I64]),
     "w4a8_gemm": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
     "w4a8_gemm_swiglu": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
     "w4a8_linear_fused": (_I, [_VP, _I64, _I64, _I64, _I64, _I64]),

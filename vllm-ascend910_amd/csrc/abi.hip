@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <string>
 
@@ -17,9 +18,27 @@
 
 namespace w4a8 {
 
-// Planning constant: MI355X has 256 CUs.  Kept fixed (not queried) so that
-// workspace sizes are a pure function of the problem shape.
-int device_cu_count() { return 256; }
+// Compute units of the current device, queried once per device (plans and
+// workspace sizes follow it; a partitioned MI355X exposes fewer than 256).
+// Without a usable device (the query fails, e.g. on a host without a GPU)
+// the full part's 256 is assumed.
+int device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cached[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        n = 256;
+    }
+    cached[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
 
 namespace {
 
@@ -39,6 +58,18 @@ int hip_status(hipError_t e, const char* what) {
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Most rows one GEMM launch takes at row stride lda: the kernels address A
+// with 32-bit offsets, up to 128 rows past a launch's last row, with 2^31
+// added on top for out-of-range reads.  A multiple of 128 (the prefill tile)
+// and at least 256, so that every chunk of a split call has more than 64 rows
+// and stays on the prefill path (no workspace); 0 when not even that fits.
+int64_t gemm_row_chunk(int64_t lda) {
+    if (lda <= 0) return 0;
+    const int64_t rows = ((1ll << 31) - 1) / lda - 128;
+    const int64_t chunk = (rows / 128) * 128;
+    return chunk >= 256 ? chunk : 0;
+}
 
 int check_problem(int64_t M, int64_t N, int64_t K, int64_t group) {
     if (M < 0 || N <= 0 || K <= 0 || group <= 0)
@@ -67,6 +98,17 @@ int check_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_
         return fail(W4A8_ERR_ALIGN, "a_q must be 16-byte aligned with lda %% 16 == 0 (lda=%lld)", lda);
     if (!aligned(w_tiles, 16) || !aligned(s_tiles, 2) || !aligned(y, 2) || !aligned(a_scale, 2))
         return fail(W4A8_ERR_ALIGN, "w_tiles must be 16-byte aligned; s_tiles, y, a_scale 2-byte aligned");
+    // The kernels address the weight tiles with 32-bit buffer offsets,
+    // including up to one tile past the end, and mark out-of-range reads with
+    // an offset of 2^31 added on top (every path: the fused single-row linear too).
+    const int64_t w_span = (geom::col_blocks(N) + 16) * geom::k_tiles(K, group) * geom::kTileBytes;
+    if (w_span >= (1ll << 31))
+        return fail(W4A8_ERR_UNSUPPORTED, "weights too large for 32-bit offsets (%lld B for N=%lld)", w_span, N);
+    // A is addressed the same way: a call whose rows do not fit is split into
+    // row chunks (run_gemm), which needs more than 64 rows and a chunk size.
+    if (lda >= (1ll << 31) ||
+        ((M + 128) * lda >= (1ll << 31) && (M <= kDecodeMaxM || gemm_row_chunk(lda) == 0)))
+        return fail(W4A8_ERR_UNSUPPORTED, "M=%lld rows at lda=%lld exceed 32-bit activation offsets", M, lda);
     const int64_t need = w4a8_gemm_workspace_bytes(M, N, K, group);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)))
         return fail(W4A8_ERR_WORKSPACE, "workspace needs %lld bytes, 256-byte aligned (got %lld)", need,
@@ -100,18 +142,28 @@ int run_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_ti
     a.workspace = workspace;
     a.workspace_bytes = workspace_bytes;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    {
-        // Both kernels address A and the weight tiles with 32-bit buffer
-        // offsets, including up to one tile past the end of each, and mark
-        // out-of-range reads with an offset of 2^31 added on top.
-        const int64_t a_span = (M + 128) * lda;
-        const int64_t w_span = (geom::col_blocks(N) + 16) * geom::k_tiles(K, group) * geom::kTileBytes;
-        if (a_span >= (1ll << 31) || w_span >= (1ll << 31))
-            return fail(W4A8_ERR_UNSUPPORTED, "operands too large for 32-bit offsets (A %lld B, weights %lld B)",
-                        a_span, w_span);
+    const int64_t chunk = gemm_row_chunk(lda);
+    if ((M + 128) * lda < (1ll << 31)) {
+        const hipError_t e = (M <= kDecodeMaxM) ? launch_gemm_decode(a, s) : launch_gemm_prefill(a, s);
+        return hip_status(e, "w4a8_gemm launch");
     }
-    const hipError_t e = (M <= kDecodeMaxM) ? launch_gemm_decode(a, s) : launch_gemm_prefill(a, s);
-    return hip_status(e, "w4a8_gemm launch");
+    // A too large for 32-bit offsets (e.g. K = 27648 past ~77k rows): the rows
+    // go in balanced chunks of at most `chunk` (> 64 rows each: prefill
+    // launches, no workspace).  The partial dump indexes rows of one launch.
+    if (partials)
+        return fail(W4A8_ERR_UNSUPPORTED, "M=%lld rows at lda=%lld need row chunks, not available with the "
+                    "partial dump", M, lda);
+    const int64_t nchunks = (M + chunk - 1) / chunk;
+    for (int64_t c = 0; c < nchunks; ++c) {
+        const int64_t m0 = (M * c) / nchunks, m1 = (M * (c + 1)) / nchunks;
+        GemmArgs ac = a;
+        ac.a_q = a.a_q + m0 * lda;
+        ac.a_scale = a.a_scale + m0;
+        ac.y = a.y + m0 * ldy;
+        ac.M = m1 - m0;
+        if (int rc = hip_status(launch_gemm_prefill(ac, s), "w4a8_gemm launch")) return rc;
+    }
+    return W4A8_OK;
 }
 
 }  // namespace
@@ -163,6 +215,12 @@ int w4a8_repack(const void* w_q, const void* w_scale, int scale_dtype, void* w_t
                                     static_cast<uint8_t*>(w_tiles), static_cast<uint16_t*>(s_tiles), N, K,
                                     group, static_cast<hipStream_t>(stream)),
                       "w4a8_repack launch");
+}
+
+int64_t w4a8_gemm_row_chunk(int64_t M, int64_t lda) {
+    if (M <= 0 || lda <= 0) return 0;
+    if ((M + 128) * lda < (1ll << 31)) return M;
+    return M > kDecodeMaxM ? gemm_row_chunk(lda) : 0;
 }
 
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {

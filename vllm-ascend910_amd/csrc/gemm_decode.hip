@@ -614,8 +614,6 @@ hipError_t launch_linear_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx
 
 namespace {
 
-constexpr int64_t kCUs = 256;   // MI355X compute units
-
 // The decode kernel's own plans (no wide layout): every shape has one.
 DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int mt = static_cast<int>((M + 15) / 16);
@@ -623,8 +621,8 @@ DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int64_t NB = geom::col_blocks(N);
     DecodeConfig c{4, 2, 4};
     const int64_t wgs = (NB + 1) / 2;
-    if (wgs >= 1024) {
-        // Wide N already gives >= 1024 workgroups of all rows: one wave each
+    if (wgs >= 4 * device_cu_count()) {
+        // Wide N already gives >= 4 workgroups of all rows per CU: one wave each
         // -- two for a single row, whose fused-quant plan (the same split)
         // needs a wave's K range to fit its prologue's registers.
         if (mt == 1) c.KW = M == 1 ? 2 : 1;
@@ -648,7 +646,7 @@ DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
         // 13.5 us, o M=64 14.1 -> 13.1 us; o M=48 stays at 10 us on 240
         // 16-row workgroups against 12.6 us).
         const int64_t cg = (NB + 3) / 4;
-        if (cg * ((M + 15) / 16) <= kCUs) c = DecodeConfig{2, 4, M <= 28 ? 6 : 4, 1};
+        if (cg * ((M + 15) / 16) <= device_cu_count()) c = DecodeConfig{2, 4, M <= 28 ? 6 : 4, 1};
         else c = DecodeConfig{2, 4, 4, 2};
     }
     return c;
@@ -664,7 +662,7 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     const int64_t NB = geom::col_blocks(N);
     const int64_t wgs = (NB + 1) / 2;
     DecodeConfig c{4, 2, 1};
-    if (M > 8 && wgs >= 1024) {
+    if (M > 8 && wgs >= 4 * device_cu_count()) {
         // Wide N past 8 rows: the activations each decode workgroup reads
         // weigh as much as its weights; four column waves share them in LDS.
         c.WIDE = mt == 1 ? kWide1x2 : (mt == 2 ? kWide2x2 : kWide4x2);
@@ -673,12 +671,13 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     if (M > 8 && KT >= 128) {
         // Narrow N, long K, past 8 rows: the same sharing with one column
         // block per wave, K split over workgroups (at least 8 tiles each):
-        // ~960 of them for the 16-row layout, ~640 for 32 rows, ~480 for 64
-        // (the lighter the workgroup, the more of them; down_proj: 12, 8 and
-        // 6 splits).
+        // ~3.75 per CU for the 16-row layout, ~2.5 for 32 rows, ~1.9 for 64
+        // (the lighter the workgroup, the more of them; down_proj on 256
+        // CUs: 960 / 640 / 480 workgroups, 12, 8 and 6 splits).
         c.WIDE = mt == 1 ? kWide1x1 : (mt == 2 ? kWide2x1 : kWide4x1);
         const int64_t cg = (NB + 3) / 4;
-        const int64_t target = mt == 1 ? 960 : (mt == 2 ? 640 : 480);
+        const int64_t cus = device_cu_count();
+        const int64_t target = mt == 1 ? cus * 15 / 4 : (mt == 2 ? cus * 5 / 2 : cus * 15 / 8);
         const int64_t s = std::min<int64_t>({(target + cg / 2) / cg, int64_t{16}, KT / 8});
         c.SPLITS = static_cast<int>(std::max<int64_t>(s, 1));
         return c;

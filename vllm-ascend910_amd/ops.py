@@ -67,25 +67,52 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
 
 
 # One workspace per (device, stream), allocated only when the library asks
-# for one (decode shapes that split K over workgroups); it only grows.  Concurrent calls on one
-# stream are stream-ordered, so sharing per stream is safe.
+# for one (decode shapes that split K over workgroups); it only grows.  Eager
+# calls on one stream are stream-ordered, so sharing per stream is safe.
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+# Calls captured into a HIP graph get a workspace of that capture instead:
+# the graph may be replayed on any stream, while eager calls keep using the
+# stream's own, so the two never share memory.  Calls inside one graph run in
+# its captured order and share the capture's workspace.
+_CAPTURE_WS: Dict[Tuple[int, int], torch.Tensor] = {}
 # Workspaces replaced by a larger one stay allocated: a captured HIP graph
 # keeps the address it was captured with, so that memory must never return
-# to the caching allocator.
+# to the caching allocator (nor may a capture's own workspace).
 _RETIRED: list = []
+
+_hip = None
+
+
+def _capture_id(stream_handle: int) -> int:
+    """The HIP capture sequence id of a stream that is being captured (the
+    runtime torch loaded, found by its soname)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
+                                                 ctypes.POINTER(ctypes.c_ulonglong)]
+        _hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
+    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    rc = _hip.hipStreamGetCaptureInfo(ctypes.c_void_p(stream_handle), ctypes.byref(status), ctypes.byref(cid))
+    if rc != 0 or status.value != 1:
+        raise RuntimeError(f"w4a8: could not read the capture id of stream {stream_handle:#x} (rc {rc})")
+    return int(cid.value)
 
 
 def _workspace(dev: torch.device, need: int) -> torch.Tensor:
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
-           torch.cuda.current_stream(dev).cuda_stream)
-    ws = _WORKSPACES.get(key)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if torch.cuda.is_current_stream_capturing():
+        table, key = _CAPTURE_WS, (index, _capture_id(stream))
+    else:
+        table, key = _WORKSPACES, (index, stream)
+    ws = table.get(key)
     if ws is None or ws.numel() < need:
         if ws is not None:
             _RETIRED.append(ws)
         # no clearing needed: the split GEMM writes every sum the reduce reads
         ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=dev)
-        _WORKSPACES[key] = ws
+        table[key] = ws
     return ws
 
 
