@@ -136,6 +136,25 @@ int w4a8_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_t
               int64_t K, int64_t group, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * w4a8_gemm without the workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference, whose host path allocates its
+ * workspace per call (npu_ops/host/midgroup_w4a8_gemm.cpp:116-118).  The fp32
+ * split sums of the shapes that split K over workgroups go to a static device
+ * array of W4A8_NOALLOC_SCRATCH_BYTES per GPU (the library's, held until the
+ * process ends; no hipMalloc, no hipFree, nothing cleared -- every sum is
+ * written before it is read).  Shapes that need more (w4a8_gemm_workspace_bytes
+ * above the limit) return W4A8_ERR_WORKSPACE without launching; every
+ * QwQ-32B projection at M <= 64 fits.  All calls on one GPU share that array:
+ * calls that overlap in time on one GPU (other streams, concurrent replays)
+ * race and must be ordered by the caller.  Results equal w4a8_gemm's bit for bit.
+ */
+#define W4A8_NOALLOC_SCRATCH_BYTES (8ll << 20)
+int w4a8_gemm_noalloc(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
+                      const void* s_tiles, int scale_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+                      int64_t K, int64_t group, void* stream);
+
+/*
  * The same GEMM over a merged gate/up weight (N = 2*I output columns: gate
  * rows [0, I), up rows [I, 2I), as vLLM's merged gate_up projection stores
  * them) with the SwiGLU activation fused into its epilogue:

@@ -19,6 +19,7 @@ ABI_VERSION = 4
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1
+NOALLOC_SCRATCH_BYTES = 8 << 20   # W4A8_NOALLOC_SCRATCH_BYTES
 
 # Every symbol include/w4a8_amd.h declares, with its ctypes signature.
 _VP, _I64, _I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
@@ -32,6 +33,7 @@ SIGNATURES = {
     "w4a8_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "w4a8_gemm_row_chunk": (_I64, [_I64, _I64]),
     "w4a8_gemm": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
+    "w4a8_gemm_noalloc": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP]),
     "w4a8_gemm_swiglu": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
     "w4a8_linear_fused": (_I, [_VP, _I64, _I64, _I64, _I64, _I64]),
     "w4a8_linear": (_I, [_VP, _I64, _VP, _VP, _I, _VP, _I64, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/w4a8_amd.h"
@@ -166,6 +167,38 @@ int run_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_ti
     return W4A8_OK;
 }
 
+// ---- scratch of the allocation-free GEMM (w4a8_gemm_noalloc)
+// A file-scope device array: the runtime gives every GPU the library runs on
+// its own copy, held until the process ends.  Host code must not pass the
+// array's name to a kernel (on the host it is only a stand-in symbol): the
+// device address of this GPU's copy comes from hipGetSymbolAddress, looked up
+// once per device with that device current and kept.
+static __device__ __align__(256) unsigned char scratch[W4A8_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// This device's copy of `scratch`, or a status code.
+int scratch_for_current_device(void** out) {
+    int dev = 0;
+    if (int rc = hip_status(hipGetDevice(&dev), "w4a8_gemm_noalloc: hipGetDevice")) return rc;
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(W4A8_ERR_UNSUPPORTED, "w4a8_gemm_noalloc: device %lld beyond the %lld supported", dev,
+                    kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        if (int rc = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "w4a8_gemm_noalloc: hipGetSymbolAddress"))
+            return rc;
+        if (p == nullptr || !aligned(p, 256))
+            return fail(W4A8_ERR_HIP, "w4a8_gemm_noalloc: scratch of device %lld is not 256-byte aligned", dev);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return W4A8_OK;
+}
+
 }  // namespace
 }  // namespace w4a8
 
@@ -233,6 +266,22 @@ int w4a8_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_t
               void* workspace, int64_t workspace_bytes, void* stream) {
     return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, nullptr, M, N, K, group,
                     workspace, workspace_bytes, stream);
+}
+
+int w4a8_gemm_noalloc(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles, const void* s_tiles,
+                      int scale_dtype, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t group,
+                      void* stream) {
+    if (int rc = check_problem(M, N, K, group)) return rc;
+    const int64_t need = w4a8_gemm_workspace_bytes(M, N, K, group);
+    if (need > W4A8_NOALLOC_SCRATCH_BYTES)
+        return fail(W4A8_ERR_WORKSPACE, "w4a8_gemm_noalloc: the shape needs %lld bytes of scratch, the static scratch "
+                    "holds %lld (use w4a8_gemm with a workspace)", need, W4A8_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (need > 0 && M > 0)
+        if (int rc = scratch_for_current_device(&ws)) return rc;
+    // the split sums need no clearing: the split GEMM writes every sum its reduce reads
+    return run_gemm(a_q, lda, a_scale, w_tiles, s_tiles, scale_dtype, y, ldy, nullptr, M, N, K, group, ws,
+                    ws ? W4A8_NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 int w4a8_gemm_swiglu(const void* a_q, int64_t lda, const void* a_scale, const void* w_tiles,
