@@ -23,6 +23,23 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD MI355X GPU (gfx950)")
 
 
+# (tag, outputs checked, outputs that needed the float64 value) per output check
+# of the parity tests, reported at the end of the session
+OUTPUT_CHECKS: list = []
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not OUTPUT_CHECKS:
+        return
+    n = sum(c[1] for c in OUTPUT_CHECKS)
+    fb = [c for c in OUTPUT_CHECKS if c[2]]
+    terminalreporter.write_line(
+        f"bf16 output bar: {len(OUTPUT_CHECKS)} checks, {n} outputs; {sum(c[2] for c in fb)} outside 1 ulp of "
+        f"the fp32 oracle, all within 1 ulp of the float64 value, in {len(fb)} checks")
+    for tag, size, k in fb[:40]:
+        terminalreporter.write_line(f"  {tag}: {k} of {size}")
+
+
 @pytest.fixture(scope="session")
 def pkg():
     return __graft_entry__.package()

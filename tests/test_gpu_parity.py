@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import bf16_bits_tensor, tensor_bf16_bits, tie_rows
+from conftest import OUTPUT_CHECKS, bf16_bits_tensor, tensor_bf16_bits, tie_rows
 from oracle import w4a8 as ow
 
 pytestmark = pytest.mark.gpu
@@ -65,7 +65,7 @@ def check_output(y_bits: np.ndarray, y32: np.ndarray, tag: str, exact) -> None:
     and >= 99% of them bit-equal.
     """
     fail, n_fb = ow.output_bar(y_bits, y32, exact)
-    say(f"  {tag}: {n_fb} of {y32.size} outputs outside 1 ulp of the fp32 oracle, checked against float64")
+    OUTPUT_CHECKS.append((tag, int(y32.size), n_fb))
     assert not fail.any(), f"{tag}: {int(fail.sum())} outputs outside 1 bf16 ulp of both the fp32 and float64 oracle"
     y = ow.bf16_bits_to_f32(y_bits).astype(np.float64)
     rb = ow.round_bf16(y32).astype(np.float64)
