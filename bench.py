@@ -65,10 +65,11 @@ def main():
     ap.add_argument("--cold-bytes", type=float, default=1.0, help="GiB of distinct weight copies to rotate")
     ap.add_argument("--detail-launches", type=int, default=40)
     ap.add_argument("--prefill-m", default="1024,4096,16384")
-    ap.add_argument("--decoder", action="store_true",
-                    help="also run configs[4]: the 64-layer QwQ-32B-shaped decoder, 1024-token prompts + 256 "
-                         "greedy decode steps at concurrency 1, 8, 64")
+    ap.add_argument("--no-decoder", action="store_true",
+                    help="skip configs[4]: the 64-layer QwQ-32B-shaped decoder, 1024-token prompts + "
+                         "--decoder-steps greedy decode steps at concurrency 1, 8, 64 (run by default)")
     ap.add_argument("--decoder-layers", type=int, default=64)
+    ap.add_argument("--decoder-steps", type=int, default=64)
     ap.add_argument("--compat", action="store_true",
                     help="also time the reference-compat mid-group pair (group 1024, asymmetric) at M 1/16/64/1024")
     ap.add_argument("--config4", action="store_true",
@@ -261,6 +262,8 @@ def main():
         return sorted(times)[len(times) // 2]
 
     shapes = []
+    floors = {}
+    copy_dst = {}
     tot_bytes = tot_us = 0.0
     for M in DECODE_MS:
         for p in PROJS:
@@ -281,8 +284,18 @@ def main():
                     wt, st = weights[p][i % len(weights[p])]
                     torch.ops.npu.w4a8_linear(xs[(M, p)], wt, st, N, K, GROUP)
 
+            if p not in copy_dst:
+                copy_dst[p] = torch.empty_like(weights[p][0][0])
+
+            def floor_reads(p=p):
+                # the same pool rotation moved by a stock torch device copy (weight tiles)
+                for i in range(T):
+                    copy_dst[p].copy_(weights[p][i % len(weights[p])][0])
+
             us = time_graph(gemms) / T
             qus = time_graph(quants) / T
+            fus = time_graph(floor_reads) / T if M == DECODE_MS[0] else floors[p]
+            floors[p] = fus
             # quant + GEMM through w4a8_linear, on the step's stream
             lus = time_graph(linears, stream=torch.cuda.current_stream(dev)) / T
             x0 = xs[(M, p)]
@@ -293,9 +306,12 @@ def main():
             shapes.append({"proj": p, "M": M, "N": N, "K": K, "gemm_us": round(us, 3),
                            "gemm_GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                            "TOPS": round(2 * M * N * K / us / 1e6, 2), "quant_us": round(qus, 3),
-                           "linear_us": round(lus, 3), "linear_fused": fused})
+                           "linear_us": round(lus, 3), "linear_fused": fused,
+                           "copy_us": round(fus, 3)})
+            cgb = 2 * weights[p][0][0].numel() / fus / 1e3
             log(f"  {p:13s} M={M:3d}: gemm {us:8.2f} us {b / us / 1e3:7.1f} GB/s ({b / us / 1e3 / HBM_PEAK_GBS:.1%})"
-                f"  quant {qus:6.2f} us  linear {lus:7.2f} us{' (fused)' if fused else ''}")
+                f"  quant {qus:6.2f} us  linear {lus:7.2f} us{' (fused)' if fused else ''}  "
+                f"copy {fus:6.2f} us ({cgb:6.0f} GB/s)")
     achieved = tot_bytes / tot_us / 1e3
     # HBM bytes per launch from the two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) recorded in
     # profiles/ (the command is in the summary), each scaled by a 256 MiB copy's reading.
@@ -313,6 +329,12 @@ def main():
         "traffic_source": str(traffic_src.relative_to(ROOT)) if traffic is not None else None,
     }
     result["decode_shapes"] = shapes
+    result["stock_copy"] = {
+        "what": ("per projection, a stock torch device copy (Tensor.copy_) of each pool copy's repacked weight "
+                 "tiles into one buffer of the same size, graph-replayed back to back over the same rotation as "
+                 "the GEMMs: what stock code moves at each weight size, cold reads plus writes"),
+        "us": {p: round(floors[p], 3) for p in PROJS},
+        "GBs_read_plus_write": {p: round(2 * weights[p][0][0].numel() / floors[p] / 1e3, 1) for p in PROJS}}
     result["gpu_clocks"] = {"after_timed_region": clocks,
                             "note": "rocm-smi reading; the peaks above are MI355X's published figures (2.4 GHz)"}
 
@@ -322,7 +344,21 @@ def main():
         for p in PROJS:
             K, N = synth.QWQ_SHAPES[p]
             x = synth.activations_device(M, K, seed=M, device=dev)
+            # the first quant call on these freshly allocated buffers, then the warm kernel time
+            torch.cuda.synchronize()
+            e0, e1 = ev(), ev()
+            e0.record()
             a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x)
+            e1.record()
+            torch.cuda.synchronize()
+            q_first = e0.elapsed_time(e1) * 1e3
+            Tq = max(2, min(20, int(4e4 // max(1, M))))
+
+            def quants_p(x=x, Tq=Tq):
+                for _ in range(Tq):
+                    torch.ops.npu.w4a8_quant_pertoken(x)
+
+            q_us = time_graph(quants_p) / Tq
             Tp = max(2, min(10, int(2e4 // max(1, M))))
 
             def gemms(a_q=a_q, a_s=a_s, p=p, K=K, N=N, Tp=Tp):
@@ -334,23 +370,39 @@ def main():
             tops = 2 * M * N * K / us / 1e6
             prefill.append({"proj": p, "M": M, "gemm_us": round(us, 2), "TOPS": round(tops, 1),
                             "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
-                            "GBs": round(gemm_bytes(M, N, K) / us / 1e3, 1)})
-            log(f"  prefill {p:13s} M={M:5d}: {us:9.1f} us {tops:7.1f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)")
+                            "GBs": round(gemm_bytes(M, N, K) / us / 1e3, 1),
+                            "quant_us": round(q_us, 2), "quant_GBs": round(quant_bytes(M, K) / q_us / 1e3, 1),
+                            "quant_first_call_us": round(q_first, 1)})
+            log(f"  prefill {p:13s} M={M:5d}: {us:9.1f} us {tops:7.1f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)"
+                f"  quant {q_us:8.1f} us ({quant_bytes(M, K) / q_us / 1e3:6.0f} GB/s; first call {q_first:8.1f} us)")
             del x, a_q, a_s
     result["prefill_shapes"] = prefill
     if prefill:
         # right after the MFMA-bound prefill loop: the clock that kernel ran at
         result["gpu_clocks"]["after_prefill"] = gpu_clocks()
+        at = [r for r in prefill if r["M"] == 4096] or prefill
+        ops = sum(2 * r["M"] * synth.QWQ_SHAPES[r["proj"]][1] * synth.QWQ_SHAPES[r["proj"]][0] for r in at)
+        us_tot = sum(r["gemm_us"] for r in at)
+        ach = ops / us_tot / 1e6
+        result["roofline_prefill"] = {
+            "kernel": f"gemm_prefill_kernel, the four configs[2] projections at M={at[0]['M']}, group 128 "
+                      f"(algorithmic ops 2*M*N*K per call over the summed call times)",
+            "bound": "mfma", "achieved": round(ach, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+            "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": None,
+            "per_launch_ops_avg": round(ops / len(at)), "launch_us_avg": round(us_tot / len(at), 2),
+            "timing": "HIP events around graph replays of back-to-back launches"}
 
+    # the decode pools are not needed past this point
+    weights = None
+    torch.cuda.empty_cache()
     # ---------------------------------------------------------------- mid-group variants
     if args.config4:
-        del weights
-        torch.cuda.empty_cache()
         result["config4_shapes"] = config4(pkg, dev, synth, make_pool, time_graph, T)
     if args.compat:
         result["compat_shapes"] = compat(pkg, dev, synth, time_graph, T, args.cold_bytes)
-    if args.decoder:
-        result["decoder"] = decoder_bench(pkg, dev, args.decoder_layers)
+    # ---------------------------------------------------------------- decoder forward
+    if not args.no_decoder:
+        result["decoder"] = decoder_bench(pkg, dev, args.decoder_layers, steps=args.decoder_steps)
 
     # ---------------------------------------------------------------- CPU baseline
     if not args.no_cpu_baseline:
