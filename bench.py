@@ -74,6 +74,8 @@ def main():
                     help="also time the reference-compat mid-group pair (group 1024, asymmetric) at M 1/16/64/1024")
     ap.add_argument("--config4", action="store_true",
                     help="also time configs[3]: groups 64/256/512 at M 16/4096, gate_up with the fused SwiGLU")
+    ap.add_argument("--no-perchannel", action="store_true",
+                    help="skip the per-channel (group = K) points beside the reference's published ones")
     ap.add_argument("--no-detail", action="store_true", help="only the timed steps (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -395,6 +397,9 @@ def main():
     # the decode pools are not needed past this point
     weights = None
     torch.cuda.empty_cache()
+    # ---------------------------------------------------------------- per-channel (group = K)
+    if not args.no_perchannel:
+        result["perchannel_shapes"] = perchannel(pkg, dev, synth, make_pool, time_graph, T)
     # ---------------------------------------------------------------- mid-group variants
     if args.config4:
         result["config4_shapes"] = config4(pkg, dev, synth, make_pool, time_graph, T)
@@ -492,6 +497,56 @@ def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
             f"{dec_ms / steps:7.3f} ms/step ({B * steps / dec_ms * 1e3:8.1f} tok/s)")
     del m
     torch.cuda.empty_cache()
+    return rows
+
+
+# The reference's published per-channel W4A8 kernel times on its 910B4
+# (int4_cube_lab/results/midgroup_w4a8_qwen.csv, rows "w4a8_pc": avg_us per
+# projection and M; the CSV line of each value in the key).
+REF_PERCHANNEL_US = {
+    ("qkv_proj", 1): (28.26, 3), ("qkv_proj", 4): (28.46, 6), ("qkv_proj", 16): (28.57, 9),
+    ("qkv_proj", 64): (34.81, 12), ("qkv_proj", 1024): (186.51, 21),
+    ("o_proj", 1): (23.98, 24), ("o_proj", 4): (24.10, 27), ("o_proj", 16): (24.32, 30),
+    ("o_proj", 64): (28.97, 33), ("o_proj", 1024): (136.85, 42),
+    ("gate_up_proj", 1): (132.83, 45), ("gate_up_proj", 4): (132.80, 48), ("gate_up_proj", 16): (132.91, 51),
+    ("gate_up_proj", 64): (165.74, 54), ("gate_up_proj", 1024): (1564.72, 63),
+    ("down_proj", 1): (72.17, 66), ("down_proj", 4): (72.35, 69), ("down_proj", 16): (72.78, 72),
+    ("down_proj", 64): (97.98, 75), ("down_proj", 1024): (710.03, 84),
+}
+
+
+def perchannel(pkg, dev, synth, make_pool, time_graph, T, ms=(1, 4, 16, 64, 1024)):
+    """Per-channel weights (one group spanning K): GEMM time per projection and M on cold
+    pools, beside the reference's published time for the same point."""
+    import numpy as np
+    import torch
+    rows = []
+    for pi, p in enumerate(PROJS):
+        K, N = synth.QWQ_SHAPES[p]
+        pool = make_pool(p, K, "uniform", torch.bfloat16, 5000 + 100 * pi)
+        for M in ms:
+            x = torch.from_numpy(synth.activations(M, K, seed=M + 50).view(np.int16)).view(torch.bfloat16).to(dev)
+            a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, K)
+            Tm = T if M <= 64 else max(2, T // 8)
+
+            def gemms(a_q=a_q, a_s=a_s, K=K, N=N, Tm=Tm):
+                for i in range(Tm):
+                    wt, st = pool[i % len(pool)]
+                    torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, K)
+
+            us = time_graph(gemms) / Tm
+            b = gemm_bytes(M, N, K, K)
+            ref_us, line = REF_PERCHANNEL_US[(p, M)]
+            rows.append({"proj": p, "M": M, "N": N, "K": K, "group": K, "gemm_us": round(us, 3),
+                         "GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                         "TOPS": round(2 * M * N * K / us / 1e6, 1),
+                         "reference_910b4_us": ref_us,
+                         "reference_source": f"int4_cube_lab/results/midgroup_w4a8_qwen.csv:{line}",
+                         "speedup_vs_reference": round(ref_us / us, 2)})
+            log(f"  per-channel {p:13s} M={M:5d}: {us:9.2f} us {b / us / 1e3:7.1f} GB/s "
+                f"({b / us / 1e3 / HBM_PEAK_GBS:.1%}), reference 910B4 {ref_us} us")
+        del pool
+        torch.cuda.empty_cache()
     return rows
 
 

@@ -135,3 +135,28 @@ def test_gpu_golden_midgroup(pkg, dev):
     torch.cuda.synchronize()
     # the compat GEMM evaluates the reference's own fp32 order
     assert np.array_equal(tensor_bf16_bits(y)[:M], gv("mg_y"))
+
+
+@pytest.mark.gpu
+def test_gpu_golden_perchannel(pkg, dev):
+    """The reference's ReferencePerchannelGemm output on the same per-channel inputs
+    (its association float(P) * as * ws differs from the kernel's by fp32 rounding only)."""
+    import torch
+    from conftest import tensor_bf16_bits
+    M, K, N = (int(v) for v in gv("pc_shape"))
+    print(f"golden per-channel M={M} K={K} N={N}", flush=True)
+    ws = torch.from_numpy(gv("pc_ws").reshape(1, N).view(np.int16)).view(torch.bfloat16).to(dev)
+    wt, st = torch.ops.npu.w4a8_repack(torch.from_numpy(gv("pc_wq")).to(dev), ws, K, K)
+    x = torch.from_numpy(gv("pc_x").view(np.int16)).view(torch.bfloat16).to(dev)
+    y = torch.ops.npu.w4a8_linear(x, wt, st, N, K, K)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, K)
+    y2, P = torch.ops.npu.w4a8_gemm_partials(a_q, a_s, wt, st, N, K, K)
+    torch.cuda.synchronize()
+    codes = unpacked(gv("pc_wq"), K, K)
+    assert np.array_equal(P[0].cpu().numpy().astype(np.int64),
+                          gv("pc_aq").astype(np.int64) @ codes.astype(np.int64).T)
+    ws32 = ow.bf16_bits_to_f32(gv("pc_ws"))[:, None].astype(np.float32)
+    y32 = ow.gemm_fp32(gv("pc_aq"), gv("pc_as"), codes, ws32, K)
+    for got in (tensor_bf16_bits(y), tensor_bf16_bits(y2)):
+        bar_and_equal(got, gv("pc_y"), y32, lambda r, c: ow.gemm_f64(gv("pc_aq")[r], gv("pc_as")[r], codes[c],
+                                                                     ws32[c], K))

@@ -389,6 +389,79 @@ def test_gemm_row_chunks_large_m(pkg, dev):
     check_output(tensor_bf16_bits(y.index_select(0, rt)), y32, "row chunks", exact_sym(q_ref, s_ref, w, ws32, G))
 
 
+# Per-channel weights (one group spanning K, the reference's per-channel variant,
+# int4_cube_lab/kernels/perchannel_w4a8_gemm.inc): the K split falls on any tile and
+# the waves' / workgroups' int32 sums are added before the one fold.
+PERCHANNEL_CASES = [
+    # (M, N, K, scale dtype)
+    (1, 512, 5120, "f16"),        # fused single-row path's kernel plan, ten waves
+    (4, 320, 27648, "bf16"),      # eight waves over 216 tiles
+    (16, 256, 27648, "f16"),      # K split over workgroups, int32 sums reduced by the second kernel
+    (40, 1000, 16384, "bf16"),    # the 32-row split layout
+    (64, 200, 27648, "f16"),      # the 64-row split layout
+    (24, 640, 5120, "bf16"),      # row groups
+    (12, 33024, 1024, "f16"),     # wide N, one split
+    (3, 136, 5000, "bf16"),       # K % 128 != 0: a padding slab in the last tile
+    (300, 512, 5120, "f16"),      # prefill
+    (130, 264, 27648, "bf16"),    # prefill, long K (|16P| may exceed 2^24: fp32 rounding of the one fold)
+]
+
+
+@pytest.mark.parametrize("M,N,K,sd", PERCHANNEL_CASES)
+def test_gemm_perchannel_partials_and_output(pkg, dev, M, N, K, sd):
+    G = K
+    say(f"per-channel M={M} N={N} K={K}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + N + 1, scale_dtype=sd)
+    y, P, a_q, a_s = run_hip(dev, xb, w, w_scale, N, K, G)
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    P_ref = ow.group_partials(q_ref, w, G)
+    assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
+    y2, _, _, _ = run_hip(dev, xb, w, w_scale, N, K, G, partials=False)
+    assert torch.equal(y, y2), "the partial dump changed the output"
+    y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref)
+    check_output(tensor_bf16_bits(y), y32, f"per-channel M{M} N{N} K{K}", exact_sym(q_ref, s_ref, w, ws32, G))
+
+
+@pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
+@pytest.mark.parametrize("M", [1, 16, 64, 1024])
+def test_gemm_qwq_perchannel(pkg, dev, proj, M):
+    """The QwQ-32B projections with per-channel scales (G = K), decode and prefill
+    rows, through w4a8_linear (the fused single-row launch at M=1); sampled columns."""
+    K, N = pkg.synth.QWQ_SHAPES[proj]
+    say(f"qwq per-channel {proj} M={M}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, K, seed=M + 3)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(torch.from_numpy(ow.pack_grouped(w, K)).to(dev),
+                                                 w_scale.to(dev), K, K)
+    y = torch.ops.npu.w4a8_linear(bf16_bits_tensor(xb).to(dev), w_tiles, s_tiles, N, K, K)
+    torch.cuda.synchronize()
+    cols = np.sort(np.random.default_rng(M).choice(N, 256, replace=False))
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], K)
+    check_output(tensor_bf16_bits(y)[:, cols], y32, f"per-channel {proj} M{M}",
+                 exact_sym(q_ref, s_ref, w[cols], ws32[cols], K))
+
+
+def test_gemm_perchannel_every_decode_row_count(pkg, dev):
+    """Every M from 1 to 64 with per-channel scales on a narrow N with long K (the K
+    split over workgroups with int32 sums from 9 rows on) and a narrow N with short K."""
+    cols_rng = np.random.default_rng(19)
+    for N, K in ((1000, 16384), (640, 5120)):
+        xb_all, w, ws32, w_scale = make_problem(pkg, 64, N, K, K, seed=N + 7)
+        w_tiles, s_tiles = torch.ops.npu.w4a8_repack(torch.from_numpy(ow.pack_grouped(w, K)).to(dev),
+                                                     w_scale.to(dev), K, K)
+        cols = np.sort(cols_rng.choice(N, 48, replace=False))
+        for M in range(1, 65):
+            say(f"per-channel rows M={M} N={N} K={K}")
+            xb = xb_all[:M]
+            a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(bf16_bits_tensor(xb).to(dev), K)
+            y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, K)
+            torch.cuda.synchronize()
+            q_ref, s_ref = ow.quant_act_per_token(xb)
+            y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], K)
+            check_output(tensor_bf16_bits(y)[:, cols], y32, f"per-channel M{M} N{N} K{K}",
+                         exact_sym(q_ref, s_ref, w[cols], ws32[cols], K))
+
+
 def test_gemm_every_decode_row_count(pkg, dev):
     """Every M from 1 to 64 on a wide (2048 column groups) and a narrow N, and on a
     narrow N with long K: each picks a built kernel variant (a missing one is a launch

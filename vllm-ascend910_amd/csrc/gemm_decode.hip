@@ -75,9 +75,11 @@ constexpr uint32_t kOOB = 0x80000000u;
 // tile), 1 = stride 128 * 2^gshift, gshift >= 1 (groups end on a tile's upper
 // slab, or on the last tile), 2 = any other stride (a group ends on either
 // slab; a short last group may end right after another group in the same
-// tile, so each slab carries its own scale).  Modes 0 and 3 start every group
-// with a zero accumulator operand; 1 and 2, whose group starts are runtime
-// values, clear the accumulators after each fold.
+// tile, so each slab carries its own scale), 4 = one group over all of K
+// (per-channel scales): the K split then falls on any tile, the waves' int32
+// sums are added exactly in LDS and folded once.  Modes 0 and 3 start every
+// group with a zero accumulator operand; 1 and 2, whose group starts are
+// runtime values, clear the accumulators after each fold.
 // SWIGLU: the workgroup's first CPW/2 column blocks are gate blocks and the
 // rest the matching up blocks (output column n = silu(y[:, n]) * y[:, n + N/2]);
 // every column accumulates exactly as in the plain GEMM.
@@ -181,7 +183,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     // ending in them (two per tile for group 64, one otherwise), and DA tiles
     // of activations (L2-resident, so a shallower ring keeps the registers of
     // the 32- to 64-row tiles in budget).
-    constexpr int NS = (GM == 1 || GM == 3) ? 1 : 2;
+    constexpr int NS = (GM == 1 || GM == 3 || GM == 4) ? 1 : 2;
+    constexpr bool ONE = GM == 4;   // one group: int32 sums across the whole K range
     constexpr int DA = MT >= 3 ? 2 : D;
     static_assert(D % DA == 0, "activation ring depth must divide D");
     uint4 wb[D][CPW];
@@ -209,6 +212,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
         const auto rw = make_rsrc_at(p.W, static_cast<uint32_t>(t) * 1024u, t < tb ? p.w_bytes : 0u);
 #pragma unroll
         for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, wo[c]);
+        if constexpr (ONE) return;   // the one scale per column is loaded once, before the loop
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             const auto rs = make_rsrc_at(p.S, static_cast<uint32_t>(gend(min(t, p.KT - 1), j)) * 32u, p.s_bytes);
@@ -284,7 +288,9 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
                     for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(a, b[c][h], fresh ? v4i{0, 0, 0, 0} : P[mt][c]);
                 }
                 if (h == 1) load_a(s % DA, t + DA);
-                if constexpr (GM == 0) {
+                if constexpr (ONE) {
+                    // folded once, after the waves' sums meet
+                } else if constexpr (GM == 0) {
                     // a padding slab past S folds group NG: zero partials,
                     // not dumped
                     fold(2 * t + h, t < tb, sc, h);
@@ -320,9 +326,15 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
                 xv[m][i] = ok ? *reinterpret_cast<const uint4*>(p.X + m * p.ldx + k0 + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
             }
     }
+    uint32_t ws1[CPW];   // ONE: the scale of each column block's columns of this lane
     if (busy) {
 #pragma unroll
         for (int s = 0; s < D; ++s) load_slot(s, ta + s);
+    }
+    if constexpr (ONE) {
+        const auto rs = make_rsrc(p.S, p.s_bytes);
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) ws1[c] = buf_load_u16(rs, so[c]);
     }
     if constexpr (QF) {
         uint32_t am[QM];
@@ -384,17 +396,46 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
         pass(iters - 1, std::false_type{});
     }
 
-    // Fixed-order reduction of the kw wave partials, then the epilogue.
+    // Fixed-order reduction of the kw wave partials, then the epilogue.  With
+    // one group the waves' int32 sums are added (exactly, so the order does
+    // not matter) and folded with the column's scale once.
+    __shared__ float wsl[ONE ? C : 1];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int c = 0; c < CPW; ++c)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave * R * C + (mt * 16 + rowq + i) * C + c * 16 + colq] = acc[mt][c][i];
+            for (int i = 0; i < 4; ++i) {
+                float* r = &red[wave * R * C + (mt * 16 + rowq + i) * C + c * 16 + colq];
+                if constexpr (ONE) *reinterpret_cast<int*>(r) = P[mt][c][i];
+                else *r = acc[mt][c][i];
+            }
+    if constexpr (ONE) {
+        if (wave == 0 && lane < 16) {
+#pragma unroll
+            for (int c = 0; c < CPW; ++c) wsl[c * 16 + colq] = scale_to_f32<SBF16>(ws1[c]);
+        }
+    }
     if constexpr (!QF) {
         if (static_cast<int>(threadIdx.x) < R) tsc[threadIdx.x] = ts_bits;
     }
     __syncthreads();
+    // the fp32 sum (before the token scale) of local element e = row * C + cc
+    auto colsum = [&](int e, int cc) -> float {
+        if constexpr (ONE) {
+            int isum = reinterpret_cast<const int*>(red)[e];
+            for (int w = 1; w < kw; ++w) isum += reinterpret_cast<const int*>(red)[w * R * C + e];
+            if constexpr (DUMP) {
+                const int row = e / C, col = block_of(cc / 16) * 16 + cc % 16;
+                if (m0 + row < p.M && col < p.N) p.P[static_cast<int64_t>(m0 + row) * p.N + col] = isum >> 4;
+            }
+            return static_cast<float>(isum) * wsl[cc];
+        } else {
+            float sum = red[e];
+            for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
+            return sum;
+        }
+    };
     if constexpr (SWIGLU) {
         constexpr int CH = C / 2;
         for (int e = threadIdx.x; e < R * CH; e += blockDim.x) {
@@ -402,11 +443,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
             const int cc = e - row * CH;
             const int col = nb0 * 16 + cc;
             if (m0 + row >= p.M || col >= p.up_nb * 16) continue;
-            float sg = red[row * C + cc], su = red[row * C + CH + cc];
-            for (int w = 1; w < kw; ++w) {
-                sg += red[w * R * C + row * C + cc];
-                su += red[w * R * C + row * C + CH + cc];
-            }
+            const float sg = colsum(row * C + cc, cc), su = colsum(row * C + CH + cc, CH + cc);
             const float ts = bf16_bits_to_f32(tsc[row]) * 0.0625f;
             p.Y[static_cast<int64_t>(m0 + row) * p.ldy + col] = static_cast<uint16_t>(swiglu_bf16_bits(sg * ts, su * ts));
         }
@@ -415,8 +452,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
             const int row = e / C;
             const int col = nb0 * 16 + (e - row * C);
             if (m0 + row >= p.M || col >= p.N) continue;
-            float sum = red[e];
-            for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
+            const float sum = colsum(e, e - row * C);
             const uint32_t tsb = QF ? reinterpret_cast<const uint32_t*>(lds + lq_s)[row] : tsc[row];
             const float ts = bf16_bits_to_f32(tsb) * 0.0625f;
             p.Y[static_cast<int64_t>(m0 + row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum * ts));
@@ -471,9 +507,10 @@ hipError_t launch_g(const DecodeParams& p, int kw, bool sbf16, hipStream_t strea
     }
 }
 
-// Group mode by group stride: 64 -> 0; 128 -> 3; 128 * 2^s, s >= 1 -> 1;
-// anything else -> 2.
-int group_mode(int spg) {
+// Group mode: one group over all of K -> 4; otherwise by group stride: 64 ->
+// 0; 128 -> 3; 128 * 2^s, s >= 1 -> 1; anything else -> 2.
+int group_mode(int spg, int ng) {
+    if (ng == 1) return 4;
     if (spg == 1) return 0;
     if (spg == 2) return 3;
     if (spg % 2 == 0 && ((spg / 2) & (spg / 2 - 1)) == 0) return 1;
@@ -482,10 +519,11 @@ int group_mode(int spg) {
 
 template <int MT, int CPW, int D, int MODE>
 hipError_t launch_v(const DecodeParams& p, int kw, bool sbf16, hipStream_t stream) {
-    switch (group_mode(p.spg)) {
+    switch (group_mode(p.spg, p.NG)) {
         case 0: return launch_g<MT, CPW, D, 0, MODE>(p, kw, sbf16, stream);
         case 1: return launch_g<MT, CPW, D, 1, MODE>(p, kw, sbf16, stream);
         case 3: return launch_g<MT, CPW, D, 3, MODE>(p, kw, sbf16, stream);
+        case 4: return launch_g<MT, CPW, D, 4, MODE>(p, kw, sbf16, stream);
         default: return launch_g<MT, CPW, D, 2, MODE>(p, kw, sbf16, stream);
     }
 }
@@ -536,8 +574,9 @@ DecodeParams make_params(const GemmArgs& a) {
     p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + geom::kpad(a.K, a.group));
     p.w_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.KT) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(p.NB * static_cast<int64_t>(p.NG) * 16 * 2);
-    // K-split boundaries fall on both tile (2 slabs) and group boundaries.
-    p.unit = (2 * p.spg / gcd_i(2, p.spg)) / 2;
+    // K-split boundaries fall on both tile (2 slabs) and group boundaries --
+    // any tile for a single group, whose int32 sums the waves add before the fold.
+    p.unit = p.NG == 1 ? 1 : (2 * p.spg / gcd_i(2, p.spg)) / 2;
     p.units = (p.KT + p.unit - 1) / p.unit;
     return p;
 }
@@ -551,7 +590,8 @@ hipError_t launch_fused_g(const DecodeParams& p, int kw, size_t lds, hipStream_t
 }
 
 hipError_t launch_fused(const DecodeParams& p, int kw, size_t lds, bool sbf16, hipStream_t s) {
-    switch (group_mode(p.spg)) {
+    switch (group_mode(p.spg, p.NG)) {
+        case 4: return sbf16 ? launch_fused_g<4, true>(p, kw, lds, s) : launch_fused_g<4, false>(p, kw, lds, s);
         case 0: return sbf16 ? launch_fused_g<0, true>(p, kw, lds, s) : launch_fused_g<0, false>(p, kw, lds, s);
         case 1: return sbf16 ? launch_fused_g<1, true>(p, kw, lds, s) : launch_fused_g<1, false>(p, kw, lds, s);
         case 3: return sbf16 ? launch_fused_g<3, true>(p, kw, lds, s) : launch_fused_g<3, false>(p, kw, lds, s);

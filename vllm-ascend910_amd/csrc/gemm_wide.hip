@@ -63,14 +63,17 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // GM: the group modes of gemm_decode.hip (0: stride 64, 3: stride 128,
-// 1: stride 128 * 2^gshift, 2: any other stride).
+// 1: stride 128 * 2^gshift, 2: any other stride, 4: one group over all of K).
+// Mode 4 folds once after the K loop; with K split over workgroups it writes
+// the int32 sums instead, which wide_reduce_kernel adds exactly and folds.
 // kMT 16-row tiles, kWN column waves, kCPW 16-column blocks per wave, kD
 // weight ring depth, kRA activation tiles in flight.
 template <int kMT, int kWN, int kCPW, int kD, int kRA, int GM, bool SBF16, bool DUMP, bool SWIGLU>
 __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p) {
     static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
     constexpr int CG = SWIGLU ? kCPW / 2 : kCPW;   // output column blocks per wave
-    constexpr int NS = (GM == 1 || GM == 3) ? 1 : 2;
+    constexpr int NS = (GM == 1 || GM == 3 || GM == 4) ? 1 : 2;
+    constexpr bool ONE = GM == 4;
     constexpr int U = kD > kRA ? kD : kRA;           // unroll: every ring slot index is static
     static_assert(U % kD == 0 && U % kRA == 0 && U % 2 == 0, "ring depths must divide the unroll");
     constexpr int kATile = 16 * kMT * kALS;
@@ -156,6 +159,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
         const auto rw = make_rsrc_at(p.W, static_cast<uint32_t>(min(t, p.KT - 1)) * 1024u, t < tb ? p.w_bytes : 0u);
 #pragma unroll
         for (int c = 0; c < kCPW; ++c) wb[s][c] = buf_load16(rw, wo[c]);
+        if constexpr (ONE) return;   // the one scale per column is loaded once
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             const auto rs = make_rsrc_at(p.S, static_cast<uint32_t>(gend(min(t, p.KT - 1), j)) * 32u, p.s_bytes);
@@ -202,6 +206,12 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     stage_load(ta, ra[0]);
 #pragma unroll
     for (int s = 0; s < kD; ++s) load_slot(s, ta + s);
+    uint32_t ws1[kCPW];   // ONE: this lane's column scale per column block
+    if constexpr (ONE) {
+        const auto rs = make_rsrc(p.S, p.s_bytes);
+#pragma unroll
+        for (int c = 0; c < kCPW; ++c) ws1[c] = buf_load_u16(rs, so[c]);
+    }
 #pragma unroll
     for (int r = 1; r < kRA; ++r) stage_load(ta + r, ra[r]);
     stage_store(0, ra[0]);
@@ -241,7 +251,9 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
                 for (int c = 0; c < kCPW; ++c)
                     P[mt][c] = mfma16(av[h][mt], b[c][h], fresh ? v4i{0, 0, 0, 0} : P[mt][c]);
             }
-            if constexpr (GM == 0) {
+            if constexpr (ONE) {
+                // folded once, after the K loop
+            } else if constexpr (GM == 0) {
                 fold(2 * t + h, sc, h);
             } else if constexpr (GM == 3) {
                 if (h == 1) fold(t, sc, 0);
@@ -263,7 +275,15 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     });
 
     // ---- epilogue: token scale, bf16 (or the SwiGLU pair); fp32 sums to
-    // the workspace when K is split
+    // the workspace when K is split (int32 sums for one group)
+    if constexpr (ONE) {
+        if (p.splits == 1) {
+            uint32_t sc1[kCPW][NS];
+#pragma unroll
+            for (int c = 0; c < kCPW; ++c) sc1[c][0] = ws1[c];
+            fold(0, sc1, 0);
+        }
+    }
     if (tid < 16 * kMT) tsc[tid] = ts_bits;
     __syncthreads();
 #pragma unroll
@@ -286,7 +306,10 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
 #pragma unroll
                 for (int c = 0; c < kCPW; ++c) {
                     const int col = block_of(c) * 16 + colq;
-                    if (col < p.N) r[col] = acc[mt][c][q];
+                    if (col < p.N) {
+                        if constexpr (ONE) reinterpret_cast<int*>(r)[col] = P[mt][c][q];
+                        else r[col] = acc[mt][c][q];
+                    }
                 }
             } else {
                 const float ts = bf16_bits_to_f32(tsc[row]) * 0.0625f;
@@ -303,10 +326,14 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
 
 // y[m, n] = bf16((R[0, m, n] + R[1, m, n] + ...) * token scale), four
 // columns per thread; R rows are ldr (a multiple of 16) floats apart and
-// columns from N to ldr are never written.
+// columns from N to ldr are never written.  ONE (a single group over K): R
+// holds int32 sums, added exactly and then folded with the column scale
+// (s_tiles of one group are indexed by column), and the dump P, if given,
+// receives the group's partial.
+template <bool ONE, bool SBF16>
 __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restrict__ R, int64_t ldr,
                                                           const uint16_t* a_scale, uint16_t* Y, int64_t ldy, int M,
-                                                          int N, int splits) {
+                                                          int N, int splits, const uint16_t* S, int32_t* P) {
     const int n4 = static_cast<int>(ldr >> 2);
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= static_cast<int64_t>(M) * n4) return;
@@ -323,13 +350,36 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
     for (int k = 0; k < kMaxSplits; ++k)
         v[k] = k < splits ? *reinterpret_cast<const float4*>(r + k * plane) : make_float4(0.f, 0.f, 0.f, 0.f);
     float4 s = v[0];
+    if constexpr (ONE) {
+        int4 is = *reinterpret_cast<const int4*>(&v[0]);
 #pragma unroll
-    for (int k = 1; k < kMaxSplits; ++k) {
-        if (k < splits) {
-            s.x += v[k].x;
-            s.y += v[k].y;
-            s.z += v[k].z;
-            s.w += v[k].w;
+        for (int k = 1; k < kMaxSplits; ++k) {
+            if (k < splits) {
+                const int4 t = *reinterpret_cast<const int4*>(&v[k]);
+                is.x += t.x;
+                is.y += t.y;
+                is.z += t.z;
+                is.w += t.w;
+            }
+        }
+        const int iv[4] = {is.x, is.y, is.z, is.w};
+        float sv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int cc = min(col + c, N - 1);
+            sv[c] = static_cast<float>(iv[c]) * scale_to_f32<SBF16>(S[cc]);
+            if (P != nullptr && col + c < N) P[static_cast<int64_t>(row) * N + col + c] = iv[c] >> 4;
+        }
+        s = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    } else {
+#pragma unroll
+        for (int k = 1; k < kMaxSplits; ++k) {
+            if (k < splits) {
+                s.x += v[k].x;
+                s.y += v[k].y;
+                s.z += v[k].z;
+                s.w += v[k].w;
+            }
         }
     }
     const float ts = bf16_bits_to_f32(tsb) * 0.0625f;
@@ -345,7 +395,8 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
     }
 }
 
-int group_mode_of(int spg) {
+int group_mode_of(int spg, int ng) {
+    if (ng == 1) return 4;
     if (spg == 1) return 0;
     if (spg == 2) return 3;
     if (spg % 2 == 0 && ((spg / 2) & (spg / 2 - 1)) == 0) return 1;
@@ -371,7 +422,8 @@ hipError_t launch_g(const WideParams& p, int cgroups, bool sbf16, hipStream_t s)
 
 template <int kMT, int kCPW, int kD, int kRA, bool DUMP, bool SWIGLU>
 hipError_t launch_gm(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
-    switch (group_mode_of(p.spg)) {
+    switch (group_mode_of(p.spg, p.NG)) {
+        case 4: return launch_g<kMT, kCPW, kD, kRA, 4, DUMP, SWIGLU>(p, cgroups, sbf16, s);
         case 0: return launch_g<kMT, kCPW, kD, kRA, 0, DUMP, SWIGLU>(p, cgroups, sbf16, s);
         case 1: return launch_g<kMT, kCPW, kD, kRA, 1, DUMP, SWIGLU>(p, cgroups, sbf16, s);
         case 3: return launch_g<kMT, kCPW, kD, kRA, 3, DUMP, SWIGLU>(p, cgroups, sbf16, s);
@@ -401,7 +453,8 @@ WideParams make_wide_params(const GemmArgs& a, int splits) {
     p.spg = static_cast<int>(geom::group_stride(a.group) / 64);
     p.gshift = 0;
     while ((2 << p.gshift) < p.spg) ++p.gshift;
-    p.unit = (2 * p.spg / gcd_w(2, p.spg)) / 2;   // lcm(2, spg) slabs, in tiles
+    // lcm(2, spg) slabs in tiles; any tile for a single group (int32 sums)
+    p.unit = p.NG == 1 ? 1 : (2 * p.spg / gcd_w(2, p.spg)) / 2;
     p.units = (p.KT + p.unit - 1) / p.unit;
     p.splits = a.swiglu ? 1 : std::max(1, std::min({splits, p.units, kMaxSplits}));
     p.ldr = static_cast<int64_t>(p.NB) * 16;
@@ -437,8 +490,18 @@ hipError_t launch_wide_v(const GemmArgs& a, WideParams p, hipStream_t stream) {
     else e = launch_gm<kMT, kCPW, kD, kRA, false, false>(p, c, a.scale_bf16, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     const int64_t n = static_cast<int64_t>(p.M) * (p.ldr / 4);
-    wide_reduce_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy,
-                                                                                   p.M, p.N, p.splits);
+    const dim3 rg(static_cast<unsigned>((n + 255) / 256));
+    if (p.NG == 1) {
+        if (a.scale_bf16)
+            wide_reduce_kernel<true, true><<<rg, 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N,
+                                                                    p.splits, p.S, p.P);
+        else
+            wide_reduce_kernel<true, false><<<rg, 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N,
+                                                                     p.splits, p.S, p.P);
+    } else {
+        wide_reduce_kernel<false, false><<<rg, 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N,
+                                                                  p.splits, nullptr, nullptr);
+    }
     return hipGetLastError();
 }
 
