@@ -211,7 +211,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
         // tiles past this wave's range read zero weights (an empty descriptor)
         const auto rw = make_rsrc_at(p.W, static_cast<uint32_t>(t) * 1024u, t < tb ? p.w_bytes : 0u);
 #pragma unroll
-        for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, wo[c]);
+        for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16_nt(rw, wo[c]);
         if constexpr (ONE) return;   // the one scale per column is loaded once, before the loop
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
@@ -482,12 +482,15 @@ int gcd_i(int a, int b) {
 
 // Most waves per workgroup a variant is built for (its register budget: the
 // 64-row, 4-block variant needs 256 VGPRs at 2 waves per SIMD).
-constexpr int kwmax_for(int mt, int cpw) { return mt == 1 ? (cpw >= 4 ? 8 : 12) : (mt == 2 || cpw <= 2 ? 8 : 4); }
+constexpr int kwmax_for(int mt, int cpw, int d) {
+    // one 16-row tile of one column block with a 4-deep ring fits 16 waves (128 VGPRs)
+    return mt == 1 ? (cpw >= 4 ? 8 : (cpw == 1 && d <= 4 ? 16 : 12)) : (mt == 2 || cpw <= 2 ? 8 : 4);
+}
 
 // MODE: 0 = plain, 1 = plain with partial dump, 2 = SwiGLU epilogue.
 template <int MT, int CPW, int D, int GM, int MODE>
 hipError_t launch_g(const DecodeParams& p, int kw, bool sbf16, hipStream_t stream) {
-    constexpr int KWM = kwmax_for(MT, CPW);
+    constexpr int KWM = kwmax_for(MT, CPW, D);
     constexpr bool DUMP = MODE == 1, SWIGLU = MODE == 2;
     if constexpr (SWIGLU && CPW % 2 != 0) {
         return hipErrorInvalidValue;
@@ -584,7 +587,7 @@ DecodeParams make_params(const GemmArgs& a) {
 // Fused quant + GEMM: MT = 1, CPW = 2, D = 4, plain epilogue, one row.
 template <int GM, bool SBF16>
 hipError_t launch_fused_g(const DecodeParams& p, int kw, size_t lds, hipStream_t stream) {
-    constexpr int KWM = kwmax_for(1, 2);
+    constexpr int KWM = kwmax_for(1, 2, 4);
     linear_decode_kernel<KWM, GM, SBF16><<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
     return hipGetLastError();
 }
@@ -623,7 +626,7 @@ bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f)
     // The GEMM's own K split (same waves, same ranges, same reduction order),
     // so the fused call equals quant + GEMM bit for bit.
     f.kw = c.KW;
-    if (f.kw < 1 || f.kw > kwmax_for(1, 2)) return false;
+    if (f.kw < 1 || f.kw > kwmax_for(1, 2, 4)) return false;
     const int tiles = f.p.unit * ((f.p.units + f.kw - 1) / f.kw);   // most tiles a wave owns
     f.p.qcpr = (tiles + 3) / 4;                                     // 16-byte chunks per row per lane
     if (f.p.qcpr > 8 / f.qm) return false;

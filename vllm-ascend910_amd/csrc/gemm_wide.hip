@@ -158,7 +158,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     auto load_slot = [&](int s, int t) {
         const auto rw = make_rsrc_at(p.W, static_cast<uint32_t>(min(t, p.KT - 1)) * 1024u, t < tb ? p.w_bytes : 0u);
 #pragma unroll
-        for (int c = 0; c < kCPW; ++c) wb[s][c] = buf_load16(rw, wo[c]);
+        for (int c = 0; c < kCPW; ++c) wb[s][c] = buf_load16_nt(rw, wo[c]);
         if constexpr (ONE) return;   // the one scale per column is loaded once
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
