@@ -88,12 +88,21 @@ def main():
                     help="turn two rocprofv3 --pmc databases of a --pmc-probe run (FETCH_SIZE, WRITE_SIZE) into "
                          "the per-shape HBM traffic table (markdown on stdout) and exit")
     ap.add_argument("--pmc-json", metavar="OUT", help="with --pmc-summary: also write the table as JSON")
+    ap.add_argument("--prefill-probe", type=int, metavar="M", default=0,
+                    help="for rocprofv3 runs: each configs[2] projection's prefill GEMM at M rows three times "
+                         "(eager, group 128), then a 256 MiB device copy of known size")
+    ap.add_argument("--prefill-pmc-summary", nargs="+", metavar="DB",
+                    help="summarize rocprofv3 databases of a --prefill-probe run (counter passes, then a "
+                         "--kernel-trace database last) for gemm_prefill_kernel as markdown and exit")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
         return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary, args.pmc_json)
+        return
+    if args.prefill_pmc_summary:
+        prefill_pmc_summary(args.prefill_pmc_summary)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the W4A8 linear is "
@@ -109,6 +118,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     props = torch.cuda.get_device_properties(dev)
+
+    if args.prefill_probe:
+        prefill_probe(pkg, dev, args.prefill_probe)
+        return
 
     # ---------------------------------------------------------------- data
     gen = torch.Generator(device=dev)
@@ -690,6 +703,109 @@ def pmc_summary(fetch_db, write_db, out_json=None):
         with open(out_json, "w") as fh:
             json.dump(dict(factor_fetch=ff, factor_write=fw, per_shape=out, avg_traffic_bytes=tot_tr / n,
                            avg_alg_bytes=tot_alg / n), fh, indent=1)
+
+
+def prefill_probe(pkg, dev, M, calls=3):
+    """Each projection's prefill GEMM at M rows, `calls` times on distinct weight copies
+    (eager, group 128, activations drawn on the device), then a 256 MiB copy."""
+    import torch
+    synth = pkg.synth
+    gen = torch.Generator(device=dev)
+    for pi, p in enumerate(PROJS):
+        K, N = synth.QWQ_SHAPES[p]
+        x = synth.activations_device(M, K, seed=M + pi, device=dev)
+        a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, GROUP)
+        for c in range(calls):
+            gen.manual_seed(77 + 10 * pi + c)
+            codes = torch.randint(-8, 8, (N, K), dtype=torch.int8, device=dev, generator=gen)
+            ws = (torch.rand((K // GROUP, N), device=dev, generator=gen) * 0.018 + 0.002).to(torch.float16)
+            wt, st = torch.ops.npu.w4a8_repack(pkg.packing.pack_int4(codes), ws, K, GROUP)
+            del codes
+            torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP)
+            torch.cuda.synchronize()
+            del wt, st
+        del x, a_q, a_s
+    src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"bench: prefill probe done ({len(PROJS)} projections x {calls} calls at M={M}, then a 268435456-byte copy)")
+
+
+def prefill_pmc_summary(dbs):
+    """Counter table of gemm_prefill_kernel from --prefill-probe runs: counter databases
+    (one pass each) and a --kernel-trace database (the last argument) for durations."""
+    import collections
+    import sqlite3
+    *pmc_dbs, trace_db = dbs
+    import __graft_entry__ as ge
+    synth = ge.package().synth
+    rows = sqlite3.connect(trace_db).execute(
+        "select name, duration, grid_x from kernels order by start").fetchall()
+    gemms = [(d, gx) for n, d, gx in rows if "gemm_prefill_kernel" in n]
+    per = max(1, len(gemms) // len(PROJS))
+    # the probe's order: each projection's calls in turn (PROJS order); M from
+    # the first projection's grid (128 x 128 tiles of 256 threads)
+    K0, N0 = synth.QWQ_SHAPES[PROJS[0]]
+    M = gemms[0][1] // 256 // -(-N0 // 128) * 128 if gemms else 0
+    dur = collections.defaultdict(list)
+    for i, (d, gx) in enumerate(gemms):
+        dur[PROJS[min(i // per, len(PROJS) - 1)]].append(d)
+    ctr = collections.defaultdict(lambda: collections.defaultdict(list))
+    cal = {}
+    for db in pmc_dbs:
+        con = sqlite3.connect(db)
+        ev = con.execute("select dispatch_id, name, counter_name, counter_value from pmc_events "
+                         "order by dispatch_id").fetchall()
+        # the probe's dispatch order: each projection's GEMM calls in turn (PROJS order)
+        gemm_ids = sorted({did for did, name, _, _ in ev if "gemm_prefill_kernel" in name})
+        per = max(1, len(gemm_ids) // len(PROJS))
+        which = {did: PROJS[min(i // per, len(PROJS) - 1)] for i, did in enumerate(gemm_ids)}
+        for did, name, cname, val in ev:
+            if "copy" in name.lower():
+                cal[cname] = val
+            elif did in which:
+                ctr[which[did]][cname].append(val)
+    avg = lambda v: sum(v) / len(v) if v else float("nan")  # noqa: E731
+    print(f"gemm_prefill_kernel at M={M}, group 128: per-dispatch counter averages (each counter from its own "
+          f"pass; the duration from the kernel-trace run).\n")
+    names = sorted({c for p in ctr for c in ctr[p]})
+    print("| counter | " + " | ".join(PROJS) + " |\n|---|" + "---:|" * len(PROJS))
+    print("| duration us | " + " | ".join(f"{avg(dur[p]) / 1e3:.1f}" for p in PROJS) + " |")
+    for c in names:
+        print(f"| {c} | " + " | ".join(f"{avg(ctr[p][c]):.4g}" for p in PROJS) + " |")
+    print("\nDerived (per dispatch):\n\n| metric | " + " | ".join(PROJS) + " |\n|---|" + "---:|" * len(PROJS))
+    def row(label, f):
+        vals = []
+        for p in PROJS:
+            try:
+                vals.append(f(p))
+            except (KeyError, ZeroDivisionError, TypeError):
+                vals.append("n/a")
+        print(f"| {label} | " + " | ".join(v if isinstance(v, str) else f"{v:.4g}" for v in vals) + " |")
+    c = lambda p, n: avg(ctr[p][n])  # noqa: E731
+    us = lambda p: avg(dur[p]) / 1e3  # noqa: E731
+    row("TOPS (2MNK / duration)", lambda p: 2 * M * synth.QWQ_SHAPES[p][1] * synth.QWQ_SHAPES[p][0] / us(p) / 1e6)
+    row("TOPS from 32 x SQ_INSTS_VALU_MFMA_MOPS_I8 x 512", lambda p: 32 * c(p, "SQ_INSTS_VALU_MFMA_MOPS_I8") * 512 / us(p) / 1e6)
+    row("VALU instructions per MFMA (SQ_INSTS_VALU - SQ_INSTS_MFMA) / SQ_INSTS_MFMA",
+        lambda p: (c(p, "SQ_INSTS_VALU") - c(p, "SQ_INSTS_MFMA")) / c(p, "SQ_INSTS_MFMA"))
+    row("LDS instructions per MFMA", lambda p: c(p, "SQ_INSTS_LDS") / c(p, "SQ_INSTS_MFMA"))
+    # the counter table holds per-dispatch values as rocprofv3 reduces them:
+    # SQ_* counters per shader engine (32 on MI355X: the instruction totals
+    # are these times 32, checked against 2*M*N*K below), GRBM_GUI_ACTIVE in
+    # GPU cycles
+    row("clock GHz (GRBM_GUI_ACTIVE / duration)", lambda p: c(p, "GRBM_GUI_ACTIVE") / us(p) / 1e3)
+    row("MFMA busy % (32 x SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs))",
+        lambda p: 100 * 32 * c(p, "SQ_VALU_MFMA_BUSY_CYCLES") / (c(p, "GRBM_GUI_ACTIVE") * 1024))
+    row("VALU-MFMA co-execution % of MFMA busy", lambda p: 100 * c(p, "SQ_VALU_MFMA_COEXEC_CYCLES") /
+        c(p, "SQ_VALU_MFMA_BUSY_CYCLES"))
+    if "FETCH_SIZE" in cal and "WRITE_SIZE" in cal:
+        ff, fw = 256 * 1024 / cal["FETCH_SIZE"], 256 * 1024 / cal["WRITE_SIZE"]
+        row("HBM MB (FETCH_SIZE + WRITE_SIZE, scaled by the 256 MiB copy)",
+            lambda p: (c(p, "FETCH_SIZE") * ff + c(p, "WRITE_SIZE") * fw) * 1024 / 1e6)
+        row("algorithmic MB", lambda p: gemm_bytes(M, synth.QWQ_SHAPES[p][1], synth.QWQ_SHAPES[p][0]) / 1e6)
+        print(f"\nCalibration: the 256 MiB copy reads FETCH_SIZE {cal['FETCH_SIZE']:.0f} KiB (factor {ff:.4f}) and "
+              f"WRITE_SIZE {cal['WRITE_SIZE']:.0f} KiB (factor {fw:.4f}).")
 
 
 def cpu_baseline(pkg, dev, seconds):

@@ -56,6 +56,7 @@ struct PrefillParams {
     int tpg;           // GMODE 3: K steps per group stride
     int tiles_m, tiles_n, band;
     uint32_t a_bytes, w_bytes, s_bytes;
+    bool vec_out;      // y 16-byte aligned with ldy % 8 == 0: 16-byte output stores
 };
 
 // K is walked in the padded group layout (kgeom.h): group g starts at g*gs,
@@ -103,6 +104,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     const auto ra_rsrc = make_rsrc(p.A, p.a_bytes);
     const auto rw_rsrc = make_rsrc(p.W, p.w_bytes);
     const auto rs_rsrc = make_rsrc(p.S, p.s_bytes);
+
+    // Token scales of the tile's rows: requested now, parked in LDS for the
+    // epilogue (a load issued there would add a memory round trip per row).
+    __shared__ uint32_t tsl[kBM];
+    uint32_t ts_bits = 0;
+    if (tid < kBM && m0 + tid < p.M) ts_bits = p.a_scale[m0 + tid];
 
     // ---- weights: byte offsets of this lane's two 16-byte chunks per step,
     // for the wave's 32-column blocks j = 0, 1 (column blocks past N read 0).
@@ -207,6 +214,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     load_s(0, sc);
 #pragma unroll
     for (int i = 0; i < kNA; ++i) *reinterpret_cast<uint4*>(&la[0][aoff[i]]) = ra[0][i];
+    if (tid < kBM) tsl[tid] = ts_bits;   // the scale load returned before A(0) (loads return in order)
     __syncthreads();
 
     const int8_t* abase = &la[0][0] + (wm * 64 + c32) * kLS + hh * 16;
@@ -328,25 +336,52 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     for (int u = 0; u < DW - 1; ++u)
         if (kt + u < p.KT) one(kt + u, u);
 
+    // ---- epilogue: the tile's bf16 outputs go through LDS (the A buffers are
+    // free once every wave passed the barrier below) and leave as 16-byte
+    // row stores.  Output tile: kBM rows x OC columns (OC = kBN, or kBN / 2
+    // SwiGLU outputs), row stride OS elements.
+    constexpr int OC = SWIGLU ? kBN / 2 : kBN;
+    constexpr int OS = OC + 8;
+    static_assert(kBM * OS * 2 <= 2 * kBM * kLS, "output tile fits the A buffers");
+    __syncthreads();
+    uint16_t* ot = reinterpret_cast<uint16_t*>(&la[0][0]);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int row = m0 + wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
-            if (row >= p.M) continue;
-            const float ts = bf16_bits_to_f32(p.a_scale[row]) * 0.0625f;
+            const int r = wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);   // row in the tile
+            const float ts = bf16_bits_to_f32(tsl[r]) * 0.0625f;
             if constexpr (SWIGLU) {
-                const int col = colj[0];
-                if (col < p.half_n)
-                    p.Y[static_cast<int64_t>(row) * p.ldy + col] =
-                        static_cast<uint16_t>(swiglu_bf16_bits(acc[rb][0][i] * ts, acc[rb][1][i] * ts));
+                ot[r * OS + wn * 32 + c32] =
+                    static_cast<uint16_t>(swiglu_bf16_bits(acc[rb][0][i] * ts, acc[rb][1][i] * ts));
             } else {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int col = colj[j];
-                    if (col < p.N) p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][j][i] * ts));
-                }
+                for (int j = 0; j < 2; ++j)
+                    ot[r * OS + wn * 64 + j * 32 + c32] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][j][i] * ts));
             }
+        }
+    }
+    __syncthreads();
+    // 8 columns per thread and step; rows past M are skipped, a chunk past the
+    // last column (or a row that cannot take 16-byte stores) is stored element
+    // by element
+    const int ncols = SWIGLU ? p.half_n : p.N;
+    constexpr int CPR = OC / 8;   // chunks per row
+#pragma unroll
+    for (int k = 0; k < kBM * CPR / kThreads; ++k) {
+        const int c = tid + k * kThreads;
+        const int r = c / CPR, c8 = (c % CPR) * 8;
+        const int row = m0 + r, col = n0 + c8;
+        if (row >= p.M || col >= ncols) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(&ot[r * OS + c8]);
+        uint16_t* y = p.Y + static_cast<int64_t>(row) * p.ldy + col;
+        if (p.vec_out && col + 8 <= ncols) {
+            *reinterpret_cast<uint4*>(y) = v;
+        } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (col + q < ncols) y[q] = static_cast<uint16_t>(w[q >> 1] >> (16 * (q & 1)));
         }
     }
 }
@@ -400,6 +435,7 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + p.kpad);
     p.w_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::k_tiles(a.K, a.group) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
+    p.vec_out = (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (a.ldy % 8 == 0);
     if (a.swiglu) return a.scale_bf16 ? launch<true, false, true>(p, stream) : launch<false, false, true>(p, stream);
     const bool dump = a.partials != nullptr;
     if (a.scale_bf16) return dump ? launch<true, true, false>(p, stream) : launch<true, false, false>(p, stream);

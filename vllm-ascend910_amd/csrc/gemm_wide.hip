@@ -489,23 +489,26 @@ hipError_t launch_wide_v(const GemmArgs& a, WideParams p, hipStream_t stream) {
     } else if (a.partials) e = launch_gm<kMT, kCPW, kD, kRA, true, false>(p, c, a.scale_bf16, stream);
     else e = launch_gm<kMT, kCPW, kD, kRA, false, false>(p, c, a.scale_bf16, stream);
     if (e != hipSuccess || p.splits == 1) return e;
-    const int64_t n = static_cast<int64_t>(p.M) * (p.ldr / 4);
-    const dim3 rg(static_cast<unsigned>((n + 255) / 256));
-    if (p.NG == 1) {
-        if (a.scale_bf16)
-            wide_reduce_kernel<true, true><<<rg, 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N,
-                                                                    p.splits, p.S, p.P);
-        else
-            wide_reduce_kernel<true, false><<<rg, 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N,
-                                                                     p.splits, p.S, p.P);
-    } else {
-        wide_reduce_kernel<false, false><<<rg, 256, 0, stream>>>(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N,
-                                                                  p.splits, nullptr, nullptr);
-    }
-    return hipGetLastError();
+    return launch_split_reduce(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N, p.splits, p.NG == 1, a.scale_bf16, p.S,
+                               p.P, stream);
 }
 
 }  // namespace
+
+hipError_t launch_split_reduce(const float* R, int64_t ldr, const uint16_t* a_scale, uint16_t* Y, int64_t ldy, int M,
+                               int N, int splits, bool one, bool sbf16, const uint16_t* S, int32_t* P,
+                               hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(M) * (ldr / 4);
+    const dim3 rg(static_cast<unsigned>((n + 255) / 256));
+    if (one) {
+        if (sbf16) wide_reduce_kernel<true, true><<<rg, 256, 0, stream>>>(R, ldr, a_scale, Y, ldy, M, N, splits, S, P);
+        else wide_reduce_kernel<true, false><<<rg, 256, 0, stream>>>(R, ldr, a_scale, Y, ldy, M, N, splits, S, P);
+    } else {
+        wide_reduce_kernel<false, false><<<rg, 256, 0, stream>>>(R, ldr, a_scale, Y, ldy, M, N, splits, nullptr,
+                                                                  nullptr);
+    }
+    return hipGetLastError();
+}
 
 // The layouts launch_gemm_wide builds: (row tiles, column blocks per wave,
 // weight ring, activation ring), measured best for their row counts on

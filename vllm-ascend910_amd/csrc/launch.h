@@ -81,9 +81,17 @@ bool linear_fusable(const GemmArgs& a, const uint16_t* x, int64_t ldx);
 hipError_t launch_linear_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t lda,
                                uint16_t* a_scale, hipStream_t stream);
 
+// Adds `splits` fp32 K-split sums R [splits, M, ldr] in split order, applies
+// the token scale and rounds to bf16 (one: int32 sums of a single group, folded
+// with the column scales S, optional partial dump P).
+hipError_t launch_split_reduce(const float* R, int64_t ldr, const uint16_t* a_scale, uint16_t* Y, int64_t ldy, int M,
+                               int N, int splits, bool one, bool sbf16, const uint16_t* S, int32_t* P,
+                               hipStream_t stream);
+
 // Prefill path (M > kDecodeMaxM): MFMA bound, LDS-tiled.
 int64_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
+
 
 // Mid-group compat path (the reference's midgroup_quant_a / midgroup_w4a8_gemm).
 hipError_t launch_quant_midgroup(const uint16_t* x, int64_t ldx, uint8_t* a_hi, uint8_t* a_lo,
