@@ -790,6 +790,8 @@ SWIGLU_CASES = [
     (24, 1024, 16384, 128, "f16"),    # narrow N, long K: no SwiGLU pairs in the K-split layout
     (1, 512, 1024, 128, "f16"),
     (4, 1024, 2048, 64, "bf16"),
+    (5, 16384, 512, 128, "bf16"),     # wide N up to 8 rows: staged activations, one wave per workgroup
+    (2, 16384, 1024, 64, "f16"),      # the same, two waves, group stride 64
     (33, 256, 1024, 256, "bf16"),
     (64, 512, 5120, 512, "bf16"),
     (3, 128, 1057, 1024, "bf16"),    # ragged K

@@ -51,6 +51,7 @@ struct DecodeConfig {
     int MT = 0;       // 16-row tiles per workgroup; 0 = all rows in one workgroup
     int WIDE = 0;     // a WideLayout: the LDS-shared-activation kernel (gemm_wide.hip); D/CPW/KW/MT unused
     int SPLITS = 1;   // WIDE: workgroups along K (fp32 sums in the workspace, reduced by a second kernel)
+    int STAGE = 0;    // 1: staged activations and scales (M <= 8, MT = 1, D = 4, CPW 1 or 2)
 };
 DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream);
