@@ -769,6 +769,15 @@ def prefill_pmc_summary(dbs):
     avg = lambda v: sum(v) / len(v) if v else float("nan")  # noqa: E731
     print(f"gemm_prefill_kernel at M={M}, group 128: per-dispatch counter averages (each counter from its own "
           f"pass; the duration from the kernel-trace run).\n")
+    print("Commands (run from /tmp with TMPDIR=/tmp; REPO is the repository root; one database per run):\n")
+    for i, db in enumerate(pmc_dbs):
+        names_db = [r[0] for r in sqlite3.connect(db).execute(
+            "select distinct counter_name from pmc_events order by counter_name")]
+        print(f"    rocprofv3 --pmc {' '.join(names_db)} -d /tmp/pf -o p{i + 1} -- "
+              f"python3 REPO/bench.py --prefill-probe {M}")
+    print(f"    rocprofv3 --kernel-trace -d /tmp/pf -o kt -- python3 REPO/bench.py --prefill-probe {M}")
+    print("    python3 REPO/bench.py --prefill-pmc-summary " +
+          " ".join(f"p{i + 1}_results.db" for i in range(len(pmc_dbs))) + " kt_results.db\n")
     names = sorted({c for p in ctr for c in ctr[p]})
     print("| counter | " + " | ".join(PROJS) + " |\n|---|" + "---:|" * len(PROJS))
     print("| duration us | " + " | ".join(f"{avg(dur[p]) / 1e3:.1f}" for p in PROJS) + " |")

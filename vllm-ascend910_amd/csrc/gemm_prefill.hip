@@ -8,10 +8,11 @@
 // BM x BN = 128 x 128 output tile; wave (wm, wn) owns rows wm*64..+64 and
 // columns wn*64..+64 as 2 x 2 blocks of v_mfma_i32_32x32x32_i8.  The K loop
 // walks 128-K steps (one repacked weight tile row):
-//   * activations: the workgroup stages A[128 rows][128 K] int8 in LDS,
-//     double-buffered (the next step's rows are loaded into registers two
-//     steps ahead and written to the other buffer at the end of a step), so
-//     there is one barrier per step;
+//   * activations: each step's A[128 rows][128 K] int8 goes from memory
+//     straight into one of four LDS buffers (16-byte buffer loads to LDS,
+//     three steps ahead, no registers on the way), in a swizzled layout
+//     that keeps the MFMA operand reads free of bank conflicts; one barrier per
+//     step, after a wait that leaves the two newest steps' loads in flight;
 //   * weights: every wave loads its own 64 columns straight from the repacked
 //     tiles into registers, DW steps ahead.  For a 32x32x32 B operand lane
 //     (column c, half hh) and slab s the natural K order k = 32s + 16hh + [0,16)
@@ -21,9 +22,13 @@
 // All global reads are raw buffer loads (SGPR descriptor + 32-bit offset):
 // rows past M and column blocks past N read as zero, and per-lane addresses
 // cost one VGPR.  The per-group fold (acc += float(16*P) * w_scale, a convert
-// and an FMA per output element and group) is VALU work of the same duration
-// as the MFMA work at group 128, so this kernel is bound by VALU issue and
-// MFMA/VALU overlap rather than by the matrix cores.
+// and an FMA per output element and group: 8 VALU instructions per MFMA at
+// group 128, 3 more unpack the weights) takes more VALU cycles (4 per wave64
+// instruction) than the MFMAs take matrix-core cycles (32 each), so this
+// kernel is bound by VALU issue and MFMA/VALU overlap rather than by the
+// matrix cores.  At group 128 each row block's fold is interleaved with the
+// other row block's MFMAs (one MFMA, eight fold instructions), so one wave
+// keeps both pipes busy.
 #include "common.h"
 #include "kgeom.h"
 #include "launch.h"
@@ -36,8 +41,30 @@ constexpr int kWN = kWaves / 2;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 128;
 constexpr int kBN = 64 * kWN;
-constexpr int kNA = kBM * 8 / kThreads;   // 16-byte A units per thread per step
-constexpr int kLS = 128 + 16;  // LDS row stride in bytes (+16 against bank conflicts)
+constexpr int kNA = kBM * 8 / kThreads;   // 16-byte A chunks per lane per step
+constexpr int kABuf = kBM * 128;           // one step's A tile in LDS (unpadded 128-byte rows)
+constexpr int kNB = 4;                     // A buffers: step kt reads kt % 4 while kt + 1..3 arrive
+// The epilogue stages the bf16 output tile in the first two A buffers (64 rows
+// each, rows of kOS elements), which are sized for it.
+constexpr int kOS = 64 * 2 + 8;
+constexpr int kABuf01 = kABuf > 64 * kOS * 2 ? kABuf : 64 * kOS * 2;
+
+// A rows sit in LDS unpadded, the 16-byte chunk q of tile row r at physical
+// chunk q ^ a_swz(r), a_swz(r) = (r / 2) % 8.  Measured on MI355X for the
+// MFMA operand reads (lane l reads row l % 32 at logical chunk 2 s + l / 32,
+// ds_read_b128): 1.00 against 1.12 for rows padded to 144 bytes, 1.8 for the
+// XORs r % 8 and (r + r / 8) % 8, and 7.0 unswizzled.
+__host__ __device__ constexpr int a_swz(int r) { return (r >> 1) & 7; }
+
+// Wait until at most N vector memory operations of this wave are outstanding
+// and its LDS operations are done, then the workgroup barrier.  One asm
+// statement with a memory clobber: no memory operation moves across it, and
+// unlike __syncthreads it does not wait for every outstanding load.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    static_assert(N >= 0 && N <= 63, "vmcnt holds 0..63");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 struct PrefillParams {
     const int8_t* A;
@@ -72,7 +99,15 @@ struct PrefillParams {
 template <int GMODE, int DW, bool SBF16, bool DUMP, bool SWIGLU>
 __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const PrefillParams p) {
     static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
-    __shared__ __attribute__((aligned(16))) int8_t la[2][kBM * kLS];
+    // Four separate A buffers (separate objects, so the compiler's tracking of
+    // loads into LDS keeps reads of one buffer from waiting on loads into
+    // another).
+    __shared__ __attribute__((aligned(16))) int8_t la0[kABuf01];
+    __shared__ __attribute__((aligned(16))) int8_t la1[kABuf01];
+    __shared__ __attribute__((aligned(16))) int8_t la2[kABuf];
+    __shared__ __attribute__((aligned(16))) int8_t la3[kABuf];
+    // buffer b (a compile-time index after unrolling)
+    auto abuf = [&](int b) -> int8_t* { return b == 0 ? la0 : (b == 1 ? la1 : (b == 2 ? la2 : la3)); };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -126,23 +161,27 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         soff[j] = (static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.NG) * 16u + (col & 15)) * 2u;
     }
 
-    // ---- activation staging: 128 rows x 8 units of 16 B = 1024 units, 2 per thread
+    // ---- activations: each step's A[128 rows][128 K] goes straight from
+    // memory into an LDS buffer (16-byte buffer loads to LDS: lane l of a
+    // load writes bytes 16 l..16 l + 15 of a contiguous 1 KB).  Load i of
+    // wave w fills tile rows 32 w + 8 i..+8; lane l takes row + l / 8,
+    // physical chunk l % 8, i.e. logical chunk (l % 8) ^ a_swz(row).
     uint32_t aoffg[kNA];
-    int aoff[kNA];
 #pragma unroll
     for (int i = 0; i < kNA; ++i) {
-        const int c = i * kThreads + tid;
-        const int r = c >> 3;
-        const int cu = (c & 7) * 16;
+        const int r = 8 * (kNA * wave + i) + (lane >> 3);
+        const int q = (lane & 7) ^ a_swz(r);
         // rows >= M lie past the buffer and read zero; they are never stored
-        aoffg[i] = static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(p.lda) + cu;
-        aoff[i] = r * kLS + cu;
+        aoffg[i] = static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(p.lda) + static_cast<uint32_t>(q) * 16u;
     }
-    auto load_a = [&](int kt, uint4 (&ra)[kNA]) {
+    auto load_a = [&](int kt, int b) {
         // the padding half of a last step reads past kpad: zero weights there
         const uint32_t k = static_cast<uint32_t>(min(kt, p.KT - 1)) * 128u;
+        int8_t* const dst = abuf(b) + kNA * 1024 * wave;
 #pragma unroll
-        for (int i = 0; i < kNA; ++i) ra[i] = buf_load16(ra_rsrc, aoffg[i] + k);
+        for (int i = 0; i < kNA; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_rsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * i),
+                                                     16, aoffg[i] + k, 0, 0, 0);
     };
 
     uint4 wr[DW][2][2];
@@ -157,6 +196,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     // Scales of the groups that may end in step kt: at its 64-K halves h=0,1
     // (group 128 only ends on the step's last slab, so one scale suffices).
     constexpr bool ONE_END = GMODE == 1 || GMODE == 3;   // groups end only on a step's last slab
+    // Group stride 128: each row block's fold is staggered against the other
+    // row block's MFMAs (row block 1 folds during the next step).
+    constexpr bool STAG = GMODE == 1;
     constexpr int NSC = ONE_END ? 1 : 2;
     auto load_s = [&](int kt, uint32_t (&sv)[2][NSC]) {
         const int ktc = min(kt, p.KT - 1);
@@ -204,28 +246,39 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         }
     };
 
-    // ---- prologue: A(0) into LDS, A(1) in registers, W(0..DW-1) in flight
-    uint4 ra[2][kNA];
-    load_a(0, ra[0]);
-    load_a(1, ra[1]);
+    // ---- prologue: A(0..2) to their LDS buffers, then W(0..DW-1) and the
+    // first scales (the empty asm statements keep this issue order, which the
+    // wait below counts on)
+    load_a(0, 0);
+    load_a(1, 1);
+    load_a(2, 2);
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int s = 0; s < DW; ++s) load_w(s, s);
     uint32_t sc[2][NSC];
     load_s(0, sc);
-#pragma unroll
-    for (int i = 0; i < kNA; ++i) *reinterpret_cast<uint4*>(&la[0][aoff[i]]) = ra[0][i];
-    if (tid < kBM) tsl[tid] = ts_bits;   // the scale load returned before A(0) (loads return in order)
-    __syncthreads();
+    asm volatile("" ::: "memory");
+    // STAG: the scale bits of the previous step's groups (zero before step 0,
+    // whose fold of row block 1 adds zero partials times zero)
+    uint32_t scp[2] = {0u, 0u};
+    if (tid < kBM) tsl[tid] = ts_bits;
+    // A(0) has landed once at most the 2 * kNA + DW * 4 + 2 * NSC newer
+    // loads are outstanding; then every wave's part of it is in LDS
+    wait_vm_barrier<2 * kNA + DW * 4 + 2 * NSC>();
 
-    const int8_t* abase = &la[0][0] + (wm * 64 + c32) * kLS + hh * 16;
+    // This lane's A operand offsets for slab s of row block 0 (row block 1 is
+    // 32 rows = 4096 bytes further): row wm * 64 + c32, logical chunk 2 s + hh.
+    uint32_t aread[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        aread[s] = static_cast<uint32_t>((wm * 64 + c32) * 128 + (((2 * s + hh) ^ a_swz(c32)) * 16));
 
     // Per step: issue the loads for later steps, unpack this step's weights
     // into all four slabs' B operands (so the ring slot is dead and its refill
     // needs no register copies), then the MFMAs.
     auto step = [&](int kt, int u, int buf) __attribute__((always_inline)) {
-        // ra[(u+1)&1] holds A(kt+1) (written to LDS at the end of this step);
-        // refill ra[u&1] with A(kt+2).
-        load_a(kt + 2, ra[u & 1]);
+        // A(kt + 3) into the buffer step kt - 1 read
+        load_a(kt + 3, (buf + 3) % kNB);
         uint32_t scn[2][NSC];
         load_s(kt + 1, scn);
         // A operands from LDS two slabs at a time: slabs 0-1 now (their
@@ -235,10 +288,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         // the LDS latency eight times per step.  Group stride 64 (a fold in
         // mid-step) and the partial dump need those registers and read per
         // slab.
-        constexpr bool PAIRS = GMODE != 0 && !DUMP;
-        const int8_t* ab = abase + buf * (kBM * kLS);
-        auto lds_a = [&](int rb, int s) { return *reinterpret_cast<const v4i*>(ab + rb * 32 * kLS + s * 32); };
+        constexpr bool PAIRS = GMODE != 0 && !DUMP && !STAG;
+        const int8_t* ab = abuf(buf);
+        auto lds_a = [&](int rb, int s) { return *reinterpret_cast<const v4i*>(ab + aread[s] + rb * 4096); };
         v4i avs[4][2];
+        if constexpr (STAG) {
+            // row block 0's A operands now (their latency hides behind the
+            // unpack), row block 1's at the start of row block 0's MFMAs
+#pragma unroll
+            for (int s = 0; s < 4; ++s) avs[s][0] = lds_a(0, s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         if constexpr (PAIRS) {
 #pragma unroll
             for (int s = 0; s < 2; ++s)
@@ -257,6 +317,45 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
                 bvs[s][j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
             }
         load_w(u, kt + DW);
+
+        if constexpr (STAG) {
+            // Group stride 128 (a group per step): row block 0's eight MFMAs,
+            // with the previous step's row block 1 folded in between them, then
+            // row block 1's, with this step's row block 0 folded in between.
+            // Each half step pairs 8 MFMAs (256 cycles of the matrix core)
+            // with 64 fold instructions (256 VALU cycles) of independent
+            // registers, so one wave keeps both pipes busy; the group's first
+            // slab takes a zero accumulator operand.
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                if (rb == 0) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) avs[s][1] = lds_a(1, s);
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) P[rb][j] = mfma32(avs[s][rb], bvs[s][j], s == 0 ? zero16 : P[rb][j]);
+                if (rb == 0) {
+                    fold_rb(1, kt - 1, scp);
+                } else {
+                    const uint32_t ws2[2] = {sc[0][0], sc[1][0]};
+                    fold_rb(0, kt, ws2);
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);   // eight VALU
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                scp[j] = sc[j][0];
+                sc[j][0] = scn[j][0];
+            }
+            return;
+        }
 
         // Slab-major: the four blocks' MFMA chains interleave, so no MFMA waits
         // on its predecessor's result.  A group ends after slab 1 or 3 (fixed
@@ -313,38 +412,46 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
             for (int h = 0; h < NSC; ++h) sc[j][h] = scn[j][h];
     };
 
-    // DW is even, so the A register buffer of step kt is ra[u & 1] with a
-    // compile-time index.
-    static_assert(DW % 2 == 0, "DW must be even");
+    // Steps are unrolled by kNB (a multiple of DW), so the A buffer and the
+    // weight ring slot of each step are compile-time indices.  A step issues
+    // exactly kNA + 4 + 2 * NSC vector memory operations (the partial dump
+    // only adds stores, which make the wait below stricter); A(kt + 1), loaded
+    // during step kt - 2, has landed once at most the two newest steps'
+    // operations are outstanding, and after the barrier every wave's part of
+    // it is in LDS.  The barrier also ends every read of the buffer step kt + 1
+    // refills.
+    static_assert(kNB % DW == 0, "an unrolled group covers whole weight rings");
     auto one = [&](int kt, int u) __attribute__((always_inline)) {
-        const int buf = kt & 1;
-        step(kt, u, buf);
-#pragma unroll
-        for (int i = 0; i < kNA; ++i) *reinterpret_cast<uint4*>(&la[buf ^ 1][aoff[i]]) = ra[(u + 1) & 1][i];
-        __syncthreads();
+        step(kt, u % DW, u % kNB);
+        wait_vm_barrier<2 * (kNA + 4 + 2 * NSC)>();
     };
-    // Whole groups of DW steps, then the remaining steps after the loop: an
+    // Whole groups of kNB steps, then the remaining steps after the loop: an
     // early exit inside the unrolled group would give the loop header a path
     // whose newest loads are this group's weight refills, and the wait counts
     // at the top of every iteration would have to cover it.
     int kt = 0;
-    for (; kt + DW <= p.KT; kt += DW) {
+    for (; kt + kNB <= p.KT; kt += kNB) {
 #pragma unroll
-        for (int u = 0; u < DW; ++u) one(kt + u, u);
+        for (int u = 0; u < kNB; ++u) one(kt + u, u);
     }
 #pragma unroll
-    for (int u = 0; u < DW - 1; ++u)
+    for (int u = 0; u < kNB - 1; ++u)
         if (kt + u < p.KT) one(kt + u, u);
+    if constexpr (STAG) fold_rb(1, p.KT - 1, scp);   // the last step's row block 1
 
-    // ---- epilogue: the tile's bf16 outputs go through LDS (the A buffers are
-    // free once every wave passed the barrier below) and leave as 16-byte
+    // ---- epilogue: the tile's bf16 outputs go through LDS (the first two A
+    // buffers, rows 0-63 and 64-127, are free once every load into LDS has
+    // landed and every wave passed the barrier below) and leave as 16-byte
     // row stores.  Output tile: kBM rows x OC columns (OC = kBN, or kBN / 2
     // SwiGLU outputs), row stride OS elements.
     constexpr int OC = SWIGLU ? kBN / 2 : kBN;
     constexpr int OS = OC + 8;
-    static_assert(kBM * OS * 2 <= 2 * kBM * kLS, "output tile fits the A buffers");
-    __syncthreads();
-    uint16_t* ot = reinterpret_cast<uint16_t*>(&la[0][0]);
+    static_assert(64 * OS * 2 <= kABuf01, "64 output rows fit an A buffer");
+    wait_vm_barrier<0>();
+    // rows 0-63 (waves wm = 0) in la0, rows 64-127 in la1
+    auto orow = [&](int r) -> uint16_t* {
+        return reinterpret_cast<uint16_t*>(r < 64 ? la0 : la1) + (r & 63) * OS;
+    };
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
@@ -352,12 +459,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
             const int r = wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);   // row in the tile
             const float ts = bf16_bits_to_f32(tsl[r]) * 0.0625f;
             if constexpr (SWIGLU) {
-                ot[r * OS + wn * 32 + c32] =
+                orow(r)[wn * 32 + c32] =
                     static_cast<uint16_t>(swiglu_bf16_bits(acc[rb][0][i] * ts, acc[rb][1][i] * ts));
             } else {
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    ot[r * OS + wn * 64 + j * 32 + c32] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][j][i] * ts));
+                    orow(r)[wn * 64 + j * 32 + c32] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][j][i] * ts));
             }
         }
     }
@@ -373,7 +480,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
         const int r = c / CPR, c8 = (c % CPR) * 8;
         const int row = m0 + r, col = n0 + c8;
         if (row >= p.M || col >= ncols) continue;
-        const uint4 v = *reinterpret_cast<const uint4*>(&ot[r * OS + c8]);
+        const uint4 v = *reinterpret_cast<const uint4*>(orow(r) + c8);
         uint16_t* y = p.Y + static_cast<int64_t>(row) * p.ldy + col;
         if (p.vec_out && col + 8 <= ncols) {
             *reinterpret_cast<uint4*>(y) = v;
