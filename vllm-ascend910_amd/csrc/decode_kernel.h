@@ -104,7 +104,8 @@ __host__ __device__ constexpr int st_wave_bytes(int m, int cpw, int gm, int d) {
 // each wave loads the bf16 rows of its own K range, the waves' absmax meet in
 // LDS, and each wave quantises its range into an LDS copy of A (the per-token
 // arithmetic of quant_act.hip) that its MFMAs then read; the row loads are
-// issued ahead of the weight ring, which streams meanwhile.
+// issued ahead of the weight ring, which streams meanwhile.  Its group scales
+// are staged per pass as below.
 // SA > 0: staged activations and scales (M <= 8, MT = 1, D = 4).  A 16-row
 // tile of a few real rows wastes most of each per-tile activation load (the
 // 16-byte lane loads of rows past M still occupy the load pipeline), and the
@@ -231,15 +232,19 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     uint4 ab[DA][MT][2];
     uint32_t sb[D][CPW][NS];
 
-    // ST: this wave's area (bytes from red): a 16-byte dump slot, then pass
-    // buffers at +16 and +16 + st_buf, each st_ab bytes of rows (slot s, row
-    // r at (s * M + r) * kStRow) and the scales of NGP groups per column block
-    // (block c, group g0 + i at st_ab + (c * NGP + i) * 32).
+    // STS: group scales staged per pass (with the activations for ST; the
+    // fused quant, whose rows are in LDS already, stages the scales alone).
+    // This wave's staging area (bytes from red): a 16-byte dump slot, then
+    // pass buffers at +16 and +16 + st_buf, each st_ab bytes of rows (slot s,
+    // row r at (s * M + r) * kStRow; ST only) and the scales of NGP groups per
+    // column block (block c, group g0 + i at st_ab + (c * NGP + i) * 32).
+    // ST areas start at wave * st_wave; QF areas follow the quant's regions.
+    constexpr bool STS = ST || (QF && !ONE);
     constexpr int NGP = st_pass_groups(GM, D);
     const int st_ab = ST ? D * p.M * kStRow : 0;
-    const int st_buf = st_ab + ((ST && !ONE) ? CPW * NGP * 32 : 0);
+    const int st_buf = st_ab + ((STS && !ONE) ? CPW * NGP * 32 : 0);
     const int st_wave = ST ? st_wave_bytes(p.M, CPW, GM, D) : R * C * 4;
-    const int lw = wave * st_wave;
+    const int lw = ST ? wave * st_wave : lq_s + 16 + wave * (16 + 2 * st_buf);
     constexpr int SAN = ST ? SA : 1;
     // Per staged chunk i (lane + 64 i: row r = chunk / 32, 16-byte piece q =
     // chunk % 32 of the pass's 512 bytes per row): its offset in the pass's
@@ -250,7 +255,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     uint32_t sgs = kOOB, sls = kOOB, arow = 0;
     const int sgi = (lane >> 1) % NGP;
     uint4 xs[SAN], xsc;
-    if constexpr (ST) {
+    if constexpr (STS) {
 #pragma unroll
         for (int i = 0; i < SA; ++i) {
             const int c = lane + 64 * i, r = c >> 5, q = c & 31;
@@ -273,9 +278,11 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     auto stage_issue = [&](int pi) {
         const int t0 = ta + pi * D;
         const bool live = t0 < tb;
-        const auto ra = make_rsrc_at(p.A, static_cast<uint32_t>(t0) * 128u, live ? p.a_bytes : 0u);
+        if constexpr (ST) {
+            const auto ra = make_rsrc_at(p.A, static_cast<uint32_t>(t0) * 128u, live ? p.a_bytes : 0u);
 #pragma unroll
-        for (int i = 0; i < SAN; ++i) xs[i] = buf_load16(ra, sg[i]);
+            for (int i = 0; i < SAN; ++i) xs[i] = buf_load16(ra, sg[i]);
+        }
         if constexpr (!ONE) {
             const int g0 = gfirst(t0);
             const auto rs = make_rsrc_at(p.S, static_cast<uint32_t>(g0) * 32u, live ? p.s_bytes : 0u);
@@ -285,8 +292,10 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     // Write the fetched pass pi into its buffer.
     auto stage_commit = [&](int pi) {
         char* const buf = lds + lw + 16 + (pi & 1) * st_buf;
+        if constexpr (ST) {
 #pragma unroll
-        for (int i = 0; i < SAN; ++i) *reinterpret_cast<uint4*>(sl[i] != kOOB ? buf + sl[i] : lds + lw) = xs[i];
+            for (int i = 0; i < SAN; ++i) *reinterpret_cast<uint4*>(sl[i] != kOOB ? buf + sl[i] : lds + lw) = xs[i];
+        }
         if constexpr (!ONE) *reinterpret_cast<uint4*>(sls != kOOB ? buf + sls : lds + lw) = xsc;
     };
     // Activations of slot si of pass pi into ring slot sa.
@@ -317,8 +326,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
         const auto rw = make_rsrc_at(p.W, static_cast<uint32_t>(t) * 1024u, t < tb ? p.w_bytes : 0u);
 #pragma unroll
         for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16_nt(rw, wo[c]);
-        // the one scale per column is loaded once, before the loop; ST stages them
-        if constexpr (ONE || ST) return;
+        // the one scale per column is loaded once, before the loop; STS stages them
+        if constexpr (ONE || STS) return;
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             const auto rs = make_rsrc_at(p.S, static_cast<uint32_t>(gend(min(t, p.KT - 1), j)) * 32u, p.s_bytes);
@@ -368,7 +377,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     // every pass.  Tiles of the last pass past tb hold zero weights: their
     // MFMAs add nothing and a fold there adds zero.
     auto pass = [&](int it, auto prefetch) {
-        if constexpr (ST && decltype(prefetch)::value) {
+        if constexpr (STS && decltype(prefetch)::value) {
             // the next pass's buffer (its activations are read during this one)
             stage_commit(it + 1);
             stage_issue(it + 2);
@@ -377,7 +386,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
         for (int s = 0; s < D; ++s) {
             const int t = ta + it * D + s;
             uint32_t sc[CPW][NS];
-            if constexpr (ST && !ONE) {
+            if constexpr (STS && !ONE) {
                 const char* const sbase = lds + lw + 16 + (it & 1) * st_buf + st_ab + colq * 2;
                 const int g0 = gfirst(ta + it * D);
 #pragma unroll
@@ -452,7 +461,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     }
     uint32_t ws1[CPW];   // ONE: the scale of each column block's columns of this lane
     if (busy) {
-        if constexpr (ST) stage_issue(0);
+        if constexpr (STS) stage_issue(0);
 #pragma unroll
         for (int s = 0; s < D; ++s) load_slot(s, ta + s);
     }
@@ -520,6 +529,10 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
 #pragma unroll
             for (int s = 0; s < D; ++s) load_a_st(s, 0, s);
         } else {
+            if constexpr (STS) {
+                stage_commit(0);
+                stage_issue(1);
+            }
 #pragma unroll
             for (int s = 0; s < DA; ++s) load_a(s, ta + s);
         }

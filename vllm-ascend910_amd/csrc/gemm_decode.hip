@@ -112,6 +112,11 @@ bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f)
     // and ~2 us on gate_up's 1728 column groups; at 2-4 rows the
     // per-workgroup quant costs more than the launch it saves.)
     if (a.M != 1 || a.swiglu || a.partials || !geom::is_unpadded(a.K, a.group)) return false;
+    // Long K (>= 128 tiles) takes the two kernels: each wave's quant prologue
+    // (its bf16 rows, then a workgroup-wide absmax) outlasts the launch it
+    // saves against the staged GEMM (down_proj: 19.2 us fused, 14.8 + 3.5 us
+    // for the pair on MI355X).
+    if (geom::k_tiles(a.K, a.group) >= 128) return false;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx % 8 != 0) return false;
     const DecodeConfig c = decode_config(a.M, a.N, a.K, a.group);
     if (c.D != 4 || c.CPW != 2 || c.MT != 0 || c.WIDE) return false;
@@ -127,7 +132,12 @@ bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f)
     f.p.qcpr = (tiles + 3) / 4;                                     // 16-byte chunks per row per lane
     if (f.p.qcpr > 8 / f.qm) return false;
     f.p.lrs = f.p.KT * 128 + 16;   // 16-byte skew: the rows' reads fall on different banks
-    f.lds = static_cast<size_t>(f.kw) * 16 * 32 * 4 + static_cast<size_t>(f.qm) * f.p.lrs + 64 + f.kw * 16 + 16;
+    // reduction rows, quantised rows, zero block, absmax, scale bits, then per
+    // wave the staged group scales (a dump slot and two pass buffers)
+    const int gm = group_mode(f.p.spg, f.p.NG);
+    const int sts = gm == 4 ? 0 : 16 + 2 * 2 * st_pass_groups(gm, 4) * 32;
+    f.lds = static_cast<size_t>(f.kw) * 16 * 32 * 4 + static_cast<size_t>(f.qm) * f.p.lrs + 64 + f.kw * 16 + 16 +
+            static_cast<size_t>(f.kw) * sts;
     if (f.lds > 64 * 1024) return false;
     f.p.X = x;
     f.p.ldx = ldx;
