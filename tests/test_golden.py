@@ -160,3 +160,45 @@ def test_gpu_golden_perchannel(pkg, dev):
     for got in (tensor_bf16_bits(y), tensor_bf16_bits(y2)):
         bar_and_equal(got, gv("pc_y"), y32, lambda r, c: ow.gemm_f64(gv("pc_aq")[r], gv("pc_as")[r], codes[c],
                                                                      ws32[c], K))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 2, 4, 8])
+def test_gpu_golden_row_prefixes(pkg, dev, rows):
+    """The first rows of the per-token and per-channel golden cases through the
+    GEMM and the linear (outputs are row-independent, so each prefix must match
+    the reference's rows): up to 8 rows run the staged decode variants, one row
+    the fused single-row linear."""
+    import torch
+    from conftest import tensor_bf16_bits
+    M, K, N, G = (int(v) for v in gv("pt_shape"))
+    print(f"golden per-token prefix rows={rows} K={K} N={N} G={G}", flush=True)
+    ws = torch.from_numpy(gv("pt_ws").view(np.int16)).view(torch.bfloat16).to(dev)
+    wt, st = torch.ops.npu.w4a8_repack(torch.from_numpy(gv("pt_wq")).to(dev), ws, K, G)
+    x = torch.from_numpy(gv("pt_x")[:rows].view(np.int16)).view(torch.bfloat16).to(dev)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, G)
+    y = torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, G)
+    yl = torch.ops.npu.w4a8_linear(x, wt, st, N, K, G)
+    y2, P = torch.ops.npu.w4a8_gemm_partials(a_q, a_s, wt, st, N, K, G)
+    torch.cuda.synchronize()
+    aq, as_ = gv("pt_aq")[:rows], gv("pt_as")[:rows]
+    assert np.array_equal(a_q.cpu().numpy(), aq) and np.array_equal(tensor_bf16_bits(a_s), as_)
+    codes = unpacked(gv("pt_wq"), K, G)
+    assert np.array_equal(P.cpu().numpy().astype(np.int64), ow.group_partials(aq, codes, G))
+    ws32 = ow.bf16_bits_to_f32(gv("pt_ws")).T.copy()
+    y32 = ow.gemm_fp32(aq, as_, codes, ws32, G)
+    for got in (tensor_bf16_bits(y), tensor_bf16_bits(yl), tensor_bf16_bits(y2)):
+        bar_and_equal(got, gv("pt_y")[:rows], y32, lambda r, c: ow.gemm_f64(aq[r], as_[r], codes[c], ws32[c], G))
+
+    Mc, Kc, Nc = (int(v) for v in gv("pc_shape"))
+    wsc = torch.from_numpy(gv("pc_ws").reshape(1, Nc).view(np.int16)).view(torch.bfloat16).to(dev)
+    wtc, stc = torch.ops.npu.w4a8_repack(torch.from_numpy(gv("pc_wq")).to(dev), wsc, Kc, Kc)
+    xc = torch.from_numpy(gv("pc_x")[:rows].view(np.int16)).view(torch.bfloat16).to(dev)
+    yc = torch.ops.npu.w4a8_linear(xc, wtc, stc, Nc, Kc, Kc)
+    torch.cuda.synchronize()
+    aqc, asc = gv("pc_aq")[:rows], gv("pc_as")[:rows]
+    codes_c = unpacked(gv("pc_wq"), Kc, Kc)
+    ws32c = ow.bf16_bits_to_f32(gv("pc_ws"))[:, None].astype(np.float32)
+    y32c = ow.gemm_fp32(aqc, asc, codes_c, ws32c, Kc)
+    bar_and_equal(tensor_bf16_bits(yc), gv("pc_y")[:rows], y32c,
+                  lambda r, c: ow.gemm_f64(aqc[r], asc[r], codes_c[c], ws32c[c], Kc))
