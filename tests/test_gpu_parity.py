@@ -51,6 +51,17 @@ def run_hip(dev, xb, w, w_scale, N, K, G, partials=True):
     return y, P, a_q, a_s
 
 
+def assert_production_equals_dump(pkg, dev, a_q, a_s, w, w_scale, y_dump, N, K, G):
+    """The plain GEMM (the production kernel variant, whose plan may differ from
+    the partial dump's, e.g. 64-row prefill tiles) returns the dump call's output
+    bit for bit."""
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(torch.from_numpy(ow.pack_grouped(w, G)).to(dev),
+                                                 w_scale.to(dev), K, G)
+    y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_dump.view(torch.int16)), "production output differs from the dump's"
+
+
 def check_output(y_bits: np.ndarray, y32: np.ndarray, tag: str, exact) -> None:
     """Output bars.
 
@@ -232,6 +243,7 @@ def test_gemm_partials_bit_exact_and_output(pkg, dev, M, N, K, G, sd):
     assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
     y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref)
     check_output(tensor_bf16_bits(y), y32, f"M{M} N{N} K{K} G{G}", exact_sym(q_ref, s_ref, w, ws32, G))
+    assert_production_equals_dump(pkg, dev, a_q, a_s, w, w_scale, y, N, K, G)
 
 
 # The reference's ragged-K cases (int4_cube_lab/host/ragged_layout_test.cpp:195-223:
@@ -280,6 +292,7 @@ def test_gemm_ragged_k(pkg, dev, M, N, K, G, sd):
     assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
     y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref)
     check_output(tensor_bf16_bits(y), y32, f"ragged M{M} N{N} K{K} G{G}", exact_sym(q_ref, s_ref, w, ws32, G))
+    assert_production_equals_dump(pkg, dev, a_q, a_s, w, w_scale, y, N, K, G)
 
 
 @pytest.mark.parametrize("K,G", [(1057, 1024), (100, 33), (1057, 96), (3456, 1024), (5000, 128), (35, 1024),

@@ -36,18 +36,21 @@
 namespace w4a8 {
 namespace {
 
-constexpr int kWaves = 4;   // 2 x kWN waves of 64 x 64
-constexpr int kWN = kWaves / 2;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = 128;
+// Tile BM x kBN: BM = 128 (2 x 2 waves of 64 x 64, two workgroups per CU) or
+// BM = 64 (1 x 2 waves, four workgroups per CU: twice as many tiles, for
+// prefills whose 128-row tiles would load the CUs unevenly; prefill_tile_rows).
+constexpr int kWN = 2;                     // waves across the tile's columns
 constexpr int kBN = 64 * kWN;
-constexpr int kNA = kBM * 8 / kThreads;   // 16-byte A chunks per lane per step
-constexpr int kABuf = kBM * 128;           // one step's A tile in LDS (unpadded 128-byte rows)
+constexpr int kNA = 4;                     // 16-byte A chunks per lane per step (BM * 8 / threads)
 constexpr int kNB = 4;                     // A buffers: step kt reads kt % 4 while kt + 1..3 arrive
-// The epilogue stages the bf16 output tile in the first two A buffers (64 rows
-// each, rows of kOS elements), which are sized for it.
-constexpr int kOS = 64 * 2 + 8;
-constexpr int kABuf01 = kABuf > 64 * kOS * 2 ? kABuf : 64 * kOS * 2;
+template <int BM> constexpr int threads_for() { return 64 * kWN * (BM / 64); }
+// The epilogue stages the bf16 output tile in the first two A buffers (BM / 2
+// rows each, rows of OS elements: padded by 8 at BM = 128, unpadded at 64 so
+// that four workgroups fit a CU's LDS).
+template <int BM, bool SWIGLU> constexpr int out_stride() { return (SWIGLU ? kBN / 2 : kBN) + (BM == 128 ? 8 : 0); }
+template <int BM, bool SWIGLU> constexpr int abuf01_bytes() {
+    return BM * 128 > BM / 2 * out_stride<BM, SWIGLU>() * 2 ? BM * 128 : BM / 2 * out_stride<BM, SWIGLU>() * 2;
+}
 
 // A rows sit in LDS unpadded, the 16-byte chunk q of tile row r at physical
 // chunk q ^ a_swz(r), a_swz(r) = (r / 2) % 8.  Measured on MI355X for the
@@ -84,6 +87,7 @@ struct PrefillParams {
     int tiles_m, tiles_n, band;
     uint32_t a_bytes, w_bytes, s_bytes;
     bool vec_out;      // y 16-byte aligned with ldy % 8 == 0: 16-byte output stores
+    int bm;            // tile rows: 128 or 64
 };
 
 // K is walked in the padded group layout (kgeom.h): group g starts at g*gs,
@@ -96,8 +100,13 @@ struct PrefillParams {
 // up columns, so each lane holds both operands of its outputs
 // silu(y[:, n]) * y[:, n + N/2] (a tile covers 64 outputs); every column
 // accumulates exactly as in the plain GEMM.
-template <int GMODE, int DW, bool SBF16, bool DUMP, bool SWIGLU>
-__global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const PrefillParams p) {
+template <int GMODE, int DW, bool SBF16, bool DUMP, bool SWIGLU, int BM>
+__global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(const PrefillParams p) {
+    constexpr int kThreads = threads_for<BM>();
+    constexpr int kBM = BM;
+    constexpr int kABuf = BM * 128;              // one step's A tile in LDS (unpadded 128-byte rows)
+    constexpr int kABuf01 = abuf01_bytes<BM, SWIGLU>();
+    static_assert(kNA == BM * 8 / kThreads, "four 16-byte A chunks per lane per step");
     static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
     // Four separate A buffers (separate objects, so the compiler's tracking of
     // loads into LDS keeps reads of one buffer from waiting on loads into
@@ -112,7 +121,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / kWN;  // 0..1
+    const int wm = wave / kWN;  // 0..BM / 64 - 1
     const int wn = wave % kWN;
     // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
     // L2.  Renumber them so that every XCD walks one contiguous run of tiles,
@@ -445,12 +454,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_prefill_kernel(const Prefill
     // row stores.  Output tile: kBM rows x OC columns (OC = kBN, or kBN / 2
     // SwiGLU outputs), row stride OS elements.
     constexpr int OC = SWIGLU ? kBN / 2 : kBN;
-    constexpr int OS = OC + 8;
-    static_assert(64 * OS * 2 <= kABuf01, "64 output rows fit an A buffer");
+    constexpr int OS = out_stride<BM, SWIGLU>();
+    constexpr int RPA = BM / 2;   // output rows per staging buffer
+    static_assert(RPA * OS * 2 <= kABuf01, "half the output rows fit an A buffer");
     wait_vm_barrier<0>();
-    // rows 0-63 (waves wm = 0) in la0, rows 64-127 in la1
+    // rows 0..RPA-1 in la0, the rest in la1
     auto orow = [&](int r) -> uint16_t* {
-        return reinterpret_cast<uint16_t*>(r < 64 ? la0 : la1) + (r & 63) * OS;
+        return reinterpret_cast<uint16_t*>(r < RPA ? la0 : la1) + (r % RPA) * OS;
     };
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
@@ -498,7 +508,13 @@ constexpr int kDW = 2;   // weight prefetch depth in K steps
 template <int GMODE, bool SBF16, bool DUMP, bool SWIGLU>
 hipError_t launch_g(const PrefillParams& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
-    gemm_prefill_kernel<GMODE, kDW, SBF16, DUMP, SWIGLU><<<grid, dim3(kThreads), 0, stream>>>(p);
+    // The partial dump keeps 128-row tiles (the compiler fails on the 64-row
+    // dump variants); each output element's arithmetic does not depend on the
+    // tile height, so its outputs equal the 64-row kernel's bit for bit.
+    if (p.bm == 64 && !DUMP)
+        gemm_prefill_kernel<GMODE, kDW, SBF16, false, SWIGLU, 64><<<grid, dim3(threads_for<64>()), 0, stream>>>(p);
+    else
+        gemm_prefill_kernel<GMODE, kDW, SBF16, DUMP, SWIGLU, 128><<<grid, dim3(threads_for<128>()), 0, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -514,7 +530,24 @@ hipError_t launch(const PrefillParams& p, hipStream_t stream) {
 
 int64_t prefill_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
 
+int prefill_tile_rows(int64_t M, int64_t N, bool swiglu) {
+    // 64-row tiles (twice as many, up to four workgroups per CU) where the
+    // 128-row ones would leave CUs idle or unevenly loaded: at most one for
+    // every second CU, or between one and two per CU.  Measured on MI355X
+    // (QwQ-32B shapes, 128 -> 64 rows): o_proj M=1024 49.2 -> 46.1 us,
+    // down_proj M=1024 222 -> 205 us, qkv/o/down M=128-256 3-6% faster; at
+    // M=512 (at most one 128-row tile per CU) 64 rows lose 30-50%.
+    const int64_t tn = swiglu ? geom::ceil_div(N / 2, kBN / 2) : geom::ceil_div(N, kBN);
+    const int64_t tiles = geom::ceil_div(M, int64_t{128}) * tn, cus = device_cu_count();
+    return (tiles <= cus / 2 || (tiles > cus && tiles <= 2 * cus)) ? 64 : 128;
+}
+
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
+    return launch_gemm_prefill_bm(a, prefill_tile_rows(a.M, a.N, a.swiglu), stream);
+}
+
+hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream) {
+    if (bm != 64 && bm != 128) return hipErrorInvalidValue;
     PrefillParams p{};
     p.A = a.a_q;
     p.lda = a.lda;
@@ -533,7 +566,9 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     p.gs = static_cast<int>(geom::group_stride(a.group));
     p.kpad = static_cast<int>(geom::kpad(a.K, a.group));
     p.tpg = p.gs / 128;
-    p.tiles_m = static_cast<int>(geom::ceil_div(a.M, kBM));
+    p.bm = a.partials ? 128 : bm;
+    bm = p.bm;
+    p.tiles_m = static_cast<int>(geom::ceil_div(a.M, p.bm));
     p.half_n = a.swiglu ? static_cast<int>(a.N / 2) : 0;
     p.tiles_n = static_cast<int>(a.swiglu ? geom::ceil_div(a.N / 2, kBN / 2) : geom::ceil_div(a.N, kBN));
     p.band = 4;

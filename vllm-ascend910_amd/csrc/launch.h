@@ -92,6 +92,10 @@ hipError_t launch_split_reduce(const float* R, int64_t ldr, const uint16_t* a_sc
 // Prefill path (M > kDecodeMaxM): MFMA bound, LDS-tiled.
 int64_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
+// The prefill GEMM with an explicit tile height (128 or 64 rows), and the
+// height launch_gemm_prefill picks.
+hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream);
+int prefill_tile_rows(int64_t M, int64_t N, bool swiglu);
 
 
 // Mid-group compat path (the reference's midgroup_quant_a / midgroup_w4a8_gemm).
