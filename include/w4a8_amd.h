@@ -45,7 +45,8 @@ enum w4a8_status {
 enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
 
 /* Library ABI version (bumped on any signature or contract change: 4 = the
- * first build whose GEMM asks a workspace of some decode shapes). */
+ * first build whose GEMM asks a workspace of some decode shapes; 5 adds
+ * w4a8_rope_kv). */
 int w4a8_abi_version(void);
 
 /* Message for the calling thread's last failed call ("" if none). */
@@ -224,6 +225,29 @@ int w4a8_gemm_debug_partials(const void* a_q, int64_t lda, const void* a_scale,
 int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight, float eps,
                        void* sum_out, int64_t lds, void* h_out, int64_t ldh, void* a_q, int64_t lda, void* a_scale,
                        int64_t M, int64_t K, int64_t group, void* stream);
+
+/*
+ * Rotary embedding of the q and k heads of a fused qkv projection output,
+ * fused with the KV-cache append, for the decoder forward that drives the
+ * W4A8 linears (QwQ-32B: H = 40 q heads, KVH = 8 kv heads, D = 128).
+ *   qkv      bf16 [B * T, ldq]   per token: H q heads, KVH k heads, KVH v heads, D each
+ *   cos_tab, sin_tab  fp32 [L, ldc]   angle tables (columns 0 .. D/2-1 used)
+ *   pos      int64 (device)      position of token 0 of every sequence; token t
+ *                                sits at pos[0] + t (read on the device, so a
+ *                                captured decode step follows it)
+ *   q_out    bf16 [B * T, H, D]  rotated q
+ *   k_cache  element (b, h, d, p) at k_strides . (b, h, d, p): rotated k written at p
+ *   v_cache  element (b, h, p, d) at v_strides . (b, h, p, d): v copied at p
+ * Rotate-half form with the rounding sequence torch evaluates on float
+ * tensors: y[i] = bf16(fl(x1*c) - fl(x2*s)), y[i+D/2] = bf16(fl(x2*c) +
+ * fl(x1*s)), no fused multiply-add.  A token whose position falls outside
+ * [0, L) writes nothing to the caches and zeros to its q rows.  No
+ * counterpart in the reference, whose decoder-layer bench appends k and v in
+ * place without a rotary embedding (npu_ops/python/bench_decode_layer.py:57-73).
+ */
+int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* cos_tab, const void* sin_tab, int64_t ldc, int64_t L,
+                 const void* pos, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
+                 const int64_t* v_strides, int64_t B, int64_t T, int64_t H, int64_t KVH, int64_t D, void* stream);
 
 /*
  * ---- Reference-compat mid-group path ----

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported(pkg, lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.w4a8_abi_version() == 4
+    assert lib.w4a8_abi_version() == 5
     # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
     assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
@@ -95,6 +95,27 @@ def test_quant_and_repack_reject_bad_arguments(lib):
     assert lib.w4a8_repack(16, 16, 2, 16, 16, 64, 256, 128, None) == 3
     assert lib.w4a8_repack(18, 16, 0, 16, 16, 64, 256, 128, None) == 4
     assert lib.w4a8_repack(16, 16, 0, 16, 16, 64, 256, 0, None) == 2
+
+
+def test_rope_kv_rejects_bad_arguments(lib):
+    # fake, never-dereferenced addresses: validation fails before any launch
+    st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+
+    def call(**kw):
+        a = dict(qkv=16, ldq=7168, cos=16, sin=16, ldc=64, L=64, pos=16, q=16, kc=16, vc=16, B=1, T=1, H=40,
+                 KVH=8, D=128)
+        a.update(kw)
+        return lib.w4a8_rope_kv(a["qkv"], a["ldq"], a["cos"], a["sin"], a["ldc"], a["L"], a["pos"], a["q"],
+                                a["kc"], st, a["vc"], st, a["B"], a["T"], a["H"], a["KVH"], a["D"], None)
+    assert call(D=127) == 2 and "D even" in lib.w4a8_last_error().decode()
+    assert call(L=0) == 2
+    assert call(ldq=7000) == 2 and "leading dimensions" in lib.w4a8_last_error().decode()
+    assert call(ldc=63) == 2
+    assert call(qkv=None) == 1
+    assert call(cos=18) == 4                 # fp32 table not 4-byte aligned
+    assert call(pos=20) == 4                 # int64 position not 8-byte aligned
+    assert call(B=0, qkv=None) == 0          # nothing to do
+    assert lib.w4a8_rope_kv(16, 7168, 16, 16, 64, 64, 16, 16, 16, None, 16, st, 1, 1, 40, 8, 128, None) == 1
 
 
 def test_errors_raise_runtimeerror_from_python(pkg):

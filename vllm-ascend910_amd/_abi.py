@@ -15,7 +15,7 @@ from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "_lib" / "libw4a8_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1
@@ -44,6 +44,8 @@ SIGNATURES = {
                                 _I64, _I64, _I64, _VP]),
     "w4a8_gemm_debug_partials": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _VP, _I64, _I64, _I64, _I64,
                                       _VP, _I64, _VP]),
+    "w4a8_rope_kv": (_I, [_VP, _I64, _VP, _VP, _I64, _I64, _VP, _VP, _VP, ctypes.POINTER(_I64), _VP,
+                          ctypes.POINTER(_I64), _I64, _I64, _I64, _I64, _I64, _VP]),
 }
 
 STATUS_NAMES = {0: "OK", 1: "NULL", 2: "SHAPE", 3: "DTYPE", 4: "ALIGN", 5: "UNSUPPORTED", 6: "WORKSPACE",

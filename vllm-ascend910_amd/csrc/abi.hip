@@ -206,7 +206,7 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 4; }
+int w4a8_abi_version(void) { return 5; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
@@ -446,6 +446,46 @@ int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t
     a.K = K;
     a.group = group;
     return hip_status(launch_rmsnorm_quant(a, static_cast<hipStream_t>(stream)), "w4a8_rmsnorm_quant launch");
+}
+
+int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* cos_tab, const void* sin_tab, int64_t ldc, int64_t L,
+                 const void* pos, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
+                 const int64_t* v_strides, int64_t B, int64_t T, int64_t H, int64_t KVH, int64_t D, void* stream) {
+    if (B < 0 || T < 0 || L <= 0 || B * T >= (1ll << 31))
+        return fail(W4A8_ERR_SHAPE, "bad shape: B=%lld T=%lld L=%lld", B, T, L);
+    if (H <= 0 || KVH <= 0 || D <= 0 || D % 2 != 0 || (H + 2 * KVH) * D > (1ll << 30))
+        return fail(W4A8_ERR_SHAPE, "bad heads: H=%lld KVH=%lld D=%lld (D even)", H, KVH, D);
+    if (B * T == 0) return W4A8_OK;
+    if (!qkv || !cos_tab || !sin_tab || !pos || !q_out || !k_cache || !v_cache || !k_strides || !v_strides)
+        return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (ldq < (H + 2 * KVH) * D || ldc < D / 2)
+        return fail(W4A8_ERR_SHAPE, "leading dimensions must cover the row (qkv %lld, cos/sin %lld)",
+                    (H + 2 * KVH) * D, D / 2);
+    if (!aligned(qkv, 2) || !aligned(q_out, 2) || !aligned(k_cache, 2) || !aligned(v_cache, 2) ||
+        !aligned(cos_tab, 4) || !aligned(sin_tab, 4) || !aligned(pos, 8))
+        return fail(W4A8_ERR_ALIGN, "bf16 operands 2-byte, cos/sin 4-byte and pos 8-byte aligned");
+    RopeKvArgs a{};
+    a.qkv = static_cast<const uint16_t*>(qkv);
+    a.ldq = ldq;
+    a.cos = static_cast<const float*>(cos_tab);
+    a.sin = static_cast<const float*>(sin_tab);
+    a.ldc = ldc;
+    a.pos = static_cast<const int64_t*>(pos);
+    a.q_out = static_cast<uint16_t*>(q_out);
+    a.k_cache = static_cast<uint16_t*>(k_cache);
+    a.v_cache = static_cast<uint16_t*>(v_cache);
+    for (int i = 0; i < 4; ++i) {
+        if (k_strides[i] < 0 || v_strides[i] < 0) return fail(W4A8_ERR_SHAPE, "cache strides must be >= 0");
+        a.ks[i] = k_strides[i];
+        a.vs[i] = v_strides[i];
+    }
+    a.B = static_cast<int>(B);
+    a.T = static_cast<int>(T);
+    a.H = static_cast<int>(H);
+    a.KVH = static_cast<int>(KVH);
+    a.D = static_cast<int>(D);
+    a.L = L;
+    return hip_status(launch_rope_kv(a, static_cast<hipStream_t>(stream)), "w4a8_rope_kv launch");
 }
 
 }  // extern "C"

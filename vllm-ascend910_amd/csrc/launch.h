@@ -141,6 +141,25 @@ struct RmsNormArgs {
 };
 hipError_t launch_rmsnorm_quant(const RmsNormArgs& a, hipStream_t stream);
 
+// Rotary embedding of the q and k heads of a fused qkv projection output and
+// the KV-cache append (rope_kv.hip).
+struct RopeKvArgs {
+    const uint16_t* qkv;    // bf16 [B * T, ldq]: H q heads, KVH k heads, KVH v heads of D
+    int64_t ldq;
+    const float* cos;       // fp32 [L, ldc], columns 0 .. D/2-1 used
+    const float* sin;
+    int64_t ldc;
+    const int64_t* pos;     // device: position of token 0 of every sequence
+    uint16_t* q_out;        // bf16 [B * T, H, D]
+    uint16_t* k_cache;      // element (b, h, d, p) at b*ks[0] + h*ks[1] + d*ks[2] + p*ks[3]
+    int64_t ks[4];
+    uint16_t* v_cache;      // element (b, h, p, d) at b*vs[0] + h*vs[1] + p*vs[2] + d*vs[3]
+    int64_t vs[4];
+    int B, T, H, KVH, D;
+    int64_t L;              // cache positions
+};
+hipError_t launch_rope_kv(const RopeKvArgs& a, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace w4a8

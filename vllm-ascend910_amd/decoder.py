@@ -11,6 +11,9 @@ embeddings, RMSNorm) on this build's ops:
   (``torch.ops.npu.w4a8_rmsnorm_quant``) in front of qkv and gate_up;
 * gate_up runs with the fused SwiGLU epilogue (``w4a8_gemm_swiglu``);
 * o and down run ``w4a8_linear`` (quant + GEMM, one launch for a single row);
+* the rotary embedding of q and k and the KV-cache append run as one kernel
+  (``torch.ops.npu.w4a8_rope_kv``, fp32 products and sums rounded to bf16 as
+  torch rounds them on float tensors);
 * attention stays on PyTorch-ROCm in bf16, written with contiguous batched
   products only: the K cache is stored transposed ``[B, KVH, D, L]`` and the
   query heads of one KV head form the rows of one product, so grouped-query
@@ -119,6 +122,7 @@ class W4A8Decoder:
         self.positions = torch.arange(max_len, device=dev)
         # decode-step state (device tensors, so a captured step is position-independent)
         self.pos = torch.zeros((1,), dtype=torch.long, device=dev)
+        self._pos0 = torch.zeros((1,), dtype=torch.long, device=dev)   # prefill writes from position 0
         self.tokens = torch.zeros((batch,), dtype=torch.long, device=dev)
         self._graph: Optional[torch.cuda.CUDAGraph] = None
 
@@ -141,13 +145,13 @@ class W4A8Decoder:
         self.pos.zero_()
 
     # ------------------------------------------------------------ pieces
-    def _rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-        """Rotary embedding, rotate-half form; x [..., T, heads, d], cos/sin [T, d/2]."""
-        h = x.shape[-1] // 2
-        xf = x.float()
-        x1, x2 = xf[..., :h], xf[..., h:]
-        c, s = cos[:, None, :], sin[:, None, :]
-        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1).to(torch.bfloat16)
+    def _rope_kv(self, li: int, qkv: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """Rotary embedding (rotate-half form, fp32 products and sums, bf16 result) of the q and
+        k heads of qkv [B, T, width]; k and v appended to layer li's caches at positions
+        pos[0] + t; returns q [B, T, heads, head_dim].  One kernel (w4a8_rope_kv)."""
+        c = self.cfg
+        return torch.ops.npu.w4a8_rope_kv(qkv, self.cos, self.sin, pos, self.k_cache[li], self.v_cache[li],
+                                          c.heads, c.kv_heads)
 
     def _attend(self, q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
         """q [B, KVH, R, D] (R = query heads per KV head x query tokens), kc [B, KVH, D, L],
@@ -172,19 +176,14 @@ class W4A8Decoder:
         S = tokens.shape[1]
         assert tokens.shape[0] == B and S <= self.max_len
         G = c.heads // c.kv_heads
-        cos, sin = self.cos[:S], self.sin[:S]
         causal = torch.full((S, S), float("-inf"), device=self.device).triu_(1)
         x = self.embed[tokens.reshape(-1)]                               # [B*S, hidden]
         delta = None
         for li, L in enumerate(self.layers):
             aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
             x = s if delta is not None else x
-            qkv = L["qkv"](aq, as_).view(B, S, c.heads + 2 * c.kv_heads, c.head_dim)
-            q = self._rope(qkv[:, :, :c.heads], cos, sin)
-            k = self._rope(qkv[:, :, c.heads:c.heads + c.kv_heads], cos, sin)
-            v = qkv[:, :, c.heads + c.kv_heads:]
-            self.k_cache[li][:, :, :, :S] = k.permute(0, 2, 3, 1)
-            self.v_cache[li][:, :, :S, :] = v.permute(0, 2, 1, 3)
+            qkv = L["qkv"](aq, as_).view(B, S, -1)
+            q = self._rope_kv(li, qkv, self._pos0)                  # [B, S, H, D]; caches filled for [0, S)
             kc = self.k_cache[li][:, :, :, :S].contiguous()
             vc = self.v_cache[li][:, :, :S, :].contiguous()
             out = torch.empty((B, S, c.heads, c.head_dim), dtype=torch.bfloat16, device=self.device)
@@ -214,20 +213,14 @@ class W4A8Decoder:
         """One greedy step at self.pos for self.tokens, updating both in place (capturable)."""
         c, B = self.cfg, self.batch
         G = c.heads // c.kv_heads
-        cos = self.cos.index_select(0, self.pos)
-        sin = self.sin.index_select(0, self.pos)
         bias = torch.where(self.positions > self.pos, float("-inf"), 0.0).view(1, 1, 1, self.max_len)
         x = self.embed.index_select(0, self.tokens)                      # [B, hidden]
         delta = None
         for li, L in enumerate(self.layers):
             aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
             x = s if delta is not None else x
-            qkv = L["qkv"](aq, as_).view(B, 1, c.heads + 2 * c.kv_heads, c.head_dim)
-            q = self._rope(qkv[:, :, :c.heads], cos, sin)                # [B, 1, H, D]
-            k = self._rope(qkv[:, :, c.heads:c.heads + c.kv_heads], cos, sin)
-            v = qkv[:, :, c.heads + c.kv_heads:]
-            self.k_cache[li].index_copy_(3, self.pos, k.view(B, c.kv_heads, c.head_dim, 1))
-            self.v_cache[li].index_copy_(2, self.pos, v.reshape(B, c.kv_heads, 1, c.head_dim))
+            qkv = L["qkv"](aq, as_).view(B, 1, -1)
+            q = self._rope_kv(li, qkv, self.pos)                         # [B, 1, H, D]
             qg = q.view(B, c.kv_heads, G, c.head_dim)
             o = self._attend(qg, self.k_cache[li], self.v_cache[li], bias)          # [B, KVH, G, D]
             x, delta = self._mlp_and_next(L, x, o.reshape(B, c.heads * c.head_dim))
