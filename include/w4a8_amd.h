@@ -231,6 +231,8 @@ int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t
  * fused with the KV-cache append, for the decoder forward that drives the
  * W4A8 linears (QwQ-32B: H = 40 q heads, KVH = 8 kv heads, D = 128).
  *   qkv      bf16 [B * T, ldq]   per token: H q heads, KVH k heads, KVH v heads, D each
+ *   bias     bf16 [(H + 2 KVH) * D] or NULL: the projection bias, added first as
+ *                                torch adds two bf16 tensors, x = bf16(x + bias)
  *   cos_tab, sin_tab  fp32 [L, ldc]   angle tables (columns 0 .. D/2-1 used)
  *   pos      int64 (device)      position of token 0 of every sequence; token t
  *                                sits at pos[0] + t (read on the device, so a
@@ -245,8 +247,8 @@ int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t
  * counterpart in the reference, whose decoder-layer bench appends k and v in
  * place without a rotary embedding (npu_ops/python/bench_decode_layer.py:57-73).
  */
-int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* cos_tab, const void* sin_tab, int64_t ldc, int64_t L,
-                 const void* pos, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
+int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* bias, const void* cos_tab, const void* sin_tab, int64_t ldc,
+                 int64_t L, const void* pos, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
                  const int64_t* v_strides, int64_t B, int64_t T, int64_t H, int64_t KVH, int64_t D, void* stream);
 
 /*

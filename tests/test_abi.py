@@ -105,8 +105,8 @@ def test_rope_kv_rejects_bad_arguments(lib):
         a = dict(qkv=16, ldq=7168, cos=16, sin=16, ldc=64, L=64, pos=16, q=16, kc=16, vc=16, B=1, T=1, H=40,
                  KVH=8, D=128)
         a.update(kw)
-        return lib.w4a8_rope_kv(a["qkv"], a["ldq"], a["cos"], a["sin"], a["ldc"], a["L"], a["pos"], a["q"],
-                                a["kc"], st, a["vc"], st, a["B"], a["T"], a["H"], a["KVH"], a["D"], None)
+        return lib.w4a8_rope_kv(a["qkv"], a["ldq"], a.get("bias"), a["cos"], a["sin"], a["ldc"], a["L"], a["pos"],
+                                a["q"], a["kc"], st, a["vc"], st, a["B"], a["T"], a["H"], a["KVH"], a["D"], None)
     assert call(D=127) == 2 and "D even" in lib.w4a8_last_error().decode()
     assert call(L=0) == 2
     assert call(ldq=7000) == 2 and "leading dimensions" in lib.w4a8_last_error().decode()
@@ -114,8 +114,10 @@ def test_rope_kv_rejects_bad_arguments(lib):
     assert call(qkv=None) == 1
     assert call(cos=18) == 4                 # fp32 table not 4-byte aligned
     assert call(pos=20) == 4                 # int64 position not 8-byte aligned
+    assert call(bias=17) == 4                # bf16 bias not 2-byte aligned
+    assert call(H=65535) == 2                # one workgroup row per head
     assert call(B=0, qkv=None) == 0          # nothing to do
-    assert lib.w4a8_rope_kv(16, 7168, 16, 16, 64, 64, 16, 16, 16, None, 16, st, 1, 1, 40, 8, 128, None) == 1
+    assert lib.w4a8_rope_kv(16, 7168, None, 16, 16, 64, 64, 16, 16, 16, None, 16, st, 1, 1, 40, 8, 128, None) == 1
 
 
 def test_errors_raise_runtimeerror_from_python(pkg):

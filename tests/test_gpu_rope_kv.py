@@ -1,8 +1,9 @@
 """w4a8_rope_kv: the decoder's rotary embedding + KV-cache append in one kernel.
 
-Bar: bit-identical to the torch evaluation it replaces -- q and k rotated with
-fp32 products and sums on float tensors (rotate-half form), rounded to bf16,
-then k written at [b, h, :, p] of the transposed K cache and v at [b, h, p, :]
+Bar: bit-identical to the torch evaluation it replaces -- the projection bias
+added as a bf16 add, q and k rotated with fp32 products and sums on float
+tensors (rotate-half form), rounded to bf16, then k written at [b, h, :, p] of
+the transposed K cache and v at [b, h, p, :]
 -- for decode (one token at a device-held position), prefill (many tokens from
 position 0 and from an offset), a token range crossing the cache end (q zero,
 nothing written past it), a K cache given as a strided view, and replays of a
@@ -38,8 +39,11 @@ def tables(L, D, dev, theta=1.0e6):
     return torch.cos(ang), torch.sin(ang)
 
 
-def reference(qkv, cos, sin, p0, kc, vc, H, KVH):
-    """The torch path: (q, k_cache', v_cache') for tokens at p0 .. p0+T-1 (all inside the cache)."""
+def reference(qkv, cos, sin, p0, kc, vc, H, KVH, bias=None):
+    """The torch path: (q, k_cache', v_cache') for tokens at p0 .. p0+T-1 (all inside the cache),
+    the projection bias added first as a bf16 add."""
+    if bias is not None:
+        qkv = qkv + bias
     B, T, W = qkv.shape
     D = W // (H + 2 * KVH)
     x = qkv.view(B, T, H + 2 * KVH, D)
@@ -65,19 +69,24 @@ def make(B, T, H, KVH, D, L, dev, seed):
     return qkv, kc, vc
 
 
-@pytest.mark.parametrize("B,T,H,KVH,D,L,p0", [
-    (2, 1, 40, 8, 128, 64, 17),      # QwQ-32B heads, one decode token
-    (1, 1, 40, 8, 128, 1280, 1279),  # the last slot of a 1024 + 256 cache
-    (3, 37, 40, 8, 128, 48, 0),      # prefill from position 0
-    (2, 23, 4, 2, 64, 40, 5),        # small heads, prefill after 5 cached tokens
+@pytest.mark.parametrize("B,T,H,KVH,D,L,p0,with_bias", [
+    (2, 1, 40, 8, 128, 64, 17, True),      # QwQ-32B heads (qkv bias), one decode token
+    (1, 1, 40, 8, 128, 1280, 1279, True),  # the last slot of a 1024 + 256 cache
+    (3, 37, 40, 8, 128, 48, 0, True),      # prefill from position 0
+    (2, 23, 4, 2, 64, 40, 5, False),       # small heads, no bias, prefill after 5 cached tokens
+    (2, 1, 4, 2, 64, 40, 9, False),
 ])
-def test_rope_kv_matches_torch(pkg, dev, B, T, H, KVH, D, L, p0):
-    say(f"rope_kv B={B} T={T} H={H} KVH={KVH} D={D} L={L} p0={p0}")
+def test_rope_kv_matches_torch(pkg, dev, B, T, H, KVH, D, L, p0, with_bias):
+    say(f"rope_kv B={B} T={T} H={H} KVH={KVH} D={D} L={L} p0={p0} bias={with_bias}")
     qkv, kc, vc = make(B, T, H, KVH, D, L, dev, seed=B * 1000 + T)
     cos, sin = tables(L, D, dev)
-    q_ref, kc_ref, vc_ref = reference(qkv, cos, sin, p0, kc, vc, H, KVH)
+    bias = None
+    if with_bias:
+        g = torch.Generator(device=dev).manual_seed(99)
+        bias = ((torch.rand(((H + 2 * KVH) * D,), device=dev, generator=g) - 0.5) * 0.2).to(torch.bfloat16)
+    q_ref, kc_ref, vc_ref = reference(qkv, cos, sin, p0, kc, vc, H, KVH, bias)
     pos = torch.tensor([p0], dtype=torch.int64, device=dev)
-    q = torch.ops.npu.w4a8_rope_kv(qkv, cos, sin, pos, kc, vc, H, KVH)
+    q = torch.ops.npu.w4a8_rope_kv(qkv, cos, sin, pos, kc, vc, H, KVH, bias)
     torch.cuda.synchronize()
     assert q.shape == (B, T, H, D)
     assert bits_equal(q, q_ref)

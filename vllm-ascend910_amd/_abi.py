@@ -44,7 +44,7 @@ SIGNATURES = {
                                 _I64, _I64, _I64, _VP]),
     "w4a8_gemm_debug_partials": (_I, [_VP, _I64, _VP, _VP, _VP, _I, _VP, _I64, _VP, _I64, _I64, _I64, _I64,
                                       _VP, _I64, _VP]),
-    "w4a8_rope_kv": (_I, [_VP, _I64, _VP, _VP, _I64, _I64, _VP, _VP, _VP, ctypes.POINTER(_I64), _VP,
+    "w4a8_rope_kv": (_I, [_VP, _I64, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, ctypes.POINTER(_I64), _VP,
                           ctypes.POINTER(_I64), _I64, _I64, _I64, _I64, _I64, _VP]),
 }
 

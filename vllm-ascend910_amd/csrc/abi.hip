@@ -448,12 +448,12 @@ int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t
     return hip_status(launch_rmsnorm_quant(a, static_cast<hipStream_t>(stream)), "w4a8_rmsnorm_quant launch");
 }
 
-int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* cos_tab, const void* sin_tab, int64_t ldc, int64_t L,
-                 const void* pos, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
+int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* bias, const void* cos_tab, const void* sin_tab, int64_t ldc,
+                 int64_t L, const void* pos, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
                  const int64_t* v_strides, int64_t B, int64_t T, int64_t H, int64_t KVH, int64_t D, void* stream) {
     if (B < 0 || T < 0 || L <= 0 || B * T >= (1ll << 31))
         return fail(W4A8_ERR_SHAPE, "bad shape: B=%lld T=%lld L=%lld", B, T, L);
-    if (H <= 0 || KVH <= 0 || D <= 0 || D % 2 != 0 || (H + 2 * KVH) * D > (1ll << 30))
+    if (H <= 0 || KVH <= 0 || D <= 0 || D % 2 != 0 || H + 2 * KVH > 65535 || (H + 2 * KVH) * D > (1ll << 30))
         return fail(W4A8_ERR_SHAPE, "bad heads: H=%lld KVH=%lld D=%lld (D even)", H, KVH, D);
     if (B * T == 0) return W4A8_OK;
     if (!qkv || !cos_tab || !sin_tab || !pos || !q_out || !k_cache || !v_cache || !k_strides || !v_strides)
@@ -461,12 +461,13 @@ int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* cos_tab, const void* 
     if (ldq < (H + 2 * KVH) * D || ldc < D / 2)
         return fail(W4A8_ERR_SHAPE, "leading dimensions must cover the row (qkv %lld, cos/sin %lld)",
                     (H + 2 * KVH) * D, D / 2);
-    if (!aligned(qkv, 2) || !aligned(q_out, 2) || !aligned(k_cache, 2) || !aligned(v_cache, 2) ||
+    if (!aligned(qkv, 2) || !aligned(bias, 2) || !aligned(q_out, 2) || !aligned(k_cache, 2) || !aligned(v_cache, 2) ||
         !aligned(cos_tab, 4) || !aligned(sin_tab, 4) || !aligned(pos, 8))
         return fail(W4A8_ERR_ALIGN, "bf16 operands 2-byte, cos/sin 4-byte and pos 8-byte aligned");
     RopeKvArgs a{};
     a.qkv = static_cast<const uint16_t*>(qkv);
     a.ldq = ldq;
+    a.bias = static_cast<const uint16_t*>(bias);
     a.cos = static_cast<const float*>(cos_tab);
     a.sin = static_cast<const float*>(sin_tab);
     a.ldc = ldc;

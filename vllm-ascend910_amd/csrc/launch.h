@@ -146,6 +146,7 @@ hipError_t launch_rmsnorm_quant(const RmsNormArgs& a, hipStream_t stream);
 struct RopeKvArgs {
     const uint16_t* qkv;    // bf16 [B * T, ldq]: H q heads, KVH k heads, KVH v heads of D
     int64_t ldq;
+    const uint16_t* bias;   // optional bf16 [(H + 2 KVH) * D], added before the rotation
     const float* cos;       // fp32 [L, ldc], columns 0 .. D/2-1 used
     const float* sin;
     int64_t ldc;

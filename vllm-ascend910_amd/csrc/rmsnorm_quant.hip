@@ -81,6 +81,14 @@ __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const RmsParams p) {
     const uint4* rr = RES ? reinterpret_cast<const uint4*>(p.res + row * p.ldr) : nullptr;
     const uint4* wr = reinterpret_cast<const uint4*>(p.w);
 
+    // the norm weight is requested with the row (it is used after the
+    // reduction, which would otherwise wait for a second memory round trip)
+    uint4 wv[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * NT;
+        wv[i] = idx < nvec ? wr[idx] : make_uint4(0u, 0u, 0u, 0u);
+    }
     // s = bf16(x + r) kept as packed bf16 pairs; per-thread sum of squares
     uint4 v[VPT];
     float ss = 0.0f;
@@ -122,9 +130,8 @@ __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const RmsParams p) {
         const int idx = static_cast<int>(threadIdx.x) + i * NT;
         if (idx >= nvec) continue;
         if (p.sum_out) *reinterpret_cast<uint4*>(p.sum_out + row * p.lds + idx * 8) = v[i];
-        const uint4 wv = wr[idx];
         uint32_t* pa = reinterpret_cast<uint32_t*>(&v[i]);
-        const uint32_t* pw = reinterpret_cast<const uint32_t*>(&wv);
+        const uint32_t* pw = reinterpret_cast<const uint32_t*>(&wv[i]);
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const float h0 = bf16r(bf16r(__uint_as_float(pa[d] << 16) * r) * __uint_as_float(pw[d] << 16));

@@ -75,8 +75,12 @@ class _Linear:
         self.bias = ((torch.rand((N,), device=device, generator=gen) - 0.5) * 0.2).to(torch.bfloat16) if bias \
             else None
 
+    def gemm(self, a_q: torch.Tensor, a_s: torch.Tensor) -> torch.Tensor:
+        """The GEMM alone (the bias left to the consumer)."""
+        return torch.ops.npu.w4a8_gemm(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+
     def __call__(self, a_q: torch.Tensor, a_s: torch.Tensor) -> torch.Tensor:
-        y = torch.ops.npu.w4a8_gemm(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+        y = self.gemm(a_q, a_s)
         return y + self.bias if self.bias is not None else y
 
     def linear(self, x: torch.Tensor) -> torch.Tensor:
@@ -145,13 +149,16 @@ class W4A8Decoder:
         self.pos.zero_()
 
     # ------------------------------------------------------------ pieces
-    def _rope_kv(self, li: int, qkv: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        """Rotary embedding (rotate-half form, fp32 products and sums, bf16 result) of the q and
-        k heads of qkv [B, T, width]; k and v appended to layer li's caches at positions
-        pos[0] + t; returns q [B, T, heads, head_dim].  One kernel (w4a8_rope_kv)."""
+    def _rope_kv(self, li: int, L: dict, aq: torch.Tensor, as_: torch.Tensor, T: int,
+                 pos: torch.Tensor) -> torch.Tensor:
+        """qkv projection of layer li, then its bias (a bf16 add), the rotary embedding (rotate-half
+        form, fp32 products and sums, bf16 result) of the q and k heads, and k and v appended to
+        the layer's caches at positions pos[0] + t; returns q [B, T, heads, head_dim].  The bias,
+        rotation and append are one kernel (w4a8_rope_kv)."""
         c = self.cfg
+        qkv = L["qkv"].gemm(aq, as_).view(self.batch, T, -1)
         return torch.ops.npu.w4a8_rope_kv(qkv, self.cos, self.sin, pos, self.k_cache[li], self.v_cache[li],
-                                          c.heads, c.kv_heads)
+                                          c.heads, c.kv_heads, L["qkv"].bias)
 
     def _attend(self, q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
         """q [B, KVH, R, D] (R = query heads per KV head x query tokens), kc [B, KVH, D, L],
@@ -182,8 +189,7 @@ class W4A8Decoder:
         for li, L in enumerate(self.layers):
             aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
             x = s if delta is not None else x
-            qkv = L["qkv"](aq, as_).view(B, S, -1)
-            q = self._rope_kv(li, qkv, self._pos0)                  # [B, S, H, D]; caches filled for [0, S)
+            q = self._rope_kv(li, L, aq, as_, S, self._pos0)        # [B, S, H, D]; caches filled for [0, S)
             kc = self.k_cache[li][:, :, :, :S].contiguous()
             vc = self.v_cache[li][:, :, :S, :].contiguous()
             out = torch.empty((B, S, c.heads, c.head_dim), dtype=torch.bfloat16, device=self.device)
@@ -219,8 +225,7 @@ class W4A8Decoder:
         for li, L in enumerate(self.layers):
             aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
             x = s if delta is not None else x
-            qkv = L["qkv"](aq, as_).view(B, 1, -1)
-            q = self._rope_kv(li, qkv, self.pos)                         # [B, 1, H, D]
+            q = self._rope_kv(li, L, aq, as_, 1, self.pos)               # [B, 1, H, D]
             qg = q.view(B, c.kv_heads, G, c.head_dim)
             o = self._attend(qg, self.k_cache[li], self.v_cache[li], bias)          # [B, KVH, G, D]
             x, delta = self._mlp_and_next(L, x, o.reshape(B, c.heads * c.head_dim))

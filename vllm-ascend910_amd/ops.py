@@ -16,7 +16,7 @@ and two producer-side helpers of the decoder forward that drives them:
 
     torch.ops.npu.w4a8_rmsnorm_quant(x, weight, eps, residual=None, group=0, want_normed=False)
         -> (a_q, a_scale, s, h)
-    torch.ops.npu.w4a8_rope_kv(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads) -> q
+    torch.ops.npu.w4a8_rope_kv(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads, bias=None) -> q
 
 and, with the reference's own names and schemas (group appended with the
 reference's fixed value as default), its mid-group compat pair:
@@ -55,7 +55,7 @@ _LIB.define("w4a8_linear(Tensor x, Tensor w_tiles, Tensor s_tiles, int N, int K,
 _LIB.define("w4a8_rmsnorm_quant(Tensor x, Tensor weight, float eps, Tensor? residual=None, int group=0, "
             "bool want_normed=False) -> (Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("w4a8_rope_kv(Tensor qkv, Tensor cos, Tensor sin, Tensor pos, Tensor(a!) k_cache, Tensor(b!) v_cache, "
-            "int heads, int kv_heads) -> Tensor")
+            "int heads, int kv_heads, Tensor? bias=None) -> Tensor")
 _LIB.define("midgroup_quant_a(Tensor x, int group=1024) -> Tensor[]")
 _LIB.define("midgroup_w4a8_gemm(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
             "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> Tensor")
@@ -351,10 +351,11 @@ def _rmsnorm_quant_fake(x, weight, eps, residual=None, group=0, want_normed=Fals
 # ---------------------------------------------------------------- RoPE + KV-cache append
 @torch.library.impl(_LIB, "w4a8_rope_kv", "CUDA")
 def _rope_kv_cuda(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
-                  k_cache: torch.Tensor, v_cache: torch.Tensor, heads: int, kv_heads: int) -> torch.Tensor:
-    """q [B, T, heads, D]: the rotated q heads of qkv [B, T, (heads + 2 kv_heads) * D]; the rotated k
-    heads go to k_cache [B, kv_heads, D, L] and the v heads to v_cache [B, kv_heads, L, D] at
-    positions pos[0] + t (any strides; cos/sin fp32 [>= L, >= D/2] angle tables)."""
+                  k_cache: torch.Tensor, v_cache: torch.Tensor, heads: int, kv_heads: int,
+                  bias=None) -> torch.Tensor:
+    """q [B, T, heads, D]: the rotated q heads of qkv [B, T, (heads + 2 kv_heads) * D] (+ bias, a bf16
+    add); the rotated k heads go to k_cache [B, kv_heads, D, L] and the v heads to v_cache
+    [B, kv_heads, L, D] at positions pos[0] + t (any strides; cos/sin fp32 [>= L, >= D/2] angle tables)."""
     _require(qkv.dim() == 3 and qkv.dtype == torch.bfloat16, "w4a8_rope_kv: qkv must be bfloat16 [B, T, W]")
     B, T, W = qkv.shape
     _require(heads > 0 and kv_heads > 0 and W % (heads + 2 * kv_heads) == 0,
@@ -374,19 +375,24 @@ def _rope_kv_cuda(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: 
              "w4a8_rope_kv: pos must be an int64 tensor on the device")
     if qkv.stride(2) != 1 or qkv.stride(0) != T * qkv.stride(1):
         qkv = qkv.contiguous()
+    if bias is not None:
+        _require(bias.dtype == torch.bfloat16 and bias.numel() == W and bias.device == qkv.device,
+                 "w4a8_rope_kv: bias must be bfloat16 [(heads + 2 kv_heads) * head_dim] on the device")
+        bias = bias.contiguous()
     q = torch.empty((B, T, heads, D), dtype=torch.bfloat16, device=qkv.device)
     if B * T:
         ks = (ctypes.c_int64 * 4)(*k_cache.stride())
         vs = (ctypes.c_int64 * 4)(*v_cache.stride())
         _abi.check(_abi.lib().w4a8_rope_kv(
-            qkv.data_ptr(), qkv.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0), L, pos.data_ptr(),
+            qkv.data_ptr(), qkv.stride(1), bias.data_ptr() if bias is not None else None, cos.data_ptr(),
+            sin.data_ptr(), cos.stride(0), L, pos.data_ptr(),
             q.data_ptr(), k_cache.data_ptr(), ks, v_cache.data_ptr(), vs, B, T, heads, kv_heads, D,
             _stream(qkv.device)), "w4a8_rope_kv")
     return q
 
 
 @torch.library.register_fake("npu::w4a8_rope_kv")
-def _rope_kv_fake(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads):
+def _rope_kv_fake(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads, bias=None):
     B, T, W = qkv.shape
     return qkv.new_empty((B, T, heads, W // (heads + 2 * kv_heads)))
 
