@@ -11,7 +11,8 @@
 // tree, so results are deterministic; its order differs from torch's
 // vectorised mean, which moves r by at most an fp32 ulp.  Optionally writes s
 // (the updated residual stream) and h.  One workgroup per row, the row held in
-// registers (256 threads up to 8192 elements, 1024 threads up to 65536).
+// registers (256 threads up to 8192 elements -- one 8-element unit per thread
+// for up to 64 rows -- and 1024 threads up to 65536).
 #include <type_traits>
 
 #include "common.h"
@@ -219,7 +220,13 @@ hipError_t launch_rmsnorm_quant(const RmsNormArgs& a, hipStream_t stream) {
         if (res) rmsnorm_quant_kernel<V, NT, true><<<grid, dim3(NT), 0, stream>>>(p);                    \
         else rmsnorm_quant_kernel<V, NT, false><<<grid, dim3(NT), 0, stream>>>(p);                       \
     }
+    // A few rows (decode) are latency bound: one 8-element unit per thread
+    // shortens each thread's serial work between the two block reductions.
+    // Many rows fill the GPU either way and keep 256-thread workgroups.
+    const bool few = a.M <= 64;
     if (nvec <= 256) W4A8_RMS(1, 256)
+    else if (few && nvec <= 512) W4A8_RMS(1, 512)
+    else if (few && nvec <= 1024) W4A8_RMS(1, 1024)
     else if (nvec <= 512) W4A8_RMS(2, 256)
     else if (nvec <= 1024) W4A8_RMS(4, 256)
     else if (nvec <= 2048) W4A8_RMS(2, 1024)
