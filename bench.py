@@ -91,6 +91,14 @@ def main():
     ap.add_argument("--prefill-probe", type=int, metavar="M", default=0,
                     help="for rocprofv3 runs: each configs[2] projection's prefill GEMM at M rows three times "
                          "(eager, group 128), then a 256 MiB device copy of known size")
+    ap.add_argument("--decoder-probe", type=int, metavar="B", default=0,
+                    help="for rocprofv3 runs: the --decoder-layers decoder at concurrency B, a 1024-token prefill "
+                         "(cache of 1024 + 64 positions, as the decoder leg), then its captured decode step "
+                         "replayed 5 + 10 times (the 10 between two marker launches are the ones "
+                         "--decoder-trace-summary reads)")
+    ap.add_argument("--decoder-trace-summary", metavar="DB",
+                    help="summarize a --kernel-trace database of a --decoder-probe run: kernels per decode step "
+                         "and their time, as markdown, and exit")
     ap.add_argument("--prefill-pmc-summary", nargs="+", metavar="DB",
                     help="summarize rocprofv3 databases of a --prefill-probe run (counter passes, then a "
                          "--kernel-trace database last) for gemm_prefill_kernel as markdown and exit")
@@ -103,6 +111,9 @@ def main():
         return
     if args.prefill_pmc_summary:
         prefill_pmc_summary(args.prefill_pmc_summary)
+        return
+    if args.decoder_trace_summary:
+        decoder_trace_summary(args.decoder_trace_summary)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the W4A8 linear is "
@@ -121,6 +132,9 @@ def main():
 
     if args.prefill_probe:
         prefill_probe(pkg, dev, args.prefill_probe)
+        return
+    if args.decoder_probe:
+        decoder_probe(pkg, dev, args.decoder_layers, args.decoder_probe)
         return
 
     # ---------------------------------------------------------------- data
@@ -470,6 +484,60 @@ def config4(pkg, dev, synth, make_pool, time_graph, T):
             del pool
             torch.cuda.empty_cache()
     return rows
+
+
+def decoder_probe(pkg, dev, layers, B, prompt=1024, steps=64, warm=5, timed=10):
+    """configs[4]'s decode step for a kernel trace, on the cache the bench's decoder leg uses
+    (`prompt` + `steps` positions): a prefill of `prompt` tokens, the step captured once, `warm`
+    graph replays, then `timed` replays between two marker launches (a tiny weight repack, a
+    kernel the decode step never runs) that --decoder-trace-summary cuts at."""
+    import torch
+    cfg = pkg.decoder.DecoderConfig(layers=layers)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=B, max_len=prompt + steps, device=dev, seed=7)
+    tokens = torch.randint(0, cfg.vocab, (B, prompt), generator=torch.Generator().manual_seed(0)).to(dev)
+    first = m.prefill(tokens)
+    torch.cuda.synchronize()
+    g = m.capture()
+    m.tokens.copy_(first)
+    m.pos.fill_(prompt)
+    w_q = torch.zeros((16, 64), dtype=torch.int8, device=dev)
+    w_s = torch.ones((1, 16), dtype=torch.float16, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(warm):
+        g.replay()
+    torch.ops.npu.w4a8_repack(w_q, w_s, 128, 128)      # marker
+    for _ in range(timed):
+        g.replay()
+    torch.ops.npu.w4a8_repack(w_q, w_s, 128, 128)      # marker
+    torch.cuda.synchronize()
+    log(f"bench: decoder probe done ({layers} layers, concurrency {B}, {timed} timed decode-step replays)")
+
+
+def decoder_trace_summary(db, timed=10):
+    """Kernels of one decode step (the average over the replays between the two markers of a
+    --decoder-probe run) as markdown."""
+    import collections
+    import sqlite3
+    rows = sqlite3.connect(db).execute("select name, duration, start, end from kernels order by start").fetchall()
+    marks = [i for i, r in enumerate(rows) if "repack_weight_kernel" in r[0]]
+    if len(marks) < 2:
+        raise SystemExit("bench.py: no --decoder-probe markers in this trace")
+    tail = [r for r in rows[marks[-2] + 1:marks[-1]] if "repack_scale_kernel" not in r[0]]
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    for name, d, _, _ in tail:
+        k = name.replace("(anonymous namespace)", "~").split("(")[0].strip()
+        if k.startswith("void "):
+            k = k[5:]
+        agg[k[:96]][0] += 1
+        agg[k[:96]][1] += d / 1e3
+    busy = sum(v[1] for v in agg.values()) / timed
+    span = (tail[-1][3] - tail[0][2]) / 1e3 / timed
+    print(f"Decode step, kernel trace of {timed} graph replays: {len(tail) / timed:.0f} launches per step, "
+          f"{busy:.0f} us of kernel time per step, {span:.0f} us from the first kernel's start to the last "
+          f"kernel's end per step (rocprof's timestamps; a traced run is slower than an untraced one).\n")
+    print("| kernel | per step | calls per step | us per call |\n|---|---:|---:|---:|")
+    for k, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:24]:
+        print(f"| `{k}` | {t / timed:.1f} us | {c / timed:.0f} | {t / c:.2f} |")
 
 
 def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
