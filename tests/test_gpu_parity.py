@@ -570,7 +570,7 @@ LINEAR_CASES = [
     (4, 5120, 5120, 128, "bf16", "two-kernel: o, four rows"),
     (1, 5120, 5120, 128, "bf16", "fused: o"),
     (2, 1024, 4096, 128, "bf16", "two-kernel: two rows"),
-    (1, 5120, 27648, 128, "f16", "two-kernel: down, one row (long K)"),
+    (1, 5120, 27648, 128, "f16", "fused: down, one row (long K, eight waves of 27 tiles)"),
     (1, 5120, 13824, 128, "f16", "fused: half of down's K (twelve waves)"),
     (2, 5120, 27648, 128, "f16", "two-kernel: down, two rows"),
     (1, 640, 4096, 64, "bf16", "fused: group stride 64"),

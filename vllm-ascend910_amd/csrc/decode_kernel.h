@@ -450,21 +450,32 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     const int nch = max(0, (k1 - k0) >> 3);
     uint4 xv[QR][QI];
     if constexpr (QF) {
+        // raw buffer loads, chunks outside the range reading zero: no
+        // per-lane branches, so the waits below can count the weight loads
+        // issued after these instead of draining everything
+        const auto rx = make_rsrc(p.X, static_cast<uint32_t>(((p.M - 1) * p.ldx + p.K) * 2));
 #pragma unroll
         for (int m = 0; m < QM; ++m)
 #pragma unroll
             for (int i = 0; i < QI; ++i) {
                 const int c = lane + 64 * i;
                 const bool ok = m < p.M && i < p.qcpr && c < nch;
-                xv[m][i] = ok ? *reinterpret_cast<const uint4*>(p.X + m * p.ldx + k0 + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+                xv[m][i] = buf_load16(rx, ok ? static_cast<uint32_t>((m * p.ldx + k0 + 8 * c) * 2) : kOOB);
             }
     }
     uint32_t ws1[CPW];   // ONE: the scale of each column block's columns of this lane
-    if (busy) {
+    // QF: issued by every wave (an idle wave's range is empty, so its loads
+    // read zeros through empty descriptors) -- under a branch the wait for
+    // the X rows below would also wait for the whole weight ring.
+    if (QF || busy) {
         if constexpr (STS) stage_issue(0);
 #pragma unroll
         for (int s = 0; s < D; ++s) load_slot(s, ta + s);
     }
+    // QF: every load above is issued before the quant's first use of X (left
+    // to itself the scheduler starts the absmax first and the ring waits for
+    // the rows to arrive)
+    if constexpr (QF) __builtin_amdgcn_sched_barrier(0);
     if constexpr (ONE) {
         const auto rs = make_rsrc(p.S, p.s_bytes);
 #pragma unroll

@@ -107,16 +107,13 @@ struct FusedPlan {
 
 bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f) {
     // One row only: each workgroup quantises the rows of its K range, so the
-    // quant work is repeated per column group.  (Measured on MI355X: one row
-    // saves 0.5-3 us per call over the quant kernel + GEMM pair on narrow N
-    // and ~2 us on gate_up's 1728 column groups; at 2-4 rows the
-    // per-workgroup quant costs more than the launch it saves.)
+    // quant work is repeated per column group.  Measured on MI355X against
+    // the quant kernel + GEMM pair (graph replays, cold weights): qkv 8.4
+    // against 8.6 us, o 7.8 against 7.9, gate_up 24.8-25.0 against 27.6,
+    // down_proj (long K, eight waves of 27 tiles) 18.5 against 18.7 -- and one
+    // launch fewer where the linear runs inside a captured graph.  The
+    // four-row variant of the same kernel lost 2 us on qkv and o at M=4.
     if (a.M != 1 || a.swiglu || a.partials || !geom::is_unpadded(a.K, a.group)) return false;
-    // Long K (>= 128 tiles) takes the two kernels: each wave's quant prologue
-    // (its bf16 rows, then a workgroup-wide absmax) outlasts the launch it
-    // saves against the staged GEMM (down_proj: 19.2 us fused, 14.8 + 3.5 us
-    // for the pair on MI355X).
-    if (geom::k_tiles(a.K, a.group) >= 128) return false;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx % 8 != 0) return false;
     const DecodeConfig c = decode_config(a.M, a.N, a.K, a.group);
     if (c.D != 4 || c.CPW != 2 || c.MT != 0 || c.WIDE) return false;
