@@ -52,6 +52,15 @@ __device__ __forceinline__ uint32_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint3
     return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
 }
 
+// One aligned dword.  Scale rings load the dword holding a lane's 16-bit
+// scale and shift it out at the fold: a ring of 16-bit loads makes the
+// compiler zero-extend (or copy) each loaded value on the loop latch, which
+// waits there for the loads just issued and drains the ring every unrolled
+// iteration.
+__device__ __forceinline__ uint32_t buf_load_u32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+}
+
 // bf16 bits -> fp32 (exact).
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
