@@ -88,6 +88,7 @@ struct PrefillParams {
     uint32_t a_bytes, w_bytes, s_bytes;
     bool vec_out;      // y 16-byte aligned with ldy % 8 == 0: 16-byte output stores
     int bm;            // tile rows: 128 or 64
+    bool cols;         // group stride 128 at 128 rows: 128 x 32 wave tiles (gemm_prefill_cols_kernel)
 };
 
 // K is walked in the padded group layout (kgeom.h): group g starts at g*gs,
@@ -505,12 +506,227 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 
 constexpr int kDW = 2;   // weight prefetch depth in K steps
 
+// Group stride 128 without the partial dump or the SwiGLU pairs: the same
+// 128 x 128 tile and K step, but each of the four waves owns all 128 rows and
+// one 32-column block (instead of 64 x 64).  Every weight is then loaded and
+// unpacked by one wave instead of two: half the weight loads, and the unpack
+// of each B operand serves four MFMAs instead of two (1.5 instead of 3 VALU
+// instructions per MFMA), for twice the A operand reads from LDS.  Row block
+// rb's fold runs during row block rb + 1's MFMAs (row block 3's during the next
+// step's row block 0), one MFMA to eight fold instructions.  Each output's
+// arithmetic is the 64 x 64 kernel's: outputs are bit-identical.
+template <bool SBF16>
+__global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const PrefillParams p) {
+    constexpr int kBM = 128, kThreads = 256;
+    constexpr int kABuf = kBM * 128;
+    constexpr int kABuf01 = abuf01_bytes<128, false>();
+    static_assert(kNA == kBM * 8 / kThreads, "four 16-byte A chunks per lane per step");
+    __shared__ __attribute__((aligned(16))) int8_t la0[kABuf01];
+    __shared__ __attribute__((aligned(16))) int8_t la1[kABuf01];
+    __shared__ __attribute__((aligned(16))) int8_t la2[kABuf];
+    __shared__ __attribute__((aligned(16))) int8_t la3[kABuf];
+    auto abuf = [&](int b) -> int8_t* { return b == 0 ? la0 : (b == 1 ? la1 : (b == 2 ? la2 : la3)); };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // the wave's 32-column block
+    int tile_m, tile_n;
+    {
+        const int nwg = static_cast<int>(gridDim.x);
+        const int bid = static_cast<int>(blockIdx.x);
+        const int xcd = bid & 7, q = nwg >> 3, r = nwg & 7;
+        const int lin = xcd * q + min(xcd, r) + (bid >> 3);
+        const int band = lin / (p.band * p.tiles_n);
+        const int inband = lin - band * p.band * p.tiles_n;
+        const int rows = min(p.band, p.tiles_m - band * p.band);
+        tile_m = band * p.band + inband % rows;
+        tile_n = inband / rows;
+    }
+    const int m0 = tile_m * kBM;
+    const int n0 = tile_n * kBN;
+    const int c32 = lane & 31;
+    const int hh = lane >> 5;
+
+    const auto ra_rsrc = make_rsrc(p.A, p.a_bytes);
+    const auto rw_rsrc = make_rsrc(p.W, p.w_bytes);
+    const auto rs_rsrc = make_rsrc(p.S, p.s_bytes);
+
+    __shared__ uint32_t tsl[kBM];
+    uint32_t ts_bits = 0;
+    if (tid < kBM && m0 + tid < p.M) ts_bits = p.a_scale[m0 + tid];
+
+    // weights: this lane's two 16-byte chunks per step of the wave's block
+    const int col = n0 + wave * 32 + c32;
+    const uint32_t tile0 = static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u;
+    const uint32_t woff0 = tile0 + static_cast<uint32_t>((col & 15) + 16 * hh) * 16u;        // slabs 0, 2
+    const uint32_t woff1 = tile0 + static_cast<uint32_t>((col & 15) + 16 * (2 + hh)) * 16u;  // slabs 1, 3
+    const uint32_t soff = (static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.NG) * 16u + (col & 15)) * 2u;
+
+    // activations: as in gemm_prefill_kernel (wave w stages tile rows 32 w..+32)
+    uint32_t aoffg[kNA];
+#pragma unroll
+    for (int i = 0; i < kNA; ++i) {
+        const int r = 8 * (kNA * wave + i) + (lane >> 3);
+        const int q = (lane & 7) ^ a_swz(r);
+        aoffg[i] = static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(p.lda) + static_cast<uint32_t>(q) * 16u;
+    }
+    auto load_a = [&](int kt, int b) {
+        const uint32_t k = static_cast<uint32_t>(min(kt, p.KT - 1)) * 128u;
+        int8_t* const dst = abuf(b) + kNA * 1024 * wave;
+#pragma unroll
+        for (int i = 0; i < kNA; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_rsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * i),
+                                                     16, aoffg[i] + k, 0, 0, 0);
+    };
+    uint4 wr[kDW][2];
+    auto load_w = [&](int slot, int kt) {
+        const uint32_t t = static_cast<uint32_t>(min(kt, p.KT - 1)) * 1024u;
+        wr[slot][0] = buf_load16(rw_rsrc, woff0 + t);
+        wr[slot][1] = buf_load16(rw_rsrc, woff1 + t);
+    };
+    // group stride 128: step kt is group kt (the padding half of a last step
+    // meets zero weights)
+    auto load_s = [&](int kt) -> uint32_t {
+        const int g = min(min(kt, p.KT - 1), p.NG - 1);
+        return buf_load_u16(rs_rsrc, soff + static_cast<uint32_t>(g) * 32u);
+    };
+
+    v16i P[4];
+    float acc[4][16];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            P[rb][i] = 0;
+            acc[rb][i] = 0.0f;
+        }
+    const v16i zero16 = {};
+    auto fold = [&](int rb, uint32_t wsb) __attribute__((always_inline)) {
+        const float ws = scale_to_f32<SBF16>(wsb);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[rb][i] += static_cast<float>(P[rb][i]) * ws;
+    };
+
+    // ---- prologue (the issue order the first wait counts on)
+    load_a(0, 0);
+    load_a(1, 1);
+    load_a(2, 2);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < kDW; ++s) load_w(s, s);
+    uint32_t sc = load_s(0);
+    asm volatile("" ::: "memory");
+    uint32_t scp = 0u;   // the previous step's scale (row block 3 folds one step late)
+    if (tid < kBM) tsl[tid] = ts_bits;
+    wait_vm_barrier<2 * kNA + kDW * 2 + 1>();
+
+    uint32_t aread[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) aread[s] = static_cast<uint32_t>(c32 * 128 + (((2 * s + hh) ^ a_swz(c32)) * 16));
+
+    auto step = [&](int kt, int u, int buf) __attribute__((always_inline)) {
+        load_a(kt + 3, (buf + 3) % kNB);
+        const uint32_t scn = load_s(kt + 1);
+        const int8_t* ab = abuf(buf);
+        auto lds_a = [&](int rb, int s) { return *reinterpret_cast<const v4i*>(ab + aread[s] + rb * 4096); };
+        v4i av[2][4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) av[0][s] = lds_a(0, s);
+        __builtin_amdgcn_sched_barrier(0);
+        v4i bvs[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint4 w = wr[u][s & 1];
+            const uint32_t d0 = (s >> 1) ? w.z : w.x;
+            const uint32_t d1 = (s >> 1) ? w.w : w.y;
+            bvs[s] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
+        }
+        load_w(u, kt + kDW);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            if (rb < 3) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) av[(rb + 1) & 1][s] = lds_a(rb + 1, s);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s) P[rb] = mfma32(av[rb & 1][s], bvs[s], s == 0 ? zero16 : P[rb]);
+            if (rb == 0) fold(3, scp);
+            else fold(rb - 1, sc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);   // eight VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        scp = sc;
+        sc = scn;
+    };
+    // a step issues kNA + 3 vector memory operations; the wait keeps the two
+    // newest steps' in flight (A(kt + 1), issued in step kt - 2, has landed)
+    auto one = [&](int kt, int u) __attribute__((always_inline)) {
+        step(kt, u % kDW, u % kNB);
+        wait_vm_barrier<2 * (kNA + 3)>();
+    };
+    int kt = 0;
+    for (; kt + kNB <= p.KT; kt += kNB) {
+#pragma unroll
+        for (int u = 0; u < kNB; ++u) one(kt + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < kNB - 1; ++u)
+        if (kt + u < p.KT) one(kt + u, u);
+    fold(3, scp);   // the last step's row block 3
+
+    // ---- epilogue: as in gemm_prefill_kernel, through the first two A buffers
+    constexpr int OC = kBN;
+    constexpr int OS = out_stride<128, false>();
+    constexpr int RPA = kBM / 2;
+    wait_vm_barrier<0>();
+    auto orow = [&](int r) -> uint16_t* {
+        return reinterpret_cast<uint16_t*>(r < RPA ? la0 : la1) + (r % RPA) * OS;
+    };
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
+            const float ts = bf16_bits_to_f32(tsl[r]) * 0.0625f;
+            orow(r)[wave * 32 + c32] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][i] * ts));
+        }
+    __syncthreads();
+    constexpr int CPR = OC / 8;
+#pragma unroll
+    for (int k = 0; k < kBM * CPR / kThreads; ++k) {
+        const int c = tid + k * kThreads;
+        const int r = c / CPR, c8 = (c % CPR) * 8;
+        const int row = m0 + r, cc = n0 + c8;
+        if (row >= p.M || cc >= p.N) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(orow(r) + c8);
+        uint16_t* y = p.Y + static_cast<int64_t>(row) * p.ldy + cc;
+        if (p.vec_out && cc + 8 <= p.N) {
+            *reinterpret_cast<uint4*>(y) = v;
+        } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (cc + q < p.N) y[q] = static_cast<uint16_t>(w[q >> 1] >> (16 * (q & 1)));
+        }
+    }
+}
+
 template <int GMODE, bool SBF16, bool DUMP, bool SWIGLU>
 hipError_t launch_g(const PrefillParams& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
     // The partial dump keeps 128-row tiles (the compiler fails on the 64-row
     // dump variants); each output element's arithmetic does not depend on the
     // tile height, so its outputs equal the 64-row kernel's bit for bit.
+    if constexpr (GMODE == 1 && !DUMP && !SWIGLU) {
+        if (p.bm == 128 && p.cols) {
+            gemm_prefill_cols_kernel<SBF16><<<grid, dim3(256), 0, stream>>>(p);
+            return hipGetLastError();
+        }
+    }
     if (p.bm == 64 && !DUMP)
         gemm_prefill_kernel<GMODE, kDW, SBF16, false, SWIGLU, 64><<<grid, dim3(threads_for<64>()), 0, stream>>>(p);
     else
@@ -527,6 +743,12 @@ hipError_t launch(const PrefillParams& p, hipStream_t stream) {
 }
 
 }  // namespace
+
+// The 128 x 32 wave tiles for group stride 128 (defined 0 only for
+// side-by-side measurements of the 64 x 64 kernel).
+#ifndef W4A8_PREFILL_COLS
+#define W4A8_PREFILL_COLS 1
+#endif
 
 int64_t prefill_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
 
@@ -578,6 +800,7 @@ hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream)
     p.w_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::k_tiles(a.K, a.group) * geom::kTileBytes);
     p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
     p.vec_out = (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (a.ldy % 8 == 0);
+    p.cols = W4A8_PREFILL_COLS != 0;
     if (a.swiglu) return a.scale_bf16 ? launch<true, false, true>(p, stream) : launch<false, false, true>(p, stream);
     const bool dump = a.partials != nullptr;
     if (a.scale_bf16) return dump ? launch<true, true, false>(p, stream) : launch<true, false, false>(p, stream);
