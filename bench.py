@@ -101,7 +101,7 @@ def main():
                          "and their time, as markdown, and exit")
     ap.add_argument("--prefill-pmc-summary", nargs="+", metavar="DB",
                     help="summarize rocprofv3 databases of a --prefill-probe run (counter passes, then a "
-                         "--kernel-trace database last) for gemm_prefill_kernel as markdown and exit")
+                         "--kernel-trace database last) for the prefill GEMM kernels as markdown and exit")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
@@ -414,7 +414,8 @@ def main():
         us_tot = sum(r["gemm_us"] for r in at)
         ach = ops / us_tot / 1e6
         result["roofline_prefill"] = {
-            "kernel": f"gemm_prefill_kernel, the four configs[2] projections at M={at[0]['M']}, group 128 "
+            "kernel": f"gemm_prefill_cols_kernel (128 x 32 wave tiles), the four configs[2] projections at "
+                      f"M={at[0]['M']}, group 128 "
                       f"(algorithmic ops 2*M*N*K per call over the summed call times)",
             "bound": "mfma", "achieved": round(ach, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
             "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": None,
@@ -801,7 +802,8 @@ def prefill_probe(pkg, dev, M, calls=3):
 
 
 def prefill_pmc_summary(dbs):
-    """Counter table of gemm_prefill_kernel from --prefill-probe runs: counter databases
+    """Counter table of the prefill GEMM (gemm_prefill_kernel or gemm_prefill_cols_kernel) from
+    --prefill-probe runs: counter databases
     (one pass each) and a --kernel-trace database (the last argument) for durations."""
     import collections
     import sqlite3
@@ -810,7 +812,9 @@ def prefill_pmc_summary(dbs):
     synth = ge.package().synth
     rows = sqlite3.connect(trace_db).execute(
         "select name, duration, grid_x from kernels order by start").fetchall()
-    gemms = [(d, gx) for n, d, gx in rows if "gemm_prefill_kernel" in n]
+    is_gemm = lambda n: "gemm_prefill_kernel" in n or "gemm_prefill_cols_kernel" in n  # noqa: E731
+    gemms = [(d, gx) for n, d, gx in rows if is_gemm(n)]
+    kname = sorted({n.split("<")[0].split("::")[-1] for n, _, _ in rows if is_gemm(n)})
     per = max(1, len(gemms) // len(PROJS))
     # the probe's order: each projection's calls in turn (PROJS order); M from
     # the first projection's grid (128 x 128 tiles of 256 threads)
@@ -826,7 +830,7 @@ def prefill_pmc_summary(dbs):
         ev = con.execute("select dispatch_id, name, counter_name, counter_value from pmc_events "
                          "order by dispatch_id").fetchall()
         # the probe's dispatch order: each projection's GEMM calls in turn (PROJS order)
-        gemm_ids = sorted({did for did, name, _, _ in ev if "gemm_prefill_kernel" in name})
+        gemm_ids = sorted({did for did, name, _, _ in ev if is_gemm(name)})
         per = max(1, len(gemm_ids) // len(PROJS))
         which = {did: PROJS[min(i // per, len(PROJS) - 1)] for i, did in enumerate(gemm_ids)}
         for did, name, cname, val in ev:
@@ -835,7 +839,7 @@ def prefill_pmc_summary(dbs):
             elif did in which:
                 ctr[which[did]][cname].append(val)
     avg = lambda v: sum(v) / len(v) if v else float("nan")  # noqa: E731
-    print(f"gemm_prefill_kernel at M={M}, group 128: per-dispatch counter averages (each counter from its own "
+    print(f"{' / '.join(kname)} at M={M}, group 128: per-dispatch counter averages (each counter from its own "
           f"pass; the duration from the kernel-trace run).\n")
     print("Commands (run from /tmp with TMPDIR=/tmp; REPO is the repository root; one database per run):\n")
     for i, db in enumerate(pmc_dbs):
