@@ -52,18 +52,6 @@ __device__ __forceinline__ uint32_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint3
     return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
 }
 
-// 16 bytes per lane from a buffer straight into LDS, non-temporal (gfx950):
-// lane l's bytes land at lds + 16 l (lds wave-uniform).  A plain device
-// function: the builtin called directly in a kernel template leaves that
-// kernel's host launch stub undefined.
-__device__ __forceinline__ void buf_load16_lds_nt(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 2);
-}
-// 4 bytes per lane from a buffer straight into LDS: lane l's dword lands at lds + 4 l.
-__device__ __forceinline__ void buf_load4_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, off, 0, 0, 0);
-}
-
 // One aligned dword.  Scale rings load the dword holding a lane's 16-bit
 // scale and shift it out at the fold: a ring of 16-bit loads makes the
 // compiler zero-extend (or copy) each loaded value on the loop latch, which

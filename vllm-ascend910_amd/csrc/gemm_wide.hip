@@ -11,8 +11,7 @@
 // share each activation tile (16 * kMT rows x 128 K), staged once into LDS
 // (double-buffered, one barrier per tile) and read from there as MFMA
 // operands.  The staging loads run kRA tiles ahead in registers and the
-// weights stream straight to registers in a kD-deep ring, or (kLW > 0) into
-// a kLW-deep ring of per-wave LDS slots by buffer loads to LDS.
+// weights stream straight to registers in a kD-deep ring.
 //
 // A workgroup walks one K range of a group-aligned split (blockIdx.y).  With
 // one split it writes bf16 directly and the accumulation order per output is
@@ -54,9 +53,6 @@ struct WideParams {
     uint32_t a_bytes, w_bytes, s_bytes;
 };
 
-constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
-constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
-
 // f(integral_constant<int, J>) for J = B .. E-1, in order.
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -71,11 +67,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Mode 4 folds once after the K loop; with K split over workgroups it writes
 // the int32 sums instead, which wide_reduce_kernel adds exactly and folds.
 // kMT 16-row tiles, kWN column waves, kCPW 16-column blocks per wave, kD
-// weight ring depth, kRA activation tiles in flight.  kLW > 0: the weight
-// ring lives in LDS instead, kLW tiles deep (buffer loads straight to LDS,
-// one 1 KB slot per column block and wave; each lane reads back the 16 bytes
-// it loaded): the weight bytes in flight per wave no longer cost registers.
-template <int kMT, int kWN, int kCPW, int kD, int kRA, int GM, bool SBF16, bool DUMP, bool SWIGLU, int kLW = 0>
+// weight ring depth, kRA activation tiles in flight.
+template <int kMT, int kWN, int kCPW, int kD, int kRA, int GM, bool SBF16, bool DUMP, bool SWIGLU>
 __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p) {
     static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
     constexpr int CG = SWIGLU ? kCPW / 2 : kCPW;   // output column blocks per wave
@@ -86,16 +79,13 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     // 40.3 -> 39.5, down M=64 31.9 -> 30.6; 16 rows lose ~0.4 us with it).
     // A ring of 16-bit loads makes the compiler zero-extend each loaded
     // value on the loop latch, a copy that waits for the loads just issued.
-    constexpr bool kDW = kMT >= 2 && !ONE && kLW == 0;
-    constexpr bool kSD = kDW || (kLW > 0 && !ONE);   // scales addressed as dwords
-    constexpr int kR = kLW > 0 ? kLW : kD;   // weight (and scale) ring depth
+    constexpr bool kDW = kMT >= 2 && !ONE;
     // Unroll: every ring slot index is static; with kDW a slot's scale lives
     // in two registers in turn (the next load is issued before the last one
     // is used), so a multiple of 2 kD steps needs no copy on the loop latch.
-    constexpr int kDU = kDW ? 2 * kR : kR;
-    constexpr int U = lcm_c(lcm_c(kDU, kRA), 2);
-    static_assert(U % kR == 0 && U % kRA == 0 && U % 2 == 0, "ring depths must divide the unroll");
-    static_assert(kLW <= 8, "at most eight LDS weight slots");
+    constexpr int kDU = kDW ? 2 * kD : kD;
+    constexpr int U = kDU > kRA ? kDU : kRA;
+    static_assert(U % kD == 0 && U % kRA == 0 && U % 2 == 0, "ring depths must divide the unroll");
     constexpr int kATile = 16 * kMT * kALS;
     // two staged activation tiles
     __shared__ __attribute__((aligned(16))) int8_t la[2][kATile];
@@ -127,12 +117,12 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     const int nit = tb - ta;
 
     uint32_t wo[kCPW], so[kCPW];
-    const uint32_t ssh = kSD ? (colq & 1) * 16u : 0u;   // column colq's half of a scale dword
+    const uint32_t ssh = kDW ? (colq & 1) * 16u : 0u;   // column colq's half of a scale dword
 #pragma unroll
     for (int c = 0; c < kCPW; ++c) {
         const uint32_t nb = static_cast<uint32_t>(min(block_of(c), p.NB - 1));
         wo[c] = nb * static_cast<uint32_t>(p.KT) * 1024u + lane * 16u;
-        so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + (kSD ? (colq & ~1) : colq)) * 2u;
+        so[c] = (nb * static_cast<uint32_t>(p.NG) * 16u + (kDW ? (colq & ~1) : colq)) * 2u;
     }
     // Staging: 16 * kMT rows x 128 K = 128 * kMT units of 16 bytes, NU per
     // lane; rows past M read zero.  With fewer units than lanes (one row
@@ -174,56 +164,18 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
         for (int j = 0; j < NU; ++j) *reinterpret_cast<uint4*>(&la[buf][sl[j]]) = r[j];
     };
 
-    // LDS ring slots (unused ones take 16 bytes): per wave and column block
-    // the 1 KB weight tile, then (one group per K: none) the scale dwords,
-    // 256 bytes per block and scale of the tile, each lane's dword at lane*4.
-    constexpr int kSlotW = kWN * kCPW * 1024;
-    constexpr int kSlot = kSlotW + (ONE ? 0 : kWN * kCPW * NS * 256);
-    __shared__ __attribute__((aligned(16))) int8_t lw0[kLW > 0 ? kSlot : 16];
-    __shared__ __attribute__((aligned(16))) int8_t lw1[kLW > 1 ? kSlot : 16];
-    __shared__ __attribute__((aligned(16))) int8_t lw2[kLW > 2 ? kSlot : 16];
-    __shared__ __attribute__((aligned(16))) int8_t lw3[kLW > 3 ? kSlot : 16];
-    __shared__ __attribute__((aligned(16))) int8_t lw4[kLW > 4 ? kSlot : 16];
-    __shared__ __attribute__((aligned(16))) int8_t lw5[kLW > 5 ? kSlot : 16];
-    __shared__ __attribute__((aligned(16))) int8_t lw6[kLW > 6 ? kSlot : 16];
-    __shared__ __attribute__((aligned(16))) int8_t lw7[kLW > 7 ? kSlot : 16];
-    // this wave's 1 KB area of block c in slot s (s a compile-time index after unrolling)
-    auto slot_base = [&](int s) -> int8_t* {
-        return s == 0 ? lw0 : s == 1 ? lw1 : s == 2 ? lw2 : s == 3 ? lw3 : s == 4 ? lw4 : s == 5 ? lw5 : s == 6 ? lw6 : lw7;
-    };
-    auto wslot = [&](int s, int c) -> int8_t* { return slot_base(s) + (wn * kCPW + c) * 1024; };
-    auto sslot = [&](int s, int c, int j) -> int8_t* { return slot_base(s) + kSlotW + ((wn * kCPW + c) * NS + j) * 256; };
-    // Loads issued after a slot's last load by the time its tile is read:
-    // the kR - 1 later slots' weights and scales, plus the activation
-    // staging loads in flight (only when every wave stages; a wave that
-    // stages fewer waits a little longer than it needs).  The prologue
-    // issues the same or more.
-    constexpr int kNSE = ONE ? 0 : NS;
-    constexpr int kWaitN = (kR - 1) * kCPW * (1 + kNSE) + (kUnits >= 64 * kWN ? (kR < kRA ? kR : kRA) * NU : 0);
-    static_assert(kLW == 0 || kWaitN <= 63, "vmcnt holds 0..63");
-
-    uint4 wb[kLW > 0 ? 1 : kD][kCPW];
-    uint32_t sb[kLW > 0 ? 1 : kD][kCPW][NS];
+    uint4 wb[kD][kCPW];
+    uint32_t sb[kD][kCPW][NS];
     auto load_slot = [&](int s, int t) {
         const auto rw = make_rsrc_at(p.W, static_cast<uint32_t>(min(t, p.KT - 1)) * 1024u, t < tb ? p.w_bytes : 0u);
 #pragma unroll
-        for (int c = 0; c < kCPW; ++c) {
-            if constexpr (kLW > 0)
-                buf_load16_lds_nt(rw, wslot(s, c), wo[c]);
-            else
-                wb[s][c] = buf_load16_nt(rw, wo[c]);
-        }
+        for (int c = 0; c < kCPW; ++c) wb[s][c] = buf_load16_nt(rw, wo[c]);
         if constexpr (ONE) return;   // the one scale per column is loaded once
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             const auto rs = make_rsrc_at(p.S, static_cast<uint32_t>(gend(min(t, p.KT - 1), j)) * 32u, p.s_bytes);
 #pragma unroll
-            for (int c = 0; c < kCPW; ++c) {
-                if constexpr (kLW > 0)
-                    buf_load4_lds(rs, sslot(s, c, j), so[c]);
-                else
-                    sb[s][c][j] = kDW ? buf_load_u32(rs, so[c]) : buf_load_u16(rs, so[c]);
-            }
+            for (int c = 0; c < kCPW; ++c) sb[s][c][j] = kDW ? buf_load_u32(rs, so[c]) : buf_load_u16(rs, so[c]);
         }
     };
 
@@ -264,7 +216,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     // the weight ring filled, tile ta staged in buffer 0
     stage_load(ta, ra[0]);
 #pragma unroll
-    for (int s = 0; s < kR; ++s) load_slot(s, ta + s);
+    for (int s = 0; s < kD; ++s) load_slot(s, ta + s);
     uint32_t ws1[kCPW];   // ONE: this lane's column scale per column block
     if constexpr (ONE) {
         const auto rs = make_rsrc(p.S, p.s_bytes);
@@ -279,35 +231,19 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
     // One tile t = ta + i; J = i mod U names the ring slots and the LDS buffer.
     auto step = [&](int i, auto jc) __attribute__((always_inline)) {
         constexpr int J = decltype(jc)::value;
-        constexpr int WS = J % kR;
+        constexpr int WS = J % kD;
         const int t = ta + i;
         // the staging slot of tile t is free again (tile t is in LDS)
         stage_load(t + kRA, ra[J % kRA]);
-        // (the partial dump's stores count in vmcnt too and need not complete
-        // in order with the loads: that debug path waits for everything)
-        if constexpr (kLW > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DUMP ? 0 : kWaitN) : "memory");
         uint32_t raw[kCPW][NS];
 #pragma unroll
         for (int c = 0; c < kCPW; ++c)
 #pragma unroll
-            for (int q = 0; q < NS; ++q) {
-                if constexpr (ONE) raw[c][q] = 0;
-                else if constexpr (kLW > 0) raw[c][q] = *reinterpret_cast<const uint32_t*>(sslot(WS, c, q) + lane * 4);
-                else raw[c][q] = sb[WS][c][q];
-            }
+            for (int q = 0; q < NS; ++q) raw[c][q] = sb[WS][c][q];
         v4i b[kCPW][2];
 #pragma unroll
-        for (int c = 0; c < kCPW; ++c) {
-            if constexpr (kLW > 0) {
-                const uint4 w = *reinterpret_cast<const uint4*>(wslot(WS, c) + lane * 16);
-                unpack_tile_lane(w, b[c][0], b[c][1]);
-            } else {
-                unpack_tile_lane(wb[WS][c], b[c][0], b[c][1]);
-            }
-        }
-        // the slot's reads complete before its refill is issued
-        if constexpr (kLW > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        load_slot(WS, t + kR);
+        for (int c = 0; c < kCPW; ++c) unpack_tile_lane(wb[WS][c], b[c][0], b[c][1]);
+        load_slot(WS, t + kD);
         // With kDW the slot's scales are converted here, once the slot's
         // next loads are issued.  The empty asm statements pin the
         // conversion: left to itself the compiler sinks it to the fold, which
@@ -321,9 +257,9 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
 #pragma unroll
             for (int q = 0; q < NS; ++q) {
                 if constexpr (ONE) continue;
-                if constexpr (kSD) asm volatile("" : "+v"(raw[c][q]));
+                if constexpr (kDW) asm volatile("" : "+v"(raw[c][q]));
                 sc[c][q] = scale_to_f32<SBF16>(raw[c][q] >> ssh);
-                if constexpr (kSD) asm volatile("" : "+v"(sc[c][q]));
+                if constexpr (kDW) asm volatile("" : "+v"(sc[c][q]));
             }
         // Every A operand of the tile read from LDS before the first MFMA
         // (left to itself the compiler reads the second half one operand at
@@ -358,15 +294,7 @@ __global__ __launch_bounds__(64 * kWN) void gemm_wide_kernel(const WideParams p)
         }
         // tile t+1 into the other buffer (free: every wave finished tile t-1)
         stage_store((J + 1) & 1, ra[(J + 1) % kRA]);
-        if constexpr (kLW > 0) {
-            // LDS writes done, then the barrier: __syncthreads' fence would
-            // also wait for every load into LDS, i.e. drain the weight ring
-            // (each wave reads only its own slots; the compiler waits for a
-            // slot's loads before reading it)
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        } else {
-            __syncthreads();
-        }
+        __syncthreads();
     };
     int i = 0;
     for (; i + U <= nit; i += U) static_for<0, U>([&](auto jc) { step(i + decltype(jc)::value, jc); });
@@ -512,22 +440,22 @@ int gcd_w(int a, int b) {
     return a;
 }
 
-template <int kMT, int kCPW, int kD, int kRA, int GM, bool DUMP, bool SWIGLU, int kLW>
+template <int kMT, int kCPW, int kD, int kRA, int GM, bool DUMP, bool SWIGLU>
 hipError_t launch_g(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(cgroups), static_cast<unsigned>(p.splits)), block(64 * kWaves);
-    if (sbf16) gemm_wide_kernel<kMT, kWaves, kCPW, kD, kRA, GM, true, DUMP, SWIGLU, kLW><<<grid, block, 0, s>>>(p);
-    else gemm_wide_kernel<kMT, kWaves, kCPW, kD, kRA, GM, false, DUMP, SWIGLU, kLW><<<grid, block, 0, s>>>(p);
+    if (sbf16) gemm_wide_kernel<kMT, kWaves, kCPW, kD, kRA, GM, true, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
+    else gemm_wide_kernel<kMT, kWaves, kCPW, kD, kRA, GM, false, DUMP, SWIGLU><<<grid, block, 0, s>>>(p);
     return hipGetLastError();
 }
 
-template <int kMT, int kCPW, int kD, int kRA, bool DUMP, bool SWIGLU, int kLW>
+template <int kMT, int kCPW, int kD, int kRA, bool DUMP, bool SWIGLU>
 hipError_t launch_gm(const WideParams& p, int cgroups, bool sbf16, hipStream_t s) {
     switch (group_mode_of(p.spg, p.NG)) {
-        case 4: return launch_g<kMT, kCPW, kD, kRA, 4, DUMP, SWIGLU, kLW>(p, cgroups, sbf16, s);
-        case 0: return launch_g<kMT, kCPW, kD, kRA, 0, DUMP, SWIGLU, kLW>(p, cgroups, sbf16, s);
-        case 1: return launch_g<kMT, kCPW, kD, kRA, 1, DUMP, SWIGLU, kLW>(p, cgroups, sbf16, s);
-        case 3: return launch_g<kMT, kCPW, kD, kRA, 3, DUMP, SWIGLU, kLW>(p, cgroups, sbf16, s);
-        default: return launch_g<kMT, kCPW, kD, kRA, 2, DUMP, SWIGLU, kLW>(p, cgroups, sbf16, s);
+        case 4: return launch_g<kMT, kCPW, kD, kRA, 4, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 0: return launch_g<kMT, kCPW, kD, kRA, 0, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 1: return launch_g<kMT, kCPW, kD, kRA, 1, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        case 3: return launch_g<kMT, kCPW, kD, kRA, 3, DUMP, SWIGLU>(p, cgroups, sbf16, s);
+        default: return launch_g<kMT, kCPW, kD, kRA, 2, DUMP, SWIGLU>(p, cgroups, sbf16, s);
     }
 }
 
@@ -570,7 +498,7 @@ int64_t split_bytes(const WideParams& p) {
 
 // One call with an explicit layout: kMT row tiles, kCPW column blocks per
 // wave, ring depths kD / kRA, p.splits workgroups along K.
-template <int kMT, int kCPW, int kD, int kRA, int kLW = 0>
+template <int kMT, int kCPW, int kD, int kRA>
 hipError_t launch_wide_v(const GemmArgs& a, WideParams p, hipStream_t stream) {
     if (a.M <= 0 || a.M > 16 * kMT) return hipErrorInvalidValue;
     if (a.swiglu && kCPW % 2 != 0) return hipErrorInvalidValue;
@@ -584,10 +512,10 @@ hipError_t launch_wide_v(const GemmArgs& a, WideParams p, hipStream_t stream) {
     const int c = static_cast<int>(cg);
     hipError_t e;
     if (a.swiglu) {
-        if constexpr (kCPW % 2 == 0) e = launch_gm<kMT, kCPW, kD, kRA, false, true, kLW>(p, c, a.scale_bf16, stream);
+        if constexpr (kCPW % 2 == 0) e = launch_gm<kMT, kCPW, kD, kRA, false, true>(p, c, a.scale_bf16, stream);
         else return hipErrorInvalidValue;
-    } else if (a.partials) e = launch_gm<kMT, kCPW, kD, kRA, true, false, kLW>(p, c, a.scale_bf16, stream);
-    else e = launch_gm<kMT, kCPW, kD, kRA, false, false, kLW>(p, c, a.scale_bf16, stream);
+    } else if (a.partials) e = launch_gm<kMT, kCPW, kD, kRA, true, false>(p, c, a.scale_bf16, stream);
+    else e = launch_gm<kMT, kCPW, kD, kRA, false, false>(p, c, a.scale_bf16, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     return launch_split_reduce(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N, p.splits, p.NG == 1, a.scale_bf16, p.S,
                                p.P, stream);
@@ -616,11 +544,7 @@ hipError_t launch_split_reduce(const float* R, int64_t ldr, const uint16_t* a_sc
 hipError_t launch_gemm_wide(const GemmArgs& a, int layout, int splits, hipStream_t stream) {
     const WideParams p = make_wide_params(a, splits);
     switch (layout) {
-        // 9-16 rows on wide N: the weight ring in LDS, four tiles deep (gate_up
-        // M=16 30.5 -> 28.8 us, bit-identical; the other layouts measured no
-        // faster with it, down_proj at 16-64 rows and gate_up at 32-64 rows
-        // within +-1 us or slower)
-        case kWide1x2: return launch_wide_v<1, 2, 2, 4, 4>(a, p, stream);
+        case kWide1x2: return launch_wide_v<1, 2, 2, 4>(a, p, stream);
         case kWide2x2: return launch_wide_v<2, 2, 2, 2>(a, p, stream);
         case kWide4x2: return launch_wide_v<4, 2, 2, 4>(a, p, stream);
         case kWide1x1: return launch_wide_v<1, 1, 4, 4>(a, p, stream);
