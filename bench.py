@@ -292,6 +292,7 @@ def main():
 
     shapes = []
     floors = {}
+    reads = {}
     copy_dst = {}
     tot_bytes = tot_us = 0.0
     for M in DECODE_MS:
@@ -321,10 +322,18 @@ def main():
                 for i in range(T):
                     copy_dst[p].copy_(weights[p][i % len(weights[p])][0])
 
+            def stock_reads(p=p):
+                # the same pool rotation read by a stock torch reduction (amax over the
+                # weight tiles as int32): what stock code reads at each weight size
+                for i in range(T):
+                    torch.amax(weights[p][i % len(weights[p])][0].view(torch.int32))
+
             us = time_graph(gemms) / T
             qus = time_graph(quants) / T
             fus = time_graph(floor_reads) / T if M == DECODE_MS[0] else floors[p]
             floors[p] = fus
+            rus = time_graph(stock_reads) / T if M == DECODE_MS[0] else reads[p]
+            reads[p] = rus
             # quant + GEMM through w4a8_linear, on the step's stream
             lus = time_graph(linears, stream=torch.cuda.current_stream(dev)) / T
             x0 = xs[(M, p)]
@@ -336,11 +345,11 @@ def main():
                            "gemm_GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                            "TOPS": round(2 * M * N * K / us / 1e6, 2), "quant_us": round(qus, 3),
                            "linear_us": round(lus, 3), "linear_fused": fused,
-                           "copy_us": round(fus, 3)})
+                           "copy_us": round(fus, 3), "stock_read_us": round(rus, 3)})
             cgb = 2 * weights[p][0][0].numel() / fus / 1e3
             log(f"  {p:13s} M={M:3d}: gemm {us:8.2f} us {b / us / 1e3:7.1f} GB/s ({b / us / 1e3 / HBM_PEAK_GBS:.1%})"
                 f"  quant {qus:6.2f} us  linear {lus:7.2f} us{' (fused)' if fused else ''}  "
-                f"copy {fus:6.2f} us ({cgb:6.0f} GB/s)")
+                f"copy {fus:6.2f} us ({cgb:6.0f} GB/s)  read {rus:6.2f} us")
     achieved = tot_bytes / tot_us / 1e3
     # HBM bytes per launch from the two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) recorded in
     # profiles/ (the command is in the summary), each scaled by a 256 MiB copy's reading.
@@ -364,6 +373,12 @@ def main():
                  "the GEMMs: what stock code moves at each weight size, cold reads plus writes"),
         "us": {p: round(floors[p], 3) for p in PROJS},
         "GBs_read_plus_write": {p: round(2 * weights[p][0][0].numel() / floors[p] / 1e3, 1) for p in PROJS}}
+    result["stock_read"] = {
+        "what": ("per projection, a stock torch reduction (torch.amax over the int32 view) of each pool copy's "
+                 "repacked weight tiles, graph-replayed back to back over the same rotation as the GEMMs: how "
+                 "fast stock code reads the weight bytes alone, cold"),
+        "us": {p: round(reads[p], 3) for p in PROJS},
+        "GBs": {p: round(weights[p][0][0].numel() / reads[p] / 1e3, 1) for p in PROJS}}
     result["gpu_clocks"] = {"after_timed_region": clocks,
                             "note": "rocm-smi reading; the peaks above are MI355X's published figures (2.4 GHz)"}
 

@@ -79,6 +79,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     return u >> 16;
 }
 
+// Two fp32 -> two bf16 (low half: a), round to nearest even, in one
+// v_cvt_pk_bf16_f32: on MI355X it equals f32_to_bf16_bits for every fp32
+// input (checked on 2^24 bit patterns including ties, subnormals, infinities
+// and NaN).
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
 // SwiGLU of one gate/up output pair, rounded the way torch evaluates
 // `F.silu(g) * u` on bf16 tensors (the reference's decoder layer,
 // npu_ops/python/bench_decode_layer.py:78-81): g and u are first rounded to the

@@ -551,7 +551,9 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
     const auto rw_rsrc = make_rsrc(p.W, p.w_bytes);
     const auto rs_rsrc = make_rsrc(p.S, p.s_bytes);
 
-    __shared__ uint32_t tsl[kBM];
+    // token scales of the tile's rows, times the 1/16 of the unpack (exact),
+    // as fp32 in LDS for the epilogue's 16-byte reads of four rows
+    __shared__ __attribute__((aligned(16))) float tsl[kBM];
     uint32_t ts_bits = 0;
     if (tid < kBM && m0 + tid < p.M) ts_bits = p.a_scale[m0 + tid];
 
@@ -617,7 +619,7 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
     uint32_t sc = load_s(0);
     asm volatile("" ::: "memory");
     uint32_t scp = 0u;   // the previous step's scale (row block 3 folds one step late)
-    if (tid < kBM) tsl[tid] = ts_bits;
+    if (tid < kBM) tsl[tid] = bf16_bits_to_f32(ts_bits) * 0.0625f;
     wait_vm_barrier<2 * kNA + kDW * 2 + 1>();
 
     uint32_t aread[4];
@@ -689,10 +691,16 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
-            const float ts = bf16_bits_to_f32(tsl[r]) * 0.0625f;
-            orow(r)[wave * 32 + c32] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rb][i] * ts));
+        for (int q = 0; q < 4; ++q) {
+            const int r0 = rb * 32 + q * 8 + hh * 4;   // this lane's four rows r0..r0+3
+            const float4 ts = *reinterpret_cast<const float4*>(&tsl[r0]);
+            const float tv[4] = {ts.x, ts.y, ts.z, ts.w};
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+                const uint32_t v = f32x2_to_bf16x2_bits(acc[rb][q * 4 + j] * tv[j], acc[rb][q * 4 + j + 1] * tv[j + 1]);
+                orow(r0 + j)[wave * 32 + c32] = static_cast<uint16_t>(v);
+                orow(r0 + j + 1)[wave * 32 + c32] = static_cast<uint16_t>(v >> 16);
+            }
         }
     __syncthreads();
     constexpr int CPR = OC / 8;
