@@ -71,18 +71,16 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 
 // fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quiet bit set).
 // Same rounding as the reference's host conversion (int4_cube_lab/host/bf16.h:17-27)
-// and torch's .to(torch.bfloat16).
+// and torch's .to(torch.bfloat16): (u + 0x7fff + lsb) >> 16, NaN -> (u >> 16)
+// | 0x40.  One v_cvt_pk_bf16_f32, which on MI355X gives exactly that for
+// every fp32 input (checked against the integer formula on 2^24 bit
+// patterns including ties, subnormals, infinities and NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
-// Two fp32 -> two bf16 (low half: a), round to nearest even, in one
-// v_cvt_pk_bf16_f32: on MI355X it equals f32_to_bf16_bits for every fp32
-// input (checked on 2^24 bit patterns including ties, subnormals, infinities
-// and NaN).
+// Two fp32 -> two bf16 (low half: a) in one v_cvt_pk_bf16_f32, rounded as
+// f32_to_bf16_bits.
 __device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
     typedef float f32x2 __attribute__((ext_vector_type(2)));
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
