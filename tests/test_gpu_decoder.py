@@ -267,3 +267,19 @@ def test_qwq_width_layers_linears_match_oracle(pkg, dev, monkeypatch):
     rel = (dec_logits - m.last_logits.float()).norm() / m.last_logits.float().norm()
     say(f"  prefill vs decode logits rel-L2 {rel:.5f}")
     assert rel < 2e-2, f"rel-L2 {rel}"
+
+
+def test_fused_score_scaling_equals_three_ops(dev):
+    """The decoder's attention scores as one torch.add(bias, s, alpha=1/sqrt(D)) equal the
+    separate s.float() * (1/sqrt(D)) + bias bit for bit when the bias holds only 0 and -inf
+    (bf16 scores of every magnitude, masked and unmasked positions)."""
+    g = torch.Generator(device=dev).manual_seed(3)
+    s = (torch.randn((2, 8, 5, 1200), generator=g, device=dev) * 40).to(torch.bfloat16)
+    s[0, 0, 0, :8] = torch.tensor([0.0, -0.0, 1e-38, -3e38, 448.0, 1.0, -1.0, 65504.0], device=dev).to(torch.bfloat16)
+    pos = torch.arange(1200, device=dev)
+    bias = torch.where(pos > 700, float("-inf"), 0.0).view(1, 1, 1, 1200)
+    for d in (64, 128):
+        a = 1.0 / math.sqrt(d)
+        ref = s.float() * a + bias
+        got = torch.add(bias, s, alpha=a)
+        assert got.dtype == torch.float32 and torch.equal(got, ref), f"head_dim {d}"

@@ -162,8 +162,12 @@ class W4A8Decoder:
 
     def _attend(self, q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
         """q [B, KVH, R, D] (R = query heads per KV head x query tokens), kc [B, KVH, D, L],
-        vc [B, KVH, L, D], additive bias broadcast to [B, KVH, R, L] -> [B, KVH, R, D]."""
-        scores = torch.matmul(q, kc).float() * (1.0 / math.sqrt(self.cfg.head_dim)) + bias
+        vc [B, KVH, L, D], additive bias broadcast to [B, KVH, R, L] -> [B, KVH, R, D].
+
+        The scores are fp32(bf16(q.k)) * 1/sqrt(D) + bias, as one torch.add with alpha: the
+        bias holds only 0 and -inf, so the one rounding of the product is that of the separate
+        .float(), multiply and add (three launches), fused multiply-add or not."""
+        scores = torch.add(bias, torch.matmul(q, kc), alpha=1.0 / math.sqrt(self.cfg.head_dim))
         p = torch.softmax(scores, dim=-1).to(torch.bfloat16)
         return torch.matmul(p, vc)
 
