@@ -91,6 +91,51 @@ struct PrefillParams {
     bool cols;         // group stride 128 at 128 rows: 128 x 32 wave tiles (gemm_prefill_cols_kernel)
 };
 
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2.  Renumber them so that every XCD walks one contiguous run of tiles, and
+// order the tiles in bands of p.band tile rows, so the workgroups resident on
+// one XCD at a time cover a compact block of the output and share A rows and
+// weight columns in that XCD's L2.
+__device__ __forceinline__ void tile_of(const PrefillParams& p, int& tile_m, int& tile_n) {
+    const int nwg = static_cast<int>(gridDim.x);
+    const int bid = static_cast<int>(blockIdx.x);
+    const int xcd = bid & 7, q = nwg >> 3, r = nwg & 7;
+    const int lin = xcd * q + min(xcd, r) + (bid >> 3);
+    const int band = lin / (p.band * p.tiles_n);
+    const int inband = lin - band * p.band * p.tiles_n;
+    const int rows = min(p.band, p.tiles_m - band * p.band);
+    tile_m = band * p.band + inband % rows;
+    tile_n = inband / rows;
+}
+
+// The bf16 output tile, staged in LDS as BM rows of OC columns (row stride OS
+// elements; rows 0..BM/2-1 from lo, the rest from hi), leaves as 16-byte row
+// stores of 8 columns per thread and step; rows past M are skipped, and a
+// chunk past the last column (or a row that cannot take 16-byte stores) is
+// stored element by element.
+template <int BM, int THREADS, int OC, int OS>
+__device__ __forceinline__ void store_tile(const PrefillParams& p, const uint16_t* lo, const uint16_t* hi, int m0,
+                                           int n0, int ncols, int tid) {
+    constexpr int CPR = OC / 8;   // chunks per row
+#pragma unroll
+    for (int k = 0; k < BM * CPR / THREADS; ++k) {
+        const int c = tid + k * THREADS;
+        const int r = c / CPR, c8 = (c % CPR) * 8;
+        const int row = m0 + r, col = n0 + c8;
+        if (row >= p.M || col >= ncols) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>((r < BM / 2 ? lo : hi) + (r % (BM / 2)) * OS + c8);
+        uint16_t* y = p.Y + static_cast<int64_t>(row) * p.ldy + col;
+        if (p.vec_out && col + 8 <= ncols) {
+            *reinterpret_cast<uint4*>(y) = v;
+        } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (col + q < ncols) y[q] = static_cast<uint16_t>(w[q >> 1] >> (16 * (q & 1)));
+        }
+    }
+}
+
 // K is walked in the padded group layout (kgeom.h): group g starts at g*gs,
 // only the last group may be shorter, and it ends at kpad.
 // GMODE: 0 = stride 64 (two groups per step), 1 = stride 128 (one per step),
@@ -124,23 +169,8 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / kWN;  // 0..BM / 64 - 1
     const int wn = wave % kWN;
-    // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
-    // L2.  Renumber them so that every XCD walks one contiguous run of tiles,
-    // and order the tiles in bands of p.band tile rows, so the workgroups
-    // resident on one XCD at a time cover a compact block of the output and
-    // share A rows and weight columns in that XCD's L2.
     int tile_m, tile_n;
-    {
-        const int nwg = static_cast<int>(gridDim.x);
-        const int bid = static_cast<int>(blockIdx.x);
-        const int xcd = bid & 7, q = nwg >> 3, r = nwg & 7;
-        const int lin = xcd * q + min(xcd, r) + (bid >> 3);
-        const int band = lin / (p.band * p.tiles_n);
-        const int inband = lin - band * p.band * p.tiles_n;
-        const int rows = min(p.band, p.tiles_m - band * p.band);
-        tile_m = band * p.band + inband % rows;
-        tile_n = inband / rows;
-    }
+    tile_of(p, tile_m, tile_n);
     const int m0 = tile_m * kBM;
     const int n0 = tile_n * (SWIGLU ? kBN / 2 : kBN);
     const int c32 = lane & 31;   // column (B) / row (A) inside a 32-block
@@ -480,28 +510,8 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
         }
     }
     __syncthreads();
-    // 8 columns per thread and step; rows past M are skipped, a chunk past the
-    // last column (or a row that cannot take 16-byte stores) is stored element
-    // by element
-    const int ncols = SWIGLU ? p.half_n : p.N;
-    constexpr int CPR = OC / 8;   // chunks per row
-#pragma unroll
-    for (int k = 0; k < kBM * CPR / kThreads; ++k) {
-        const int c = tid + k * kThreads;
-        const int r = c / CPR, c8 = (c % CPR) * 8;
-        const int row = m0 + r, col = n0 + c8;
-        if (row >= p.M || col >= ncols) continue;
-        const uint4 v = *reinterpret_cast<const uint4*>(orow(r) + c8);
-        uint16_t* y = p.Y + static_cast<int64_t>(row) * p.ldy + col;
-        if (p.vec_out && col + 8 <= ncols) {
-            *reinterpret_cast<uint4*>(y) = v;
-        } else {
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-                if (col + q < ncols) y[q] = static_cast<uint16_t>(w[q >> 1] >> (16 * (q & 1)));
-        }
-    }
+    store_tile<kBM, kThreads, OC, OS>(p, reinterpret_cast<const uint16_t*>(la0), reinterpret_cast<const uint16_t*>(la1),
+                                      m0, n0, SWIGLU ? p.half_n : p.N, tid);
 }
 
 constexpr int kDW = 2;   // weight prefetch depth in K steps
@@ -531,17 +541,7 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // the wave's 32-column block
     int tile_m, tile_n;
-    {
-        const int nwg = static_cast<int>(gridDim.x);
-        const int bid = static_cast<int>(blockIdx.x);
-        const int xcd = bid & 7, q = nwg >> 3, r = nwg & 7;
-        const int lin = xcd * q + min(xcd, r) + (bid >> 3);
-        const int band = lin / (p.band * p.tiles_n);
-        const int inband = lin - band * p.band * p.tiles_n;
-        const int rows = min(p.band, p.tiles_m - band * p.band);
-        tile_m = band * p.band + inband % rows;
-        tile_n = inband / rows;
-    }
+    tile_of(p, tile_m, tile_n);
     const int m0 = tile_m * kBM;
     const int n0 = tile_n * kBN;
     const int c32 = lane & 31;
@@ -703,24 +703,8 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
             }
         }
     __syncthreads();
-    constexpr int CPR = OC / 8;
-#pragma unroll
-    for (int k = 0; k < kBM * CPR / kThreads; ++k) {
-        const int c = tid + k * kThreads;
-        const int r = c / CPR, c8 = (c % CPR) * 8;
-        const int row = m0 + r, cc = n0 + c8;
-        if (row >= p.M || cc >= p.N) continue;
-        const uint4 v = *reinterpret_cast<const uint4*>(orow(r) + c8);
-        uint16_t* y = p.Y + static_cast<int64_t>(row) * p.ldy + cc;
-        if (p.vec_out && cc + 8 <= p.N) {
-            *reinterpret_cast<uint4*>(y) = v;
-        } else {
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-                if (cc + q < p.N) y[q] = static_cast<uint16_t>(w[q >> 1] >> (16 * (q & 1)));
-        }
-    }
+    store_tile<kBM, kThreads, OC, OS>(p, reinterpret_cast<const uint16_t*>(la0), reinterpret_cast<const uint16_t*>(la1),
+                                      m0, n0, p.N, tid);
 }
 
 template <int GMODE, bool SBF16, bool DUMP, bool SWIGLU>
