@@ -66,6 +66,14 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    # A kernel whose host launch stub the compiler dropped links fine and
+    # fails only when the library is loaded: refuse such a build here.
+    nm = shutil.which("nm")
+    if nm:
+        syms = subprocess.run([nm, "-D", "--undefined-only", str(tmp)], capture_output=True, text=True).stdout
+        missing = [l.split()[-1] for l in syms.splitlines() if "__device_stub__" in l]
+        if missing:
+            raise RuntimeError(f"undefined kernel launch stubs in {tmp.name}: {missing[:4]}")
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")

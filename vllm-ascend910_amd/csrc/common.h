@@ -48,6 +48,13 @@ __device__ __forceinline__ uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 2);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// 16 bytes per lane from a buffer straight into LDS (gfx950): lane l's bytes
+// land at lds + 16 l (lds wave-uniform).  A plain device function: with the
+// builtin written directly in some kernel templates, the host pass drops the
+// kernel's launch stub (the library then fails to load).
+__device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
+}
 __device__ __forceinline__ uint32_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
 }

@@ -220,8 +220,7 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
         int8_t* const dst = abuf(b) + kNA * 1024 * wave;
 #pragma unroll
         for (int i = 0; i < kNA; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_rsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * i),
-                                                     16, aoffg[i] + k, 0, 0, 0);
+            buf_load16_lds(ra_rsrc, dst + 1024 * i, aoffg[i] + k);
     };
 
     uint4 wr[DW][2][2];
@@ -517,20 +516,24 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 constexpr int kDW = 2;   // weight prefetch depth in K steps
 
 // Group stride 128 without the partial dump or the SwiGLU pairs: the same
-// 128 x 128 tile and K step, but each of the four waves owns all 128 rows and
-// one 32-column block (instead of 64 x 64).  Every weight is then loaded and
+// BM x 128 tile (BM = 128 or 64) and K step, but each of the four waves owns
+// all BM rows and one 32-column block (instead of 64 x 64 per wave; at 64
+// rows, four waves per tile instead of two, three workgroups per CU).  Every weight is then loaded and
 // unpacked by one wave instead of two: half the weight loads, and the unpack
 // of each B operand serves four MFMAs instead of two (1.5 instead of 3 VALU
-// instructions per MFMA), for twice the A operand reads from LDS.  Row block
+// instructions per MFMA; at 64 rows still 3), for twice the A operand reads
+// from LDS.  Row block
 // rb's fold runs during row block rb + 1's MFMAs (row block 3's during the next
 // step's row block 0), one MFMA to eight fold instructions.  Each output's
 // arithmetic is the 64 x 64 kernel's: outputs are bit-identical.
-template <bool SBF16>
-__global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const PrefillParams p) {
-    constexpr int kBM = 128, kThreads = 256;
+template <bool SBF16, int BM>
+__global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_prefill_cols_kernel(const PrefillParams p) {
+    constexpr int kBM = BM, kThreads = 256;
+    constexpr int RB = BM / 32;                  // 32-row blocks per wave
+    constexpr int NA = BM * 8 / kThreads;        // 16-byte A chunks per lane per step
     constexpr int kABuf = kBM * 128;
-    constexpr int kABuf01 = abuf01_bytes<128, false>();
-    static_assert(kNA == kBM * 8 / kThreads, "four 16-byte A chunks per lane per step");
+    constexpr int kABuf01 = abuf01_bytes<BM, false>();
+    static_assert(BM == 64 || BM == 128, "64- or 128-row tiles");
     __shared__ __attribute__((aligned(16))) int8_t la0[kABuf01];
     __shared__ __attribute__((aligned(16))) int8_t la1[kABuf01];
     __shared__ __attribute__((aligned(16))) int8_t la2[kABuf];
@@ -564,21 +567,20 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
     const uint32_t woff1 = tile0 + static_cast<uint32_t>((col & 15) + 16 * (2 + hh)) * 16u;  // slabs 1, 3
     const uint32_t soff = (static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.NG) * 16u + (col & 15)) * 2u;
 
-    // activations: as in gemm_prefill_kernel (wave w stages tile rows 32 w..+32)
-    uint32_t aoffg[kNA];
+    // activations: as in gemm_prefill_kernel (wave w stages tile rows 8 NA w..+8 NA)
+    uint32_t aoffg[NA];
 #pragma unroll
-    for (int i = 0; i < kNA; ++i) {
-        const int r = 8 * (kNA * wave + i) + (lane >> 3);
+    for (int i = 0; i < NA; ++i) {
+        const int r = 8 * (NA * wave + i) + (lane >> 3);
         const int q = (lane & 7) ^ a_swz(r);
         aoffg[i] = static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(p.lda) + static_cast<uint32_t>(q) * 16u;
     }
     auto load_a = [&](int kt, int b) {
         const uint32_t k = static_cast<uint32_t>(min(kt, p.KT - 1)) * 128u;
-        int8_t* const dst = abuf(b) + kNA * 1024 * wave;
+        int8_t* const dst = abuf(b) + NA * 1024 * wave;
 #pragma unroll
-        for (int i = 0; i < kNA; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_rsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * i),
-                                                     16, aoffg[i] + k, 0, 0, 0);
+        for (int i = 0; i < NA; ++i)
+            buf_load16_lds(ra_rsrc, dst + 1024 * i, aoffg[i] + k);
     };
     uint4 wr[kDW][2];
     auto load_w = [&](int slot, int kt) {
@@ -593,10 +595,10 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
         return buf_load_u16(rs_rsrc, soff + static_cast<uint32_t>(g) * 32u);
     };
 
-    v16i P[4];
-    float acc[4][16];
+    v16i P[RB];
+    float acc[RB][16];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             P[rb][i] = 0;
@@ -618,9 +620,9 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
     for (int s = 0; s < kDW; ++s) load_w(s, s);
     uint32_t sc = load_s(0);
     asm volatile("" ::: "memory");
-    uint32_t scp = 0u;   // the previous step's scale (row block 3 folds one step late)
+    uint32_t scp = 0u;   // the previous step's scale (the last row block folds one step late)
     if (tid < kBM) tsl[tid] = bf16_bits_to_f32(ts_bits) * 0.0625f;
-    wait_vm_barrier<2 * kNA + kDW * 2 + 1>();
+    wait_vm_barrier<2 * NA + kDW * 2 + 1>();
 
     uint32_t aread[4];
 #pragma unroll
@@ -645,14 +647,14 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
         }
         load_w(u, kt + kDW);
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            if (rb < 3) {
+        for (int rb = 0; rb < RB; ++rb) {
+            if (rb < RB - 1) {
 #pragma unroll
                 for (int s = 0; s < 4; ++s) av[(rb + 1) & 1][s] = lds_a(rb + 1, s);
             }
 #pragma unroll
             for (int s = 0; s < 4; ++s) P[rb] = mfma32(av[rb & 1][s], bvs[s], s == 0 ? zero16 : P[rb]);
-            if (rb == 0) fold(3, scp);
+            if (rb == 0) fold(RB - 1, scp);
             else fold(rb - 1, sc);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -664,11 +666,11 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
         scp = sc;
         sc = scn;
     };
-    // a step issues kNA + 3 vector memory operations; the wait keeps the two
+    // a step issues NA + 3 vector memory operations; the wait keeps the two
     // newest steps' in flight (A(kt + 1), issued in step kt - 2, has landed)
     auto one = [&](int kt, int u) __attribute__((always_inline)) {
         step(kt, u % kDW, u % kNB);
-        wait_vm_barrier<2 * (kNA + 3)>();
+        wait_vm_barrier<2 * (NA + 3)>();
     };
     int kt = 0;
     for (; kt + kNB <= p.KT; kt += kNB) {
@@ -678,18 +680,18 @@ __global__ __launch_bounds__(256, 2) void gemm_prefill_cols_kernel(const Prefill
 #pragma unroll
     for (int u = 0; u < kNB - 1; ++u)
         if (kt + u < p.KT) one(kt + u, u);
-    fold(3, scp);   // the last step's row block 3
+    fold(RB - 1, scp);   // the last step's last row block
 
     // ---- epilogue: as in gemm_prefill_kernel, through the first two A buffers
     constexpr int OC = kBN;
-    constexpr int OS = out_stride<128, false>();
+    constexpr int OS = out_stride<BM, false>();
     constexpr int RPA = kBM / 2;
     wait_vm_barrier<0>();
     auto orow = [&](int r) -> uint16_t* {
         return reinterpret_cast<uint16_t*>(r < RPA ? la0 : la1) + (r % RPA) * OS;
     };
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int r0 = rb * 32 + q * 8 + hh * 4;   // this lane's four rows r0..r0+3
@@ -714,8 +716,9 @@ hipError_t launch_g(const PrefillParams& p, hipStream_t stream) {
     // dump variants); each output element's arithmetic does not depend on the
     // tile height, so its outputs equal the 64-row kernel's bit for bit.
     if constexpr (GMODE == 1 && !DUMP && !SWIGLU) {
-        if (p.bm == 128 && p.cols) {
-            gemm_prefill_cols_kernel<SBF16><<<grid, dim3(256), 0, stream>>>(p);
+        if (p.cols) {
+            if (p.bm == 128) gemm_prefill_cols_kernel<SBF16, 128><<<grid, dim3(256), 0, stream>>>(p);
+            else gemm_prefill_cols_kernel<SBF16, 64><<<grid, dim3(256), 0, stream>>>(p);
             return hipGetLastError();
         }
     }
@@ -744,20 +747,32 @@ hipError_t launch(const PrefillParams& p, hipStream_t stream) {
 
 int64_t prefill_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
 
-int prefill_tile_rows(int64_t M, int64_t N, bool swiglu) {
-    // 64-row tiles (twice as many, up to four workgroups per CU) where the
-    // 128-row ones would leave CUs idle or unevenly loaded: at most one for
-    // every second CU, or between one and two per CU.  Measured on MI355X
-    // (QwQ-32B shapes, 128 -> 64 rows): o_proj M=1024 49.2 -> 46.1 us,
-    // down_proj M=1024 222 -> 205 us, qkv/o/down M=128-256 3-6% faster; at
-    // M=512 (at most one 128-row tile per CU) 64 rows lose 30-50%.
+int prefill_tile_rows(int64_t M, int64_t N, int64_t group, bool swiglu) {
     const int64_t tn = swiglu ? geom::ceil_div(N / 2, kBN / 2) : geom::ceil_div(N, kBN);
     const int64_t tiles = geom::ceil_div(M, int64_t{128}) * tn, cus = device_cu_count();
+    if (W4A8_PREFILL_COLS && !swiglu && geom::group_stride(group) == 128) {
+        // The four-wave tiles of gemm_prefill_cols_kernel (64-row tiles run
+        // three workgroups per CU, 128-row tiles two).  64 rows up to 1.5
+        // tiles of 128 rows per CU and between 2 and 4 per CU; 128 rows where
+        // they fill the CUs about once (up to 2 per CU) or many times.
+        // Measured on MI355X at the QwQ-32B shapes (64 / 128 rows, us): o_proj
+        // M=1024 37.0 / 41.7, M=2048 63.3 / 66.2, M=4096 123.1 / 116.5; qkv
+        // M=256 17.8 / 25.3, M=1024 49.1 / 45.1, M=4096 171 / 165; down M=1024
+        // 179 / 198; gate_up M=256 86 / 88, M=512 167 / 156.
+        return (tiles * 2 <= cus * 3 || (tiles > 2 * cus && tiles <= 4 * cus)) ? 64 : 128;
+    }
+    // The 64 x 64 wave tiles (other group strides, SwiGLU): 64-row tiles
+    // (twice as many, up to four workgroups per CU) where the 128-row ones
+    // would leave CUs idle or unevenly loaded: at most one for every second
+    // CU, or between one and two per CU.  Measured on MI355X (QwQ-32B shapes,
+    // 128 -> 64 rows): o_proj M=1024 49.2 -> 46.1 us, down_proj M=1024 222 ->
+    // 205 us, qkv/o/down M=128-256 3-6% faster; at M=512 (at most one
+    // 128-row tile per CU) 64 rows lose 30-50%.
     return (tiles <= cus / 2 || (tiles > cus && tiles <= 2 * cus)) ? 64 : 128;
 }
 
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
-    return launch_gemm_prefill_bm(a, prefill_tile_rows(a.M, a.N, a.swiglu), stream);
+    return launch_gemm_prefill_bm(a, prefill_tile_rows(a.M, a.N, a.group, a.swiglu), stream);
 }
 
 hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream) {

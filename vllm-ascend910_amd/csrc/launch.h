@@ -95,7 +95,7 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
 // The prefill GEMM with an explicit tile height (128 or 64 rows), and the
 // height launch_gemm_prefill picks.
 hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream);
-int prefill_tile_rows(int64_t M, int64_t N, bool swiglu);
+int prefill_tile_rows(int64_t M, int64_t N, int64_t group, bool swiglu);
 
 
 // Mid-group compat path (the reference's midgroup_quant_a / midgroup_w4a8_gemm).
