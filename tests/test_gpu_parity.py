@@ -229,6 +229,8 @@ GEMM_CASES = [
     (200, 300, 768, 192, "bf16"),    # prefill, groups ending mid-step, K % 128 == 64
     (96, 520, 2048, 256, "f16"),     # prefill, a group spans two steps
     (257, 264, 1024, 512, "bf16"),
+    (3200, 2000, 384, 128, "bf16"),  # four-wave 128-row prefill tiles (400 of them), ragged N
+    (6200, 1000, 448, 96, "f16"),    # the same, group 96 (stride 128, every group padded), ragged K
 ]
 
 
