@@ -424,7 +424,13 @@ def group_partials_asym(a_q: np.ndarray, w_codes: np.ndarray, w_zero_bits: Optio
         w = w_codes[:, sl].astype(np.int64)
         if w_zero_bits is not None:
             w = w - np.trunc(bf16_bits_to_f32(w_zero_bits[g])).astype(np.int64)[:, None]
-        out[g] = a_q[:, sl].astype(np.int64) @ w.T
+        a = a_q[:, sl].astype(np.int64)
+        # float64 products and sums of these integers are exact in any order
+        # while sum |a| * |w| stays below 2**53, which BLAS then computes fast
+        if int(np.abs(a).max(initial=0)) * int(np.abs(w).max(initial=0)) * a.shape[1] < 2 ** 53:
+            out[g] = (a.astype(np.float64) @ w.T.astype(np.float64)).astype(np.int64)
+        else:
+            out[g] = a @ w.T
     return out
 
 

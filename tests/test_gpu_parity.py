@@ -898,6 +898,10 @@ MIDGROUP_CASES = [
     (300, 384, 5120, 1024, True),
     (16, 200, 2048, 256, True),       # stride 256 (two tiles per group), N not a multiple of 16
     (70, 160, 1000, 128, True),       # stride 128, ragged tail of 104
+    (512, 1040, 3072, 1024, True),    # prefill 64x64 tiles, K over 3 waves, last column tile one block wide
+    (1536, 1296, 2048, 1024, False),  # prefill tiles, K over 2 waves
+    (2048, 2064, 2048, 1024, True),   # prefill tiles, 1056 workgroups: one wave walks all of K
+    (200, 200, 6400, 128, True),      # 50 groups: scales too many for the 64x64 tile, 64x32 instead
 ]
 
 

@@ -25,7 +25,8 @@
 //
 // Work split as in the decode kernel: a workgroup owns CPW column blocks of 16
 // and a block of 16*MT rows (grid.y walks row blocks), its KW waves split K at
-// group boundaries and are reduced through LDS in a fixed order.  The
+// group boundaries and are reduced through LDS in a fixed order (prefill
+// shapes: 64 x 64 tiles, K split only while the grid is small).  The
 // activation scales and ksums of the workgroup's rows, and the weight scales
 // and zero points of its columns, are staged in LDS once.  All global reads are
 // raw buffer loads; rows and columns past the tensors, and the K tail past
@@ -60,11 +61,13 @@ struct MidParams {
     uint32_t a_bytes, w_bytes;
 };
 
-__device__ __forceinline__ int act_even(uint32_t h, uint32_t l) {
-    return static_cast<int>(((h << 4) & 0xf0f0f0f0u) | ((l ^ 0x08080808u) & 0x0f0f0f0fu));
-}
-__device__ __forceinline__ int act_odd(uint32_t h, uint32_t l) {
-    return static_cast<int>((h & 0xf0f0f0f0u) | (((l >> 4) ^ 0x08080808u) & 0x0f0f0f0fu));
+// Even and odd activation bytes of one dword of each plane: byte j of `ev` is
+// (hi nibble 2j << 4) | (lo nibble 2j ^ 8), of `od` the same for nibble 2j+1.
+// The lo plane's offset flip (every nibble ^ 8) is one xor for both.
+__device__ __forceinline__ void act_pair(uint32_t h, uint32_t l, int& ev, int& od) {
+    const uint32_t lx = l ^ 0x88888888u;
+    ev = static_cast<int>(((h << 4) & 0xf0f0f0f0u) | (lx & 0x0f0f0f0fu));
+    od = static_cast<int>((h & 0xf0f0f0f0u) | ((lx >> 4) & 0x0f0f0f0fu));
 }
 
 template <int MT, int CPW, int KWMAX, int D, bool ASYM, bool DUMP>
@@ -196,8 +199,13 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const uint4 h = hb[s][mt], l = lb[s][mt];
-                    av[mt][0] = v4i{act_even(h.x, l.x), act_odd(h.x, l.x), act_even(h.y, l.y), act_odd(h.y, l.y)};
-                    av[mt][1] = v4i{act_even(h.z, l.z), act_odd(h.z, l.z), act_even(h.w, l.w), act_odd(h.w, l.w)};
+                    int e[4], o[4];
+                    act_pair(h.x, l.x, e[0], o[0]);
+                    act_pair(h.y, l.y, e[1], o[1]);
+                    act_pair(h.z, l.z, e[2], o[2]);
+                    act_pair(h.w, l.w, e[3], o[3]);
+                    av[mt][0] = v4i{e[0], o[0], e[1], o[1]};
+                    av[mt][1] = v4i{e[2], o[2], e[3], o[3]};
                 }
                 load_slot(s, t + D);
 #pragma unroll
@@ -243,27 +251,48 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
     }
 }
 
-constexpr int kwmax_mid(int mt) { return mt == 1 ? 12 : 8; }
+// Variants (rows x columns per workgroup, load depth, most waves):
+//   Ma <= 16       16 x 32, depth 4, up to 12 waves (decode)
+//   Ma <= 64       64 x 32, depth 2, up to 8 waves
+//   Ma >  64       64 x 64, depth 2, up to 4 waves (prefill): twice the
+//                  columns per activation read; one wave per SIMD
+// Depth 2 at 64 rows keeps the operand ring within the register budget (at
+// depth 4 the 64 x 32 tile spilled about 60 registers to scratch).
+constexpr int mid_depth(int mt) { return mt == 1 ? 4 : 2; }
+constexpr int kwmax_mid(int mt, int cpw) { return mt == 1 ? 12 : cpw > 2 ? 4 : 8; }
 
-template <int MT, bool ASYM, bool DUMP>
+template <int MT, int CPW, bool ASYM, bool DUMP>
 hipError_t launch_mid(const MidParams& p, int kw, hipStream_t stream) {
-    constexpr int CPW = 2, D = 4, KWM = kwmax_mid(MT);
+    constexpr int D = mid_depth(MT), KWM = kwmax_mid(MT, CPW);
     // dynamic LDS stays within the 64 KiB a launch gets without a function
     // attribute: the staged scales, then as many reduction slices as fit
     const size_t staged = static_cast<size_t>(p.NG) * (2 * 16 * MT + 2 * 16 * CPW) * sizeof(float);
     const size_t slice = static_cast<size_t>(16 * MT) * 16 * CPW * sizeof(float);
     if (staged + slice > kMidLdsLimit) return hipErrorInvalidValue;
     const int wfit = static_cast<int>((kMidLdsLimit - staged) / slice);
-    const int w = std::max(1, std::min({kw, KWM, p.NG, wfit}));
     const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW), static_cast<unsigned>((p.Ma + 16 * MT - 1) / (16 * MT)));
+    if (CPW > 2) {
+        // prefill: split K over waves only while the grid is small
+        const int64_t wgs = static_cast<int64_t>(grid.x) * grid.y;
+        kw = std::min(kw, wgs >= 1024 ? 1 : wgs >= 256 ? 2 : 4);
+    }
+    const int w = std::max(1, std::min({kw, KWM, p.NG, wfit}));
     const size_t lds = staged + static_cast<size_t>(w) * slice;
     gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP><<<grid, dim3(64 * w), lds, stream>>>(p);
     return hipGetLastError();
 }
 
+// The prefill variant's staged scales need twice the column slots; shapes
+// whose group count leaves no room for them take the 64 x 32 variant.
+bool mid_wide_fits(const MidParams& p) {
+    return static_cast<size_t>(p.NG) * (2 * 64 + 2 * 64) * sizeof(float) + 64 * 64 * sizeof(float) <= kMidLdsLimit;
+}
+
 template <bool ASYM, bool DUMP>
 hipError_t launch_mt(const MidParams& p, int kw, hipStream_t stream) {
-    return p.Ma <= 16 ? launch_mid<1, ASYM, DUMP>(p, kw, stream) : launch_mid<4, ASYM, DUMP>(p, kw, stream);
+    if (p.Ma <= 16) return launch_mid<1, 2, ASYM, DUMP>(p, kw, stream);
+    if (p.Ma <= 64 || !mid_wide_fits(p)) return launch_mid<4, 2, ASYM, DUMP>(p, kw, stream);
+    return launch_mid<4, 4, ASYM, DUMP>(p, kw, stream);
 }
 
 }  // namespace
