@@ -667,7 +667,7 @@ def compat(pkg, dev, synth, time_graph, T, cold_bytes):
             wz = torch.randint(-8, 8, (ng, N), device=dev, generator=gen).to(torch.bfloat16)
             wk = torch.zeros((ng, N), dtype=torch.int32, device=dev)
             pool.append((w_q, ws, wk, wz))
-        for M in (1, 16, 64, 1024):
+        for M in (1, 16, 64, 1024, 4096):
             x = torch.from_numpy(synth.activations(M, K, seed=M).view(np.int16)).view(torch.bfloat16).to(dev)
             a = torch.ops.npu.midgroup_quant_a(x, G)
             n = T if M <= 64 else 4
