@@ -87,7 +87,8 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="turn two rocprofv3 --pmc databases of a --pmc-probe run (FETCH_SIZE, WRITE_SIZE) into "
                          "the per-shape HBM traffic table (markdown on stdout) and exit")
-    ap.add_argument("--pmc-json", metavar="OUT", help="with --pmc-summary: also write the table as JSON")
+    ap.add_argument("--pmc-json", metavar="OUT",
+                    help="with --pmc-summary or --prefill-pmc-summary: also write the traffic figures as JSON")
     ap.add_argument("--prefill-probe", type=int, metavar="M", default=0,
                     help="for rocprofv3 runs: each configs[2] projection's prefill GEMM at M rows three times "
                          "(eager, group 128), then a 256 MiB device copy of known size")
@@ -110,7 +111,7 @@ def main():
         pmc_summary(*args.pmc_summary, args.pmc_json)
         return
     if args.prefill_pmc_summary:
-        prefill_pmc_summary(args.prefill_pmc_summary)
+        prefill_pmc_summary(args.prefill_pmc_summary, args.pmc_json)
         return
     if args.decoder_trace_summary:
         decoder_trace_summary(args.decoder_trace_summary)
@@ -436,6 +437,15 @@ def main():
             "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": None,
             "per_launch_ops_avg": round(ops / len(at)), "launch_us_avg": round(us_tot / len(at), 2),
             "timing": "HIP events around graph replays of back-to-back launches"}
+        # HBM bytes per launch from the committed counter passes of the same
+        # kernel and M (FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy)
+        tsrc = ROOT / "profiles" / "gemm_prefill_cols_kernel_traffic.json"
+        if tsrc.exists():
+            tj = json.loads(tsrc.read_text())
+            if tj.get("M") == at[0]["M"]:
+                result["roofline_prefill"].update(
+                    traffic=round(tj["avg_traffic_bytes"]), alg_bytes_avg=round(tj["avg_alg_bytes"]),
+                    traffic_source=str(tsrc.relative_to(ROOT)))
 
     # the decode pools are not needed past this point
     weights = None
@@ -816,7 +826,7 @@ def prefill_probe(pkg, dev, M, calls=3):
     log(f"bench: prefill probe done ({len(PROJS)} projections x {calls} calls at M={M}, then a 268435456-byte copy)")
 
 
-def prefill_pmc_summary(dbs):
+def prefill_pmc_summary(dbs, json_out=None):
     """Counter table of the prefill GEMM (gemm_prefill_kernel or gemm_prefill_cols_kernel) from
     --prefill-probe runs: counter databases
     (one pass each) and a --kernel-trace database (the last argument) for durations."""
@@ -864,7 +874,8 @@ def prefill_pmc_summary(dbs):
               f"python3 REPO/bench.py --prefill-probe {M}")
     print(f"    rocprofv3 --kernel-trace -d /tmp/pf -o kt -- python3 REPO/bench.py --prefill-probe {M}")
     print("    python3 REPO/bench.py --prefill-pmc-summary " +
-          " ".join(f"p{i + 1}_results.db" for i in range(len(pmc_dbs))) + " kt_results.db\n")
+          " ".join(f"p{i + 1}_results.db" for i in range(len(pmc_dbs))) + " kt_results.db" +
+          (" --pmc-json REPO/profiles/gemm_prefill_cols_kernel_traffic.json" if json_out else "") + "\n")
     names = sorted({c for p in ctr for c in ctr[p]})
     print("| counter | " + " | ".join(PROJS) + " |\n|---|" + "---:|" * len(PROJS))
     print("| duration us | " + " | ".join(f"{avg(dur[p]) / 1e3:.1f}" for p in PROJS) + " |")
@@ -902,6 +913,14 @@ def prefill_pmc_summary(dbs):
         row("algorithmic MB", lambda p: gemm_bytes(M, synth.QWQ_SHAPES[p][1], synth.QWQ_SHAPES[p][0]) / 1e6)
         print(f"\nCalibration: the 256 MiB copy reads FETCH_SIZE {cal['FETCH_SIZE']:.0f} KiB (factor {ff:.4f}) and "
               f"WRITE_SIZE {cal['WRITE_SIZE']:.0f} KiB (factor {fw:.4f}).")
+        if json_out:
+            per = {p: {"traffic_bytes": (c(p, "FETCH_SIZE") * ff + c(p, "WRITE_SIZE") * fw) * 1024,
+                       "alg_bytes": gemm_bytes(M, synth.QWQ_SHAPES[p][1], synth.QWQ_SHAPES[p][0]),
+                       "duration_us": us(p)} for p in PROJS}
+            Path(json_out).write_text(json.dumps(dict(
+                kernel=" / ".join(kname), M=M, group=128, factor_fetch=ff, factor_write=fw, per_shape=per,
+                avg_traffic_bytes=sum(v["traffic_bytes"] for v in per.values()) / len(per),
+                avg_alg_bytes=sum(v["alg_bytes"] for v in per.values()) / len(per)), indent=1) + "\n")
 
 
 def cpu_baseline(pkg, dev, seconds):
