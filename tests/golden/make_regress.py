@@ -7,8 +7,8 @@ runs one seeded case per kernel path of this build (activation quant, the
 staged, per-tile and row-group decode plans, the wide and K-split decode
 kernels, the fused single-row linear, the SwiGLU epilogue, per-channel scales,
 both prefill tile shapes at group 128 and the prefill at group 256, the
-reference-compat pair at decode and prefill sizes) and records the SHA-256 of
-each output's bytes.
+reference-compat pair at decode sizes, on wide N and at prefill sizes) and
+records the SHA-256 of each output's bytes.
 tests/test_gpu_regress.py recomputes them and fails on any changed bit.
 
 Every input is drawn by numpy from fixed seeds (the same bytes on every host),
@@ -114,6 +114,7 @@ CASES = {
     "gemm_m2048_prefill_g256": ("gemm_prefill_kernel, group 256", _gemm_case(2048, 2048, 1024, 256, 13)),
     "midgroup_m16_g1024": ("compat quant_a + mid-group GEMM", _midgroup_case(16, 2048, 4096, 1024, 14)),
     "midgroup_m512_g1024": ("compat mid-group GEMM, 64x64 prefill tiles", _midgroup_case(512, 2048, 4096, 1024, 15)),
+    "midgroup_m16_wide_n": ("compat mid-group GEMM, shared-activation decode", _midgroup_case(16, 16384, 2048, 1024, 16)),
 }
 
 

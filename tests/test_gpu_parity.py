@@ -902,6 +902,9 @@ MIDGROUP_CASES = [
     (1536, 1296, 2048, 1024, False),  # prefill tiles, K over 2 waves
     (2048, 2064, 2048, 1024, True),   # prefill tiles, 1056 workgroups: one wave walks all of K
     (200, 200, 6400, 128, True),      # 50 groups: scales too many for the 64x64 tile, 64x32 instead
+    (16, 16400, 2048, 1024, True),    # wide N: four column waves share staged activations, last workgroup 1 block
+    (1, 16384, 1057, 1024, True),     # the same kernel at one row, ragged K
+    (5, 16400, 1152, 128, False),     # the same at stride 128 with an odd tile count (last step one tile)
 ]
 
 

@@ -251,6 +251,172 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
     }
 }
 
+// Decode rows (Ma <= 16) on wide N: four waves of two column blocks each
+// share the activation planes, staged through LDS two tiles (4 KB) at a time,
+// so a workgroup reads them once rather than once per wave (on gate_up the
+// activation-plane loads were a third of the time).  No K split: every wave
+// walks all of K and folds group by group, the one-wave order of
+// gemm_midgroup_kernel, so the outputs are the same bits.
+constexpr int kShWaves = 4;   // column waves per workgroup
+constexpr int kShCPW = 2;     // column blocks per wave
+constexpr int kShD = 4;       // weight ring depth (tiles)
+constexpr int kShP = 4;       // activation steps in flight (registers)
+
+template <bool ASYM, bool DUMP>
+__global__ __launch_bounds__(64 * kShWaves) void gemm_midgroup_shared_kernel(const MidParams p) {
+    constexpr int R = 16, CPW = kShCPW, C = 16 * CPW * kShWaves, D = kShD, P = kShP;
+    static_assert(P % 2 == 0 && D == 4, "the unrolled step indexes the rings statically");
+    extern __shared__ float smem[];
+    // [NG][16] activation scales, [NG][16] ksums, [NG][128] weight scales,
+    // [NG][128] zero points
+    float* s_as = smem;
+    int* s_ak = reinterpret_cast<int*>(s_as + p.NG * R);
+    float* s_ws = reinterpret_cast<float*>(s_ak + p.NG * R);
+    float* s_wz = s_ws + p.NG * C;
+    // two steps of two tiles, each tile [plane][row][64 B]; thread tid stages
+    // the 16 bytes at tid * 16 of a step
+    __shared__ __attribute__((aligned(16))) uint8_t ring[2][4096];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nbw = blockIdx.x * (kShWaves * CPW);
+    const int q = lane >> 4;
+    const int rowq = 4 * q;
+    const int colq = lane & 15;
+
+    for (int e = tid; e < p.NG * R; e += blockDim.x) {
+        const int g = e / R, r = e - g * R;
+        const bool ok = r < p.Ma;
+        s_as[e] = ok ? bf16_bits_to_f32(p.a_scale[static_cast<int64_t>(g) * p.ld_as + r]) : 0.0f;
+        s_ak[e] = ok ? p.a_ksum[static_cast<int64_t>(g) * p.ld_as + r] : 0;
+    }
+    for (int e = tid; e < p.NG * C; e += blockDim.x) {
+        const int g = e / C, cc = e - g * C;
+        const int col = nbw * 16 + cc;
+        const bool ok = col < p.N;
+        s_ws[e] = ok ? bf16_bits_to_f32(p.w_scale[static_cast<int64_t>(g) * p.N + col]) : 0.0f;
+        s_wz[e] = (ASYM && ok) ? bf16_bits_to_f32(p.w_zero[static_cast<int64_t>(g) * p.N + col]) : 0.0f;
+    }
+
+    uint32_t wo[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int col = (nbw + wave * CPW + c) * 16 + colq;
+        wo[c] = col < p.N ? static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 16u * q : kOOBm;
+    }
+    uint4 wb[D][CPW];
+    auto load_w = [&](int s, int t) {
+        const uint32_t base = static_cast<uint32_t>(min(t, p.KT - 1)) * 64u;
+        const bool half = q >= 2 && (p.kpad - t * 128) < 128;
+        const auto rw = make_rsrc_at(p.w_q, base, t < p.KT ? p.w_bytes : 0u);
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, half ? kOOBm : wo[c]);
+    };
+    // this thread's 16 staged bytes: tile tid >> 7 of the step, plane
+    // (tid >> 6) & 1, row (tid >> 2) & 15, quad tid & 3
+    const int sts = tid >> 7;
+    const int srow = (tid >> 2) & 15;
+    const uint8_t* splane = ((tid >> 6) & 1) ? p.a_lo : p.a_hi;
+    const uint32_t soff = srow < p.Ma ? static_cast<uint32_t>(srow) * static_cast<uint32_t>(p.kb) + 16u * (tid & 3)
+                                      : kOOBm;
+    auto load_a = [&](int step) {
+        const int t = 2 * step + sts;
+        const auto r = make_rsrc_at(splane, static_cast<uint32_t>(min(t, p.KT - 1)) * 64u, t < p.KT ? p.a_bytes : 0u);
+        return buf_load16(r, soff);
+    };
+
+    float acc[CPW][4];
+    v4i Pm[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        Pm[c] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[c][i] = 0.0f;
+    }
+    auto fold = [&](int g) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const int cw = (wave * CPW + c) * 16 + colq;
+            const float ws = s_ws[g * C + cw];
+            const int wz = ASYM ? static_cast<int>(s_wz[g * C + cw]) : 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = rowq + i;
+                const int I = (Pm[c][i] >> 4) + (ASYM ? wz * s_ak[g * R + r] : 0);
+                if constexpr (DUMP) {
+                    const int col = nbw * 16 + cw;
+                    if (r < p.Ma && col < p.N) p.P[(static_cast<int64_t>(g) * p.Ma + r) * p.N + col] = I;
+                }
+                const float t1 = __fmul_rn(static_cast<float>(I), ws);
+                acc[c][i] = __fadd_rn(acc[c][i], __fmul_rn(t1, s_as[g * R + r]));
+            }
+            Pm[c] = v4i{0, 0, 0, 0};
+        }
+    };
+
+    const int nsteps = (p.KT + 1) / 2;
+    uint4 ga[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) ga[i] = load_a(i);
+#pragma unroll
+    for (int s = 0; s < D; ++s) load_w(s, s);
+    *reinterpret_cast<uint4*>(&ring[0][tid * 16]) = ga[0];
+    ga[0] = load_a(P);
+    __syncthreads();   // staged scales and step 0
+
+    for (int s0 = 0; s0 < nsteps; s0 += P) {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int s = s0 + i;
+            if (s >= nsteps) break;
+            const uint8_t* slot = ring[i & 1];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int t = 2 * s + u;
+                if (t >= p.KT) break;
+                const int ws_slot = (2 * i + u) % D;
+                v4i bw[CPW][2];
+#pragma unroll
+                for (int c = 0; c < CPW; ++c) {
+                    const uint4 w = wb[ws_slot][c];
+                    bw[c][0] = v4i{unpack_lo4(w.x), unpack_hi4(w.x), unpack_lo4(w.y), unpack_hi4(w.y)};
+                    bw[c][1] = v4i{unpack_lo4(w.z), unpack_hi4(w.z), unpack_lo4(w.w), unpack_hi4(w.w)};
+                }
+                const uint4 h = *reinterpret_cast<const uint4*>(slot + u * 2048 + colq * 64 + q * 16);
+                const uint4 l = *reinterpret_cast<const uint4*>(slot + u * 2048 + 1024 + colq * 64 + q * 16);
+                int e[4], o[4];
+                act_pair(h.x, l.x, e[0], o[0]);
+                act_pair(h.y, l.y, e[1], o[1]);
+                act_pair(h.z, l.z, e[2], o[2]);
+                act_pair(h.w, l.w, e[3], o[3]);
+                const v4i av0 = v4i{e[0], o[0], e[1], o[1]};
+                const v4i av1 = v4i{e[2], o[2], e[3], o[3]};
+                load_w(ws_slot, t + D);
+#pragma unroll
+                for (int c = 0; c < CPW; ++c) Pm[c] = mfma16(av0, bw[c][0], Pm[c]);
+#pragma unroll
+                for (int c = 0; c < CPW; ++c) Pm[c] = mfma16(av1, bw[c][1], Pm[c]);
+                if ((t + 1) % p.tpg == 0 || t == p.KT - 1) fold(t / p.tpg);
+            }
+            // step s + 1 into the other slot (read last in step s - 1, which
+            // every wave finished before the previous barrier)
+            *reinterpret_cast<uint4*>(&ring[(i + 1) & 1][tid * 16]) = ga[(i + 1) % P];
+            ga[(i + 1) % P] = load_a(s + 1 + P);
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = rowq + i, col = (nbw + wave * CPW + c) * 16 + colq;
+            if (row < p.Ma && col < p.N)
+                p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[c][i]));
+        }
+}
+
 // Variants (rows x columns per workgroup, load depth, most waves):
 //   Ma <= 16       16 x 32, depth 4, up to 12 waves (decode)
 //   Ma <= 64       64 x 32, depth 2, up to 8 waves
@@ -288,8 +454,25 @@ bool mid_wide_fits(const MidParams& p) {
     return static_cast<size_t>(p.NG) * (2 * 64 + 2 * 64) * sizeof(float) + 64 * 64 * sizeof(float) <= kMidLdsLimit;
 }
 
+// Shapes for the shared-activation decode kernel: up to 16 rows on N wide
+// enough that the per-wave plan walks K in one wave (>= 512 workgroups of two
+// column blocks), with the staged scales within 56 KiB.
+bool mid_shared_fits(const MidParams& p) {
+    return p.Ma <= 16 && (p.NB + 1) / 2 >= 512 &&
+           static_cast<size_t>(p.NG) * (2 * 16 + 2 * 16 * kShCPW * kShWaves) * sizeof(float) <= 56 * 1024;
+}
+
+template <bool ASYM, bool DUMP>
+hipError_t launch_shared(const MidParams& p, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(p.NG) * (2 * 16 + 2 * 16 * kShCPW * kShWaves) * sizeof(float);
+    const dim3 grid(static_cast<unsigned>((p.NB + kShWaves * kShCPW - 1) / (kShWaves * kShCPW)));
+    gemm_midgroup_shared_kernel<ASYM, DUMP><<<grid, dim3(64 * kShWaves), lds, stream>>>(p);
+    return hipGetLastError();
+}
+
 template <bool ASYM, bool DUMP>
 hipError_t launch_mt(const MidParams& p, int kw, hipStream_t stream) {
+    if (mid_shared_fits(p)) return launch_shared<ASYM, DUMP>(p, stream);
     if (p.Ma <= 16) return launch_mid<1, 2, ASYM, DUMP>(p, kw, stream);
     if (p.Ma <= 64 || !mid_wide_fits(p)) return launch_mid<4, 2, ASYM, DUMP>(p, kw, stream);
     return launch_mid<4, 4, ASYM, DUMP>(p, kw, stream);
