@@ -45,6 +45,7 @@ def test_version_and_sizes(lib):
     assert lib.w4a8_gemm_workspace_bytes(16, 5120, 5120, 128) == 0
     assert lib.w4a8_gemm_workspace_bytes(8, 5120, 27648, 128) == 0
     assert lib.w4a8_gemm_workspace_bytes(64, 5120, 27648, 128) == 6 * 64 * 5120 * 4
+    assert lib.w4a8_gemm_workspace_bytes(48, 5120, 27648, 128) == 6 * 48 * 5120 * 4   # split 64-row prefill tile
     assert lib.w4a8_gemm_workspace_bytes(24, 5120, 27648, 128) == 8 * 24 * 5120 * 4
     assert lib.w4a8_gemm_workspace_bytes(12, 5120, 27648, 128) == 12 * 12 * 5120 * 4
     assert lib.w4a8_gemm_workspace_bytes(20, 1000, 16384, 128) == 16 * 20 * 1008 * 4

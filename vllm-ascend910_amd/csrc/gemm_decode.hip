@@ -210,9 +210,8 @@ DecodeConfig rows_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     return c;
 }
 
-}  // namespace
-
-DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
+// The plans without the split prefill tiles.
+DecodeConfig base_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     // Picked from sweeps over ring depths, column blocks per workgroup, waves
     // per workgroup and K splits on MI355X at the QwQ-32B projection shapes.
     const int mt = static_cast<int>((M + 15) / 16);
@@ -243,12 +242,37 @@ DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
     return rows_config(M, N, K, group);
 }
 
+}  // namespace
+
+DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group) {
+    DecodeConfig c = base_config(M, N, K, group);
+    const int64_t KT = geom::k_tiles(K, group);
+    // Narrow N with long K past 32 rows at group stride 128: one 64-row tile
+    // of the prefill kernel's 128 x 32 wave tiles, K split so that the
+    // workgroups cover about 15/16 of the CUs once (down_proj on MI355X: six
+    // splits of 36 steps, 240 workgroups).  Cold, us, against the wide layout
+    // split six ways: M=48 27.5 -> 24.0, M=64 28.8 -> 25.3; at 24 and 32 rows
+    // it loses (23.7 -> 25.9, 24.3 -> 26.1), as it does on qkv/o at 24-64 rows
+    // (short K: 12.6 -> 14.8 on qkv M=64 at its best split).
+    if (c.WIDE && c.SPLITS > 1 && M > 32 && geom::group_stride(group) == 128) {
+        const int64_t tn = geom::ceil_div(N, int64_t{128});
+        const int64_t target = device_cu_count() * 15 / 16;
+        const int64_t s = std::min<int64_t>({(target + tn / 2) / tn, KT / 8, int64_t{16}});
+        if (s > 1) c.PSPLIT = static_cast<int>(s);
+    }
+    return c;
+}
+
 int64_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
     const DecodeConfig c = decode_config(M, N, K, group);
-    return c.WIDE && c.SPLITS > 1 ? wide_workspace_bytes(M, N, K, group, c.SPLITS) : 0;
+    const int64_t fb = c.WIDE && c.SPLITS > 1 ? wide_workspace_bytes(M, N, K, group, c.SPLITS) : 0;
+    return c.PSPLIT ? std::max(fb, prefill_split_workspace_bytes(M, N, K, group, c.PSPLIT)) : fb;
 }
 
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream) {
+    // the split prefill tiles have no SwiGLU pairs and no partial dump: those
+    // calls take the fallback plan held in the other fields
+    if (cfg.PSPLIT && !a.swiglu && !a.partials) return launch_gemm_prefill_split(a, cfg.PSPLIT, stream);
     if (cfg.WIDE) {
         if (!a.swiglu || wide_layout_pairs(cfg.WIDE)) return launch_gemm_wide(a, cfg.WIDE, cfg.SPLITS, stream);
         // the one-block layouts have no SwiGLU pairs: the decode kernel's plan

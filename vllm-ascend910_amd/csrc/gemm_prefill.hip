@@ -29,6 +29,8 @@
 // matrix cores.  At group 128 each row block's fold is interleaved with the
 // other row block's MFMAs (one MFMA, eight fold instructions), so one wave
 // keeps both pipes busy.
+#include <algorithm>
+
 #include "common.h"
 #include "kgeom.h"
 #include "launch.h"
@@ -89,6 +91,9 @@ struct PrefillParams {
     bool vec_out;      // y 16-byte aligned with ldy % 8 == 0: 16-byte output stores
     int bm;            // tile rows: 128 or 64
     bool cols;         // group stride 128 at 128 rows: 128 x 32 wave tiles (gemm_prefill_cols_kernel)
+    int splits;        // gemm_prefill_cols_kernel: workgroups along K (blockIdx.y); > 1 writes fp32 sums to R
+    float* R;          // splits > 1: fp32 sums before the token scale [splits, M, ldr]
+    int64_t ldr;       // NB * 16
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
@@ -549,6 +554,11 @@ __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_prefill_cols_kerne
     const int n0 = tile_n * kBN;
     const int c32 = lane & 31;
     const int hh = lane >> 5;
+    // This workgroup's K steps [ka, ka + nk): the KT steps split evenly over
+    // p.splits workgroups (the host keeps splits <= KT; one step is one group).
+    const int ks = static_cast<int>(blockIdx.y);
+    const int ka = (ks * p.KT) / p.splits;
+    const int nk = ((ks + 1) * p.KT) / p.splits - ka;
 
     const auto ra_rsrc = make_rsrc(p.A, p.a_bytes);
     const auto rw_rsrc = make_rsrc(p.W, p.w_bytes);
@@ -576,7 +586,7 @@ __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_prefill_cols_kerne
         aoffg[i] = static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(p.lda) + static_cast<uint32_t>(q) * 16u;
     }
     auto load_a = [&](int kt, int b) {
-        const uint32_t k = static_cast<uint32_t>(min(kt, p.KT - 1)) * 128u;
+        const uint32_t k = static_cast<uint32_t>(ka + min(kt, nk - 1)) * 128u;
         int8_t* const dst = abuf(b) + NA * 1024 * wave;
 #pragma unroll
         for (int i = 0; i < NA; ++i)
@@ -584,14 +594,14 @@ __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_prefill_cols_kerne
     };
     uint4 wr[kDW][2];
     auto load_w = [&](int slot, int kt) {
-        const uint32_t t = static_cast<uint32_t>(min(kt, p.KT - 1)) * 1024u;
+        const uint32_t t = static_cast<uint32_t>(ka + min(kt, nk - 1)) * 1024u;
         wr[slot][0] = buf_load16(rw_rsrc, woff0 + t);
         wr[slot][1] = buf_load16(rw_rsrc, woff1 + t);
     };
     // group stride 128: step kt is group kt (the padding half of a last step
     // meets zero weights)
     auto load_s = [&](int kt) -> uint32_t {
-        const int g = min(min(kt, p.KT - 1), p.NG - 1);
+        const int g = min(ka + min(kt, nk - 1), p.NG - 1);
         return buf_load_u16(rs_rsrc, soff + static_cast<uint32_t>(g) * 32u);
     };
 
@@ -673,20 +683,36 @@ __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_prefill_cols_kerne
         wait_vm_barrier<2 * (NA + 3)>();
     };
     int kt = 0;
-    for (; kt + kNB <= p.KT; kt += kNB) {
+    for (; kt + kNB <= nk; kt += kNB) {
 #pragma unroll
         for (int u = 0; u < kNB; ++u) one(kt + u, u);
     }
 #pragma unroll
     for (int u = 0; u < kNB - 1; ++u)
-        if (kt + u < p.KT) one(kt + u, u);
+        if (kt + u < nk) one(kt + u, u);
     fold(RB - 1, scp);   // the last step's last row block
 
     // ---- epilogue: as in gemm_prefill_kernel, through the first two A buffers
     constexpr int OC = kBN;
     constexpr int OS = out_stride<BM, false>();
     constexpr int RPA = kBM / 2;
-    wait_vm_barrier<0>();
+    wait_vm_barrier<0>();   // also: no load into LDS outlives the workgroup
+    if (p.splits > 1) {
+        // this split's fp32 sums, before the token scale, for wide_reduce_kernel
+        // (which adds the splits in index order, scales and rounds)
+        const int col = n0 + wave * 32 + c32;
+        if (col < p.N) {
+            float* const r = p.R + static_cast<int64_t>(ks) * p.M * p.ldr + col;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = m0 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
+                    if (row < p.M) r[static_cast<int64_t>(row) * p.ldr] = acc[rb][i];
+                }
+        }
+        return;
+    }
     auto orow = [&](int r) -> uint16_t* {
         return reinterpret_cast<uint16_t*>(r < RPA ? la0 : la1) + (r % RPA) * OS;
     };
@@ -775,6 +801,59 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     return launch_gemm_prefill_bm(a, prefill_tile_rows(a.M, a.N, a.group, a.swiglu), stream);
 }
 
+// Decode-sized row counts (up to 64) on narrow N: one 64-row tile of the
+// 128 x 32 wave kernel spans few workgroups (40 on o_proj), so K is split
+// over `splits` workgroups (group stride 128: every step is one group) and
+// wide_reduce_kernel adds the fp32 split sums in index order, scales by the
+// token scale and rounds -- the same reduction as the wide kernel's K split.
+int64_t prefill_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int splits) {
+    const int64_t s = std::min<int64_t>(splits, geom::k_tiles(K, group));
+    return s > 1 ? s * M * geom::col_blocks(N) * 16 * 4 : 0;
+}
+
+hipError_t launch_gemm_prefill_split(const GemmArgs& a, int splits, hipStream_t stream) {
+    if (a.swiglu || a.partials || geom::group_stride(a.group) != 128 || a.M <= 0 || a.M > 64 || splits < 1)
+        return hipErrorInvalidValue;
+    const int64_t need = prefill_split_workspace_bytes(a.M, a.N, a.K, a.group, splits);
+    if (need > 0 && (a.workspace == nullptr || a.workspace_bytes < need)) return hipErrorInvalidValue;
+    PrefillParams p{};
+    p.A = a.a_q;
+    p.lda = a.lda;
+    p.a_scale = a.a_scale;
+    p.W = reinterpret_cast<const uint4*>(a.w_tiles);
+    p.S = a.s_tiles;
+    p.Y = a.y;
+    p.ldy = a.ldy;
+    p.M = static_cast<int>(a.M);
+    p.N = static_cast<int>(a.N);
+    p.K = static_cast<int>(a.K);
+    p.KT = static_cast<int>(geom::k_tiles(a.K, a.group));
+    p.NG = static_cast<int>(geom::num_groups(a.K, a.group));
+    p.NB = static_cast<int>(geom::col_blocks(a.N));
+    p.gs = 128;
+    p.kpad = static_cast<int>(geom::kpad(a.K, a.group));
+    p.tpg = 1;
+    p.bm = 64;
+    p.tiles_m = 1;
+    p.tiles_n = static_cast<int>(geom::ceil_div(a.N, kBN));
+    p.band = 4;
+    p.a_bytes = static_cast<uint32_t>((a.M - 1) * a.lda + p.kpad);
+    p.w_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::k_tiles(a.K, a.group) * geom::kTileBytes);
+    p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
+    p.vec_out = (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (a.ldy % 8 == 0);
+    p.cols = true;
+    p.splits = need > 0 ? static_cast<int>(std::min<int64_t>(splits, p.KT)) : 1;
+    p.R = static_cast<float*>(a.workspace);
+    p.ldr = static_cast<int64_t>(p.NB) * 16;
+    const dim3 grid(static_cast<unsigned>(p.tiles_n), static_cast<unsigned>(p.splits));
+    if (a.scale_bf16) gemm_prefill_cols_kernel<true, 64><<<grid, dim3(256), 0, stream>>>(p);
+    else gemm_prefill_cols_kernel<false, 64><<<grid, dim3(256), 0, stream>>>(p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.splits == 1) return e;
+    return launch_split_reduce(p.R, p.ldr, p.a_scale, p.Y, p.ldy, p.M, p.N, p.splits, false, a.scale_bf16, p.S,
+                               nullptr, stream);
+}
+
 hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream) {
     if (bm != 64 && bm != 128) return hipErrorInvalidValue;
     PrefillParams p{};
@@ -808,6 +887,7 @@ hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream)
     p.s_bytes = static_cast<uint32_t>(geom::col_blocks(a.N) * geom::num_groups(a.K, a.group) * 16 * 2);
     p.vec_out = (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (a.ldy % 8 == 0);
     p.cols = W4A8_PREFILL_COLS != 0;
+    p.splits = 1;
     if (a.swiglu) return a.scale_bf16 ? launch<true, false, true>(p, stream) : launch<false, false, true>(p, stream);
     const bool dump = a.partials != nullptr;
     if (a.scale_bf16) return dump ? launch<true, true, false>(p, stream) : launch<true, false, false>(p, stream);

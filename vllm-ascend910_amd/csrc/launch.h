@@ -52,6 +52,7 @@ struct DecodeConfig {
     int WIDE = 0;     // a WideLayout: the LDS-shared-activation kernel (gemm_wide.hip); D/CPW/KW/MT unused
     int SPLITS = 1;   // WIDE: workgroups along K (fp32 sums in the workspace, reduced by a second kernel)
     int STAGE = 0;    // 1: staged activations and scales (M <= 8, MT = 1, D = 4, CPW 1 or 2)
+    int PSPLIT = 0;   // > 0: launch_gemm_prefill_split with this many K splits (other fields: the fallback plan)
 };
 DecodeConfig decode_config(int64_t M, int64_t N, int64_t K, int64_t group);
 hipError_t launch_gemm_decode_cfg(const GemmArgs& a, const DecodeConfig& cfg, hipStream_t stream);
@@ -96,6 +97,11 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
 // height launch_gemm_prefill picks.
 hipError_t launch_gemm_prefill_bm(const GemmArgs& a, int bm, hipStream_t stream);
 int prefill_tile_rows(int64_t M, int64_t N, int64_t group, bool swiglu);
+// Up to 64 rows at group stride 128 (no SwiGLU, no partial dump): one 64-row
+// tile of the 128 x 32 wave prefill kernel with K split over `splits`
+// workgroups, then wide_reduce_kernel (splits > 1).
+int64_t prefill_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int splits);
+hipError_t launch_gemm_prefill_split(const GemmArgs& a, int splits, hipStream_t stream);
 
 
 // Mid-group compat path (the reference's midgroup_quant_a / midgroup_w4a8_gemm).
