@@ -358,8 +358,9 @@ def main():
     if traffic_src.exists():
         traffic = round(json.loads(traffic_src.read_text())["avg_traffic_bytes"])
     result["roofline"] = {
-        "kernel": ("decode W4A8 GEMM per call: gemm_decode_kernel; gemm_wide_kernel for gate_up and down at M=16 "
-                   "and 64, down followed by wide_reduce_kernel (K split over 12 / 6 workgroups) -- all 16 configs[1] "
+        "kernel": ("decode W4A8 GEMM per call: gemm_decode_kernel; gemm_wide_kernel for gate_up at M=16 and 64 "
+                   "and down at M=16 (K split over 12 workgroups), gemm_prefill_cols_kernel's 64-row tile for down at M=64 (K split "
+                   "over 6 workgroups), each split call followed by wide_reduce_kernel -- all 16 configs[1] "
                    "shapes, cold"),
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -762,11 +763,12 @@ def pmc_summary(fetch_db, write_db, out_json=None):
     ff = cal_kib / [v for n, v in fetch if is_copy(n)][-1]
     fw = cal_kib / [v for n, v in write if is_copy(n)][-1]
     def per_call(events):
-        # a call = its gemm_decode_kernel / gemm_wide_kernel dispatch plus the
+        # a call = its gemm_decode_kernel / gemm_wide_kernel dispatch (the probe's
+        # only prefill-kernel dispatches are down_proj's split 64-row tiles) plus the
         # wide_reduce_kernel that follows it when K is split over workgroups
         out = []
         for n, v in events:
-            if "gemm_decode_kernel" in n or "gemm_wide_kernel" in n:
+            if "gemm_decode_kernel" in n or "gemm_wide_kernel" in n or "gemm_prefill_cols_kernel" in n:
                 out.append(v)
             elif "wide_reduce_kernel" in n and out:
                 out[-1] += v
