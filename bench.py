@@ -730,16 +730,21 @@ def trace_summary(db):
         if k.startswith(("gemm_", "linear_", "quant_", "wide_")):
             print(f"| {k} | {st} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
     # One decode GEMM call = one gemm_decode_kernel or gemm_wide_kernel
-    # dispatch, plus a wide_reduce_kernel when it splits K over workgroups.
+    # dispatch, or one gemm_prefill_cols_kernel dispatch split along K (grid
+    # y > 1: the 64-row tile down_proj runs at 33-64 rows), plus the
+    # wide_reduce_kernel that follows a call splitting K over workgroups (as
+    # pmc_summary counts them).
     calls, total = collections.Counter(), collections.Counter()
-    for (k, st), d in by_stream.items():
-        if k in ("gemm_decode_kernel", "gemm_wide_kernel"):
-            calls[st] += len(d)
-        if k in ("gemm_decode_kernel", "gemm_wide_kernel", "wide_reduce_kernel"):
-            total[st] += sum(d)
+    for name, dur, gx, gy, wx, stream in rows:
+        k = name.split("(")[0].split("<")[0].split("::")[-1]
+        is_call = k in ("gemm_decode_kernel", "gemm_wide_kernel") or (k == "gemm_prefill_cols_kernel" and gy > 1)
+        if is_call:
+            calls[stream] += 1
+        if is_call or k == "wide_reduce_kernel":
+            total[stream] += dur
     for st in sorted(calls):
-        print(f"| decode GEMM per call (gemm_decode_kernel / gemm_wide_kernel + wide_reduce_kernel) | {st} | "
-              f"{calls[st]} | {total[st] / calls[st] / 1e3:.3f} |")
+        print(f"| decode GEMM per call (gemm_decode_kernel / gemm_wide_kernel / split gemm_prefill_cols_kernel + "
+              f"wide_reduce_kernel) | {st} | {calls[st]} | {total[st] / calls[st] / 1e3:.3f} |")
     print("\n| kernel | grid x (threads) | grid y | workgroup | calls | avg us |\n|---|---:|---:|---:|---:|---:|")
     for (k, gx, gy, wx), d in sorted(by_shape.items()):
         if k.startswith(("gemm_", "linear_", "quant_", "wide_")):

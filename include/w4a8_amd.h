@@ -46,11 +46,22 @@ enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
 
 /* Library ABI version (bumped on any signature or contract change: 4 = the
  * first build whose GEMM asks a workspace of some decode shapes; 5 adds
- * w4a8_rope_kv). */
+ * w4a8_rope_kv; 6 adds w4a8_stream_capture_id and requires 4-byte aligned
+ * s_tiles). */
 int w4a8_abi_version(void);
 
 /* Message for the calling thread's last failed call ("" if none). */
 const char* w4a8_last_error(void);
+
+/*
+ * The capture sequence id of a stream that is being captured into a HIP graph
+ * (hipStreamGetCaptureInfo of the HIP runtime this library is bound to, which
+ * is the one the process loaded): W4A8_OK and *id, or W4A8_ERR_UNSUPPORTED when
+ * the stream is not capturing.  No counterpart in the reference; for callers
+ * that key per-capture GEMM workspaces (the torch layer does) without binding
+ * the HIP runtime by a file name of their own.
+ */
+int w4a8_stream_capture_id(void* stream, unsigned long long* id);
 
 /*
  * Dynamic per-token int8 activation quant.
@@ -123,7 +134,8 @@ int64_t w4a8_gemm_row_chunk(int64_t M, int64_t lda);
  *                               padding slots may hold any value (they meet
  *                               zero weight codes)
  *   a_scale  bf16 [M]
- *   w_tiles, s_tiles            (from w4a8_repack; scale_dtype as repacked)
+ *   w_tiles, s_tiles            (from w4a8_repack; scale_dtype as repacked;
+ *                               w_tiles 16-byte and s_tiles 4-byte aligned)
  *   y        bf16 [M, ldy]      output
  * Calls whose activations exceed 32-bit offsets ((M + 128) * lda >= 2^31) run
  * as several launches over row chunks (w4a8_gemm_row_chunk); the debug
@@ -234,9 +246,10 @@ int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t
  *   bias     bf16 [(H + 2 KVH) * D] or NULL: the projection bias, added first as
  *                                torch adds two bf16 tensors, x = bf16(x + bias)
  *   cos_tab, sin_tab  fp32 [L, ldc]   angle tables (columns 0 .. D/2-1 used)
- *   pos      int64 (device)      position of token 0 of every sequence; token t
- *                                sits at pos[0] + t (read on the device, so a
- *                                captured decode step follows it)
+ *   pos      int64 [1] (device)  the position of token 0, shared by all B
+ *                                sequences; token t sits at pos[0] + t (read on
+ *                                the device, so a captured decode step follows
+ *                                it).  Per-sequence positions are not supported.
  *   q_out    bf16 [B * T, H, D]  rotated q
  *   k_cache  element (b, h, d, p) at k_strides . (b, h, d, p): rotated k written at p
  *   v_cache  element (b, h, p, d) at v_strides . (b, h, p, d): v copied at p

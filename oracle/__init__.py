@@ -25,7 +25,8 @@ How each function is pinned (tests/test_oracle.py):
                             the reference's C++ (packing, plane split, ksums,
                             geometry, the three GEMM orders) written by
                             tests/golden/make_golden.py, checked on CPU and GPU
-  * torch addcmul_ FMA   -- parity unpinned at the last fp32 bit (whether
-    contraction             ATen fuses acc + partial*s is not fixed); covered by
-                            the bf16 output tolerance instead
+  * torch addcmul_ FMA   -- fma32 (one rounding of acc + partial*s) equals
+    contraction             torch CPU's addcmul_ on every element of random and
+                            broadcast cases, and exact rational rounding
+                            (tests/test_oracle.py)
 """

@@ -211,12 +211,40 @@ def group_partials(a_q: np.ndarray, w_codes: np.ndarray, group: int, exact_int64
     return out
 
 
+def fma32(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """fp32 fused multiply-add: a*b + c with one IEEE round-to-nearest-even.
+
+    torch's CPU ``Tensor.addcmul_`` (the reference's accumulation,
+    fakequant_lab/fake_linear.py:178) evaluates acc + t1*t2 this way.  The
+    product of two fp32 values is exact in float64 (48 significant bits); the
+    sum with c is rounded to float64 and its error recovered exactly (TwoSum);
+    rounding the float64 sum to fp32 then equals rounding the exact value
+    except when the sum sits exactly on an fp32 midpoint, where the sign of the
+    error decides.  Finite inputs.
+    """
+    a64 = np.asarray(a, dtype=np.float32).astype(np.float64)
+    b64 = np.asarray(b, dtype=np.float32).astype(np.float64)
+    c64 = np.asarray(c, dtype=np.float32).astype(np.float64)
+    p = a64 * b64
+    s = p + c64
+    bb = s - p
+    e = (p - (s - bb)) + (c64 - bb)
+    r = s.astype(np.float32)
+    up = r.astype(np.float64) > s
+    lo = np.where(up, np.nextafter(r, np.float32(-np.inf)), r)
+    hi = np.where(up, r, np.nextafter(r, np.float32(np.inf)))
+    mid = (lo.astype(np.float64) + hi.astype(np.float64)) * 0.5 == s
+    r = np.where(mid & (e > 0), hi, np.where(mid & (e < 0), lo, r))
+    return r.astype(np.float32)
+
+
 def gemm_fp32(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_scale: np.ndarray,
               group: int, partials: Optional[np.ndarray] = None, return_abs: bool = False):
     """The reference's kernel-mode GEMM in fp32, per-token activation scale.
 
     fakequant_lab/fake_linear.py:166-179: for g in order,
-        acc += partial_g * (a_s[:, g] * w_s[:, g])        (fp32; a_s*w_s is exact)
+        acc.addcmul_(partial_g, a_s[:, g] * w_s[:, g])    (fp32; a_s*w_s is exact;
+                                                          addcmul_ rounds once, fma32)
     with the per-token a_s broadcast over groups (run_selftest.py:104-120 iterates
     the groups of the weight spec).  ``w_scale`` is [N, G] fp32 values (bf16 or
     fp16 scales, both exact in fp32).  Returns fp32 [M, N]; with ``return_abs``
@@ -237,10 +265,10 @@ def gemm_fp32(a_q: np.ndarray, a_scale_bits: np.ndarray, w_codes: np.ndarray, w_
             sl = slice(g * group, g * group + group_real(g, K, group))
             pg = a_q[:, sl].astype(np.float32) @ w_codes[:, sl].astype(np.float32).T
         s = (a_s[:, None] * w_scale[:, g].astype(np.float32)[None, :]).astype(np.float32)
-        term = (pg.astype(np.float32) * s).astype(np.float32)
-        acc = (acc + term).astype(np.float32)
+        # acc.addcmul_(partial, s): one rounding of acc + partial * s (fma32)
+        acc = fma32(pg.astype(np.float32), s, acc)
         if return_abs:
-            mag += np.abs(term.astype(np.float64))
+            mag += np.abs(pg.astype(np.float64) * s.astype(np.float64))
     return (acc, mag) if return_abs else acc
 
 

@@ -106,6 +106,8 @@ CASES = {
     "gemm_m16_wide_n": ("gemm_wide_kernel, 16 rows", _gemm_case(16, 32768, 1024, 128, 5)),
     "gemm_m64_wide_n": ("gemm_wide_kernel, 64 rows", _gemm_case(64, 32768, 1024, 128, 6)),
     "gemm_m16_long_k": ("gemm_wide_kernel K split + wide_reduce_kernel", _gemm_case(16, 1024, 16384, 128, 7)),
+    "gemm_m48_long_k_psplit": ("gemm_prefill_cols_kernel 64-row tile K split + wide_reduce_kernel",
+                               _gemm_case(48, 1000, 16384, 128, 17)),
     "linear_m1_qkv_proj": ("linear_decode_kernel (fused quant)", _gemm_case(1, 7168, 5120, 128, 8, op="linear")),
     "swiglu_m16": ("SwiGLU epilogue", _gemm_case(16, 2048, 1024, 128, 9, op="swiglu")),
     "gemm_m4_perchannel": ("one group over K", _gemm_case(4, 5120, 5120, 5120, 10)),

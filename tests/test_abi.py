@@ -32,7 +32,7 @@ def test_header_symbols_are_exported(pkg, lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.w4a8_abi_version() == 5
+    assert lib.w4a8_abi_version() == 6
     # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
     assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
@@ -70,6 +70,8 @@ def _gemm(lib, **kw):
     (dict(lda=100), 2, "lda"),
     (dict(lda=264), 4, "16-byte"),
     (dict(a_q=24), 4, "16-byte"),
+    # the wide decode layouts read two columns' scales as one dword
+    (dict(s_tiles=18), 4, "s_tiles 4-byte aligned"),
     # a decode shape that splits K over workgroups needs its workspace
     (dict(M=12, N=5120, K=27648, lda=27648, ldy=5120), 6, "workspace needs 2949120 bytes"),
     (dict(M=12, N=5120, K=27648, lda=27648, ldy=5120, ws=256, wsb=2949119), 6, "workspace"),
@@ -79,6 +81,14 @@ def test_gemm_rejects_bad_arguments(lib, kw, code, msg):
     # Fake, never-dereferenced addresses: validation fails before any launch.
     assert _gemm(lib, **kw) == code
     assert msg in lib.w4a8_last_error().decode()
+
+
+def test_stream_capture_id_rejects_null_and_idle_streams(lib):
+    assert lib.w4a8_stream_capture_id(None, None) == 1
+    # the null stream is never being captured; on a host without a GPU the
+    # runtime query itself fails, which is reported as a HIP error
+    cid = ctypes.c_ulonglong(0)
+    assert lib.w4a8_stream_capture_id(None, ctypes.byref(cid)) in (5, 7)
 
 
 def test_m0_is_a_noop(lib):

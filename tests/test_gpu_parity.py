@@ -499,11 +499,13 @@ def test_gemm_every_decode_row_count(pkg, dev):
             check_output(tensor_bf16_bits(y)[:, cols], y32, f"M{M} N{N} K{K}", exact_sym(q_ref, s_ref, w[cols], ws32[cols], G))
 
 
-@pytest.mark.parametrize("M,N,K", [(16, 5120, 5120), (16, 5120, 27648), (1024, 7168, 5120)])
+@pytest.mark.parametrize("M,N,K", [(16, 5120, 5120), (16, 5120, 27648), (48, 5120, 27648), (64, 5120, 27648),
+                                   (1024, 7168, 5120)])
 def test_gemm_deterministic_and_stress(pkg, dev, M, N, K):
     """Repeated launches give identical bits (the reference's --stress relaunch check,
     int4_cube_lab/host/mg_harness.h:307-334): the decode kernel's in-workgroup K split,
     the K split over workgroups with its reduce kernel and workspace (down_proj M=16),
+    the 64-row prefill tile split along K with the same reduce (down_proj M=48 and 64),
     and a prefill shape; every relaunch is compared, and the first against the oracle."""
     G = 128
     say(f"gemm stress M={M} N={N} K={K}")
@@ -521,6 +523,32 @@ def test_gemm_deterministic_and_stress(pkg, dev, M, N, K):
     q_ref, s_ref = ow.quant_act_per_token(xb)
     y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G)
     check_output(tensor_bf16_bits(first)[:, cols], y32, f"stress M{M} N{N} K{K}",
+                 exact_sym(q_ref, s_ref, w[cols], ws32[cols], G))
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 5120, 27648), (48, 5120, 27648), (40, 1000, 16384)])
+def test_gemm_split_prefill_tile_equals_fallback_plan(pkg, dev, M, N, K):
+    """Narrow N with long K past 32 rows runs one 64-row tile of the prefill kernel
+    split along K (gemm_prefill_cols_kernel + wide_reduce_kernel).  The partial dump
+    runs that shape on the fallback wide plan instead, whose K split has the same
+    boundaries and the same per-group fold order: the two outputs must be equal bit
+    for bit, the dumped int32 partials must equal the oracle's exactly, and the
+    output meets the bars."""
+    G = 128
+    say(f"split prefill tile vs fallback M={M} N={N} K={K}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + 31)
+    y_fb, P, a_q, a_s = run_hip(dev, xb, w, w_scale, N, K, G, partials=True)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(torch.from_numpy(ow.pack_grouped(w, G)).to(dev),
+                                                 w_scale.to(dev), K, G)
+    y = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_fb.view(torch.int16)), "split prefill tile differs from the wide plan"
+    cols = np.sort(np.random.default_rng(M).choice(N, 96, replace=False))
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    Pn = P.cpu().numpy()
+    assert np.array_equal(Pn[:, :, cols], ow.group_partials(q_ref, w[cols], G)), "dumped partials differ"
+    y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G)
+    check_output(tensor_bf16_bits(y)[:, cols], y32, f"split prefill tile M{M} N{N} K{K}",
                  exact_sym(q_ref, s_ref, w[cols], ws32[cols], G))
 
 
@@ -1015,6 +1043,29 @@ def test_rmsnorm_quant(pkg, dev, M, K, G, with_res):
     q, sc = ow.quant_act_per_token(hg)
     assert np.array_equal(tensor_bf16_bits(a_s), sc)
     assert np.array_equal(a_q.cpu().numpy(), ow.pad_groups(q, G) if G else q)
+
+
+@pytest.mark.parametrize("K", [5120, 4096, 3072])
+def test_rmsnorm_quant_rows_do_not_depend_on_batch(pkg, dev, K):
+    """A row's outputs are the same bytes whatever the batch: up to 64 rows the launch
+    gives each thread one 8-element unit (512 or 1024 threads at these K), past 64 rows
+    256 threads with two to four units each, and the sum of squares is one tree over the
+    unit index either way.  Rows 0..63 of a 65-row call equal those of a 64-row call
+    (and of one-row calls), with and without the residual add."""
+    say(f"rmsnorm_quant batch independence K={K}")
+    rng = np.random.default_rng(K)
+    xb = pkg.synth.activations(65, K, seed=K + 1)
+    rb = ow.f32_to_bf16_bits(rng.standard_normal((65, K)).astype(np.float32))
+    wb = ow.f32_to_bf16_bits(rng.uniform(0.5, 1.5, K).astype(np.float32))
+    x, w, r = bf16_bits_tensor(xb).to(dev), bf16_bits_tensor(wb).to(dev), bf16_bits_tensor(rb).to(dev)
+    for res in (None, r):
+        outs = {}
+        for M in (65, 64, 1):
+            outs[M] = torch.ops.npu.w4a8_rmsnorm_quant(x[:M], w, 1e-6, None if res is None else res[:M], 128, True)
+        torch.cuda.synchronize()
+        for t65, t64, t1 in zip(outs[65], outs[64], outs[1]):
+            assert torch.equal(t65[:64].view(torch.int8).cpu(), t64.view(torch.int8).cpu()), "rows differ, M=64 vs 65"
+            assert torch.equal(t65[:1].view(torch.int8).cpu(), t1.view(torch.int8).cpu()), "row 0 differs, M=1 vs 65"
 
 
 # ------------------------------------------------------------------ checkpoint formats

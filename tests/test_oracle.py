@@ -254,6 +254,83 @@ def test_gemm_fp32_close_to_float64_definition():
 
 
 @needs_ref
+def _round_f32_exact(v: Fraction) -> np.float32:
+    """Round an exact rational to fp32, ties to even (normal range)."""
+    f = np.float32(float(v))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    dist = [abs(Fraction(float(c)) - v) for c in cands]
+    best = min(dist)
+    ties = [c for c, d in zip(cands, dist) if d == best]
+    if len(ties) == 1:
+        return ties[0]
+    return [c for c in ties if (np.array(c, np.float32).view(np.uint32) & 1) == 0][0]
+
+
+def test_fma32_matches_torch_addcmul():
+    """fake_linear.py:178 accumulates with acc.addcmul_(partial, a_s*w_s): on torch's
+    CPU path that is one rounding of acc + partial*s.  fma32 equals it on every element,
+    in the reference's broadcast form too; the two-rounding evaluation does not."""
+    rng = np.random.default_rng(11)
+    n = 1 << 18
+    acc = (rng.standard_normal(n) * 1000).astype(np.float32)
+    p = rng.integers(-130000, 130000, n).astype(np.float32)
+    sc = (rng.uniform(0.002, 0.02, n) * rng.uniform(0.001, 0.05, n)).astype(np.float32)
+    t = torch.from_numpy(acc.copy())
+    t.addcmul_(torch.from_numpy(p), torch.from_numpy(sc))
+    assert np.array_equal(ow.fma32(p, sc, acc), t.numpy())
+    two = (acc + (p * sc).astype(np.float32)).astype(np.float32)
+    assert np.mean(two != t.numpy()) > 0.01, "negative control: unfused evaluation must differ"
+    M, N = 32, 2048
+    acc2 = (rng.standard_normal((M, N)) * 100).astype(np.float32)
+    P = rng.integers(-130000, 130000, (M, N)).astype(np.float32)
+    a_s = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+    w_s = rng.uniform(0.002, 0.02, (1, N)).astype(np.float32)
+    t2 = torch.from_numpy(acc2.copy())
+    t2.addcmul_(torch.from_numpy(P), torch.from_numpy(a_s) * torch.from_numpy(w_s))
+    assert np.array_equal(ow.fma32(P, (a_s * w_s).astype(np.float32), acc2), t2.numpy())
+
+
+def test_fma32_matches_rational_rounding():
+    """Exact rational a*b + c rounded once to fp32, on random operands and on sums built
+    to land exactly on an fp32 midpoint (where a float64 sum alone would round twice)."""
+    rng = np.random.default_rng(12)
+    a = rng.integers(-130000, 130000, 600).astype(np.float32)
+    b = rng.uniform(1e-5, 1e-3, 600).astype(np.float32)
+    c = (rng.standard_normal(600) * 50).astype(np.float32)
+    # a*b an exact fp32 midpoint (3 * (1 + odd * 2^-23) has 25 significant bits); c = +-2^-100
+    # leaves the float64 sum on the midpoint while the exact value is off it, c = 0 is a tie
+    for i in range(300):
+        a[i] = np.float32(3.0)
+        b[i] = np.float32(1.0 + 2.0 ** -23 * (2 * int(rng.integers(0, 1 << 20)) + 1))
+        c[i] = np.float32((0.0, 2.0 ** -100, -(2.0 ** -100))[i % 3])
+    got = ow.fma32(a, b, c)
+    for i in range(600):
+        want = _round_f32_exact(Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i])))
+        assert got[i] == want, (i, a[i], b[i], c[i], got[i], want)
+    # the constructed cases do need the midpoint rule: rounding the float64 sum alone
+    # gets the nonzero-c ones wrong whenever ties-to-even points the other way (about half)
+    naive = (a[:300].astype(np.float64) * b[:300] + c[:300]).astype(np.float32)
+    assert np.sum(naive != got[:300]) >= 50
+
+
+def test_gemm_fp32_equals_reference_torch_loop():
+    """gemm_fp32 is the reference's kernel-mode loop run on torch's CPU path (the
+    fake_linear.py:166-179 statement sequence on int8 codes and fp32 scales), bit for bit."""
+    rng = np.random.default_rng(13)
+    M, N, K, G = 6, 40, 512, 128
+    q = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    w = rng.integers(-8, 8, (N, K)).astype(np.int8)
+    sb = ow.f32_to_bf16_bits((rng.uniform(0.001, 0.05, M)).astype(np.float32))
+    ws = rng.uniform(0.002, 0.02, (N, K // G)).astype(np.float16).astype(np.float32)
+    a_s = torch.from_numpy(ow.bf16_bits_to_f32(sb))
+    acc = torch.zeros((M, N), dtype=torch.float32)
+    for g in range(K // G):
+        sl = slice(g * G, (g + 1) * G)
+        partial = torch.from_numpy(q[:, sl].astype(np.float32)) @ torch.from_numpy(w[:, sl].astype(np.float32)).T
+        acc.addcmul_(partial, a_s[:, None] * torch.from_numpy(ws[:, g])[None, :])
+    assert np.array_equal(ow.gemm_fp32(q, sb, w, ws, G), acc.numpy())
+
+
 def test_gemm_bf16_matches_reference_cpp():
     for seed, (M, N, K, G) in enumerate(((8, 64, 512, 128), (16, 128, 5120 // 4, 256), (4, 32, 1024, 64))):
         xb, w, wsb = _gemm_case(seed + 10, M, N, K, G)

@@ -15,7 +15,7 @@ from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "_lib" / "libw4a8_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1
@@ -26,6 +26,7 @@ _VP, _I64, _I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
 SIGNATURES = {
     "w4a8_abi_version": (_I, []),
     "w4a8_last_error": (ctypes.c_char_p, []),
+    "w4a8_stream_capture_id": (_I, [_VP, ctypes.POINTER(ctypes.c_ulonglong)]),
     "w4a8_quant_act": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I64, _I64, _VP]),
     "w4a8_repacked_weight_bytes": (_I64, [_I64, _I64, _I64]),
     "w4a8_repacked_scale_bytes": (_I64, [_I64, _I64, _I64]),

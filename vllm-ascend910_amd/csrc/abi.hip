@@ -97,8 +97,10 @@ int check_gemm(const void* a_q, int64_t lda, const void* a_scale, const void* w_
         return fail(W4A8_ERR_SHAPE, "lda=%lld must be >= kpad=%lld and ldy=%lld >= the output width", lda, kp, ldy);
     if (lda % 16 != 0 || !aligned(a_q, 16))
         return fail(W4A8_ERR_ALIGN, "a_q must be 16-byte aligned with lda %% 16 == 0 (lda=%lld)", lda);
-    if (!aligned(w_tiles, 16) || !aligned(s_tiles, 2) || !aligned(y, 2) || !aligned(a_scale, 2))
-        return fail(W4A8_ERR_ALIGN, "w_tiles must be 16-byte aligned; s_tiles, y, a_scale 2-byte aligned");
+    // s_tiles: the wide decode layouts load the group scales of two columns
+    // as one dword (gemm_wide.hip), so 4-byte alignment is part of the contract
+    if (!aligned(w_tiles, 16) || !aligned(s_tiles, 4) || !aligned(y, 2) || !aligned(a_scale, 2))
+        return fail(W4A8_ERR_ALIGN, "w_tiles must be 16-byte aligned, s_tiles 4-byte aligned; y, a_scale 2-byte aligned");
     // The kernels address the weight tiles with 32-bit buffer offsets,
     // including up to one tile past the end, and mark out-of-range reads with
     // an offset of 2^31 added on top (every path: the fused single-row linear too).
@@ -206,9 +208,22 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 5; }
+int w4a8_abi_version(void) { return 6; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
+
+int w4a8_stream_capture_id(void* stream, unsigned long long* id) {
+    if (id == nullptr) return fail(W4A8_ERR_NULL, "id is NULL");
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (int rc = hip_status(hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &st, &cid),
+                            "hipStreamGetCaptureInfo"))
+        return rc;
+    if (st != hipStreamCaptureStatusActive)
+        return fail(W4A8_ERR_UNSUPPORTED, "stream is not being captured (capture status %lld)", static_cast<long long>(st));
+    *id = cid;
+    return W4A8_OK;
+}
 
 int w4a8_quant_act(const void* x, int64_t ldx, void* a_q, int64_t lda, void* a_scale, int64_t M,
                    int64_t K, int64_t group, void* stream) {

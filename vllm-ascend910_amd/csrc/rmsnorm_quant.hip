@@ -7,9 +7,13 @@
 //   r      = 1 / sqrt(mean(float(s)^2) + eps)            fp32, IEEE sqrt and divide
 //   h      = bf16( float(bf16(float(s) * r)) * float(w) )  the reference's two bf16 roundings
 //   a_q, a_scale = per-token quant of h      (quant_act.hip semantics, quant.py:89-141)
-// The sum of squares is taken per thread, then across the workgroup in a fixed
-// tree, so results are deterministic; its order differs from torch's
-// vectorised mean, which moves r by at most an fp32 ulp.  Optionally writes s
+// The sum of squares is one fixed tree over the row's 8-element units: each
+// unit's squares are added in element order, then units u and u ^ 2^b are
+// paired for b = 0, 1, 2, ... (units past the row add exact zeros).  The tree
+// depends only on the unit index, not on how units are spread over threads,
+// so a row's result does not depend on the launch shape the batch size
+// selects; its order differs from torch's vectorised mean, which moves r by
+// at most an fp32 ulp.  Optionally writes s
 // (the updated residual stream) and h.  One workgroup per row, the row held in
 // registers (256 threads up to 8192 elements -- one 8-element unit per thread
 // for up to 64 rows -- and 1024 threads up to 65536).
@@ -45,17 +49,41 @@ struct RmsParams {
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
 
-template <int NT>
-__device__ __forceinline__ float block_sum_f(float v, float* red) {
+// Sum of the VPT per-unit partials v[i] of every thread, where thread t holds
+// unit t + i NT: unit-index bits 0-5 are the lane (xor shuffles, bit 0 first),
+// the next log2(NT / 64) bits the wave, the bits above the register index i
+// -- so pairing lanes, then waves, then registers, each in increasing bit
+// order, is the tree over the unit index, for every NT.
+template <int VPT, int NT>
+__device__ __forceinline__ float block_sum_units(float (&v)[VPT], float* red) {
+    constexpr int NW = NT / 64;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float s = red[0];
+    for (int i = 0; i < VPT; ++i)
 #pragma unroll
-    for (int i = 1; i < NT / 64; ++i) s += red[i];
+        for (int off = 1; off < 64; off <<= 1) v[i] += __shfl_xor(v[i], off, 64);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) red[i * NW + (threadIdx.x >> 6)] = v[i];
+    }
     __syncthreads();
-    return s;
+    float r[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        float w[NW];
+#pragma unroll
+        for (int k = 0; k < NW; ++k) w[k] = red[i * NW + k];
+#pragma unroll
+        for (int st = 1; st < NW; st <<= 1)
+#pragma unroll
+            for (int k = 0; k + st < NW; k += 2 * st) w[k] += w[k + st];
+        r[i] = w[0];
+    }
+#pragma unroll
+    for (int st = 1; st < VPT; st <<= 1)
+#pragma unroll
+        for (int i = 0; i + st < VPT; i += 2 * st) r[i] += r[i + st];
+    __syncthreads();
+    return r[0];
 }
 
 template <int NT>
@@ -74,7 +102,8 @@ __device__ __forceinline__ uint32_t block_max_u(uint32_t v, uint32_t* red) {
 // VPT units of 8 elements per thread; K % 8 == 0, rows 16-byte aligned.
 template <int VPT, int NT, bool RES>
 __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const RmsParams p) {
-    __shared__ float redf[NT / 64];
+    static_assert((VPT & (VPT - 1)) == 0 && (NT & (NT - 1)) == 0, "power-of-two units and threads");
+    __shared__ float redf[VPT * NT / 64];
     __shared__ uint32_t redu[NT / 64];
     const int64_t row = blockIdx.x;
     const int nvec = p.K >> 3;
@@ -92,7 +121,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const RmsParams p) {
     }
     // s = bf16(x + r) kept as packed bf16 pairs; per-thread sum of squares
     uint4 v[VPT];
-    float ss = 0.0f;
+    float ss[VPT];
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = static_cast<int>(threadIdx.x) + i * NT;
@@ -114,14 +143,15 @@ __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const RmsParams p) {
         }
         v[i] = a;
         const uint32_t* pa = reinterpret_cast<const uint32_t*>(&v[i]);
+        ss[i] = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const float e0 = __uint_as_float(pa[d] << 16), e1 = __uint_as_float(pa[d] & 0xffff0000u);
-            ss = fmaf(e0, e0, ss);
-            ss = fmaf(e1, e1, ss);
+            ss[i] = fmaf(e0, e0, ss[i]);
+            ss[i] = fmaf(e1, e1, ss[i]);
         }
     }
-    const float tot = block_sum_f<NT>(ss, redf);
+    const float tot = block_sum_units<VPT, NT>(ss, redf);
     const float r = 1.0f / sqrtf(tot / static_cast<float>(p.K) + p.eps);
 
     // h = bf16(bf16(s * r) * w); absmax of h

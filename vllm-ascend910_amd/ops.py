@@ -88,22 +88,14 @@ _CAPTURE_WS: Dict[Tuple[int, int], torch.Tensor] = {}
 # to the caching allocator (nor may a capture's own workspace).
 _RETIRED: list = []
 
-_hip = None
-
-
 def _capture_id(stream_handle: int) -> int:
-    """The HIP capture sequence id of a stream that is being captured (the
-    runtime torch loaded, found by its soname)."""
-    global _hip
-    if _hip is None:
-        _hip = ctypes.CDLL("libamdhip64.so.7")
-        _hip.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
-                                                 ctypes.POINTER(ctypes.c_ulonglong)]
-        _hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
-    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
-    rc = _hip.hipStreamGetCaptureInfo(ctypes.c_void_p(stream_handle), ctypes.byref(status), ctypes.byref(cid))
-    if rc != 0 or status.value != 1:
-        raise RuntimeError(f"w4a8: could not read the capture id of stream {stream_handle:#x} (rc {rc})")
+    """The HIP capture sequence id of a stream that is being captured, asked
+    through the W4A8 library (bound to the HIP runtime the process loaded)."""
+    cid = ctypes.c_ulonglong(0)
+    rc = _abi.lib().w4a8_stream_capture_id(ctypes.c_void_p(stream_handle), ctypes.byref(cid))
+    if rc != 0:
+        raise RuntimeError(f"w4a8: could not read the capture id of stream {stream_handle:#x}: "
+                           f"{_abi.lib().w4a8_last_error().decode('utf-8', 'replace')}")
     return int(cid.value)
 
 
@@ -371,8 +363,9 @@ def _rope_kv_cuda(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: 
         _require(t.dim() == 2 and t.dtype == torch.float32 and t.shape[0] >= L and t.shape[1] >= D // 2
                  and t.stride(1) == 1, f"w4a8_rope_kv: {name} must be float32 [>= L, >= head_dim / 2]")
     _require(cos.stride(0) == sin.stride(0), "w4a8_rope_kv: cos and sin must share a row stride")
-    _require(pos.dtype == torch.int64 and pos.numel() >= 1 and pos.device == qkv.device,
-             "w4a8_rope_kv: pos must be an int64 tensor on the device")
+    _require(pos.dtype == torch.int64 and pos.numel() == 1 and pos.device == qkv.device,
+             "w4a8_rope_kv: pos must be one int64 on the device (the position of token 0, shared by every "
+             "sequence; per-sequence positions are not supported)")
     if qkv.stride(2) != 1 or qkv.stride(0) != T * qkv.stride(1):
         qkv = qkv.contiguous()
     if bias is not None:
