@@ -28,6 +28,7 @@ reported in the same JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -69,11 +70,14 @@ def main():
                     help="skip configs[4]: the 64-layer QwQ-32B-shaped decoder, 1024-token prompts + "
                          "--decoder-steps greedy decode steps at concurrency 1, 8, 64 (run by default)")
     ap.add_argument("--decoder-layers", type=int, default=64)
-    ap.add_argument("--decoder-steps", type=int, default=64)
-    ap.add_argument("--compat", action="store_true",
-                    help="also time the reference-compat mid-group pair (group 1024, asymmetric) at M 1/16/64/1024")
-    ap.add_argument("--config4", action="store_true",
-                    help="also time configs[3]: groups 64/256/512 at M 16/4096, gate_up with the fused SwiGLU")
+    ap.add_argument("--decoder-steps", type=int, default=256,
+                    help="greedy decode steps per concurrency (configs[4] states 256)")
+    ap.add_argument("--no-compat", action="store_true",
+                    help="skip the reference-compat mid-group pair (group 1024, asymmetric) at M 1/16/64/1024/4096")
+    ap.add_argument("--no-config4", action="store_true",
+                    help="skip configs[3]: groups 64/256/512 at M 16/4096, gate_up with the fused SwiGLU")
+    ap.add_argument("--no-tp4", action="store_true",
+                    help="skip the tensor-parallel shard shapes (TP=4 slices of the four projections)")
     ap.add_argument("--no-perchannel", action="store_true",
                     help="skip the per-channel (group = K) points beside the reference's published ones")
     ap.add_argument("--no-detail", action="store_true", help="only the timed steps (for profiling)")
@@ -141,9 +145,10 @@ def main():
     # ---------------------------------------------------------------- data
     gen = torch.Generator(device=dev)
 
-    def make_pool(p, G, codes_dist, scale_dtype, seed):
-        """>= 8 distinct repacked copies of projection p's weight, >= cold_bytes in total."""
-        K, N = synth.QWQ_SHAPES[p]
+    def make_pool(p, G, codes_dist, scale_dtype, seed, shape=None):
+        """>= 8 distinct repacked copies of projection p's weight (or of a [N, K] = shape
+        slice), >= cold_bytes in total."""
+        K, N = shape if shape is not None else synth.QWQ_SHAPES[p]
         per = gemm_bytes(0, N, K, G)
         n = max(8, math.ceil(args.cold_bytes * 2 ** 30 / per))
         pool = []
@@ -292,6 +297,7 @@ def main():
         return sorted(times)[len(times) // 2]
 
     shapes = []
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
     floors = {}
     reads = {}
     copy_dst = {}
@@ -323,17 +329,21 @@ def main():
                 for i in range(T):
                     copy_dst[p].copy_(weights[p][i % len(weights[p])][0])
 
-            def stock_reads(p=p):
-                # the same pool rotation read by a stock torch reduction (amax over the
-                # weight tiles as int32): what stock code reads at each weight size
+            def floor_read(p=p):
+                # the same pool rotation streamed by the library's read-floor kernel
+                # (w4a8_read_floor): the time the weight tiles take to read, nothing else
+                lib = pkg._abi.lib()
+                st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
                 for i in range(T):
-                    torch.amax(weights[p][i % len(weights[p])][0].view(torch.int32))
+                    wt = weights[p][i % len(weights[p])][0]
+                    pkg._abi.check(lib.w4a8_read_floor(wt.data_ptr(), wt.numel(), sink.data_ptr(), st),
+                                   "w4a8_read_floor")
 
             us = time_graph(gemms) / T
             qus = time_graph(quants) / T
             fus = time_graph(floor_reads) / T if M == DECODE_MS[0] else floors[p]
             floors[p] = fus
-            rus = time_graph(stock_reads) / T if M == DECODE_MS[0] else reads[p]
+            rus = time_graph(floor_read) / T if M == DECODE_MS[0] else reads[p]
             reads[p] = rus
             # quant + GEMM through w4a8_linear, on the step's stream
             lus = time_graph(linears, stream=torch.cuda.current_stream(dev)) / T
@@ -346,11 +356,12 @@ def main():
                            "gemm_GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                            "TOPS": round(2 * M * N * K / us / 1e6, 2), "quant_us": round(qus, 3),
                            "linear_us": round(lus, 3), "linear_fused": fused,
-                           "copy_us": round(fus, 3), "stock_read_us": round(rus, 3)})
+                           "copy_us": round(fus, 3), "read_floor_us": round(rus, 3),
+                           "vs_read_floor": round(rus / us, 4)})
             cgb = 2 * weights[p][0][0].numel() / fus / 1e3
             log(f"  {p:13s} M={M:3d}: gemm {us:8.2f} us {b / us / 1e3:7.1f} GB/s ({b / us / 1e3 / HBM_PEAK_GBS:.1%})"
                 f"  quant {qus:6.2f} us  linear {lus:7.2f} us{' (fused)' if fused else ''}  "
-                f"copy {fus:6.2f} us ({cgb:6.0f} GB/s)  read {rus:6.2f} us")
+                f"copy {fus:6.2f} us ({cgb:6.0f} GB/s)  read floor {rus:6.2f} us ({rus / us:.0%} of gemm time)")
     achieved = tot_bytes / tot_us / 1e3
     # HBM bytes per launch from the two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) recorded in
     # profiles/ (the command is in the summary), each scaled by a 256 MiB copy's reading.
@@ -375,12 +386,14 @@ def main():
                  "the GEMMs: what stock code moves at each weight size, cold reads plus writes"),
         "us": {p: round(floors[p], 3) for p in PROJS},
         "GBs_read_plus_write": {p: round(2 * weights[p][0][0].numel() / floors[p] / 1e3, 1) for p in PROJS}}
-    result["stock_read"] = {
-        "what": ("per projection, a stock torch reduction (torch.amax over the int32 view) of each pool copy's "
-                 "repacked weight tiles, graph-replayed back to back over the same rotation as the GEMMs: how "
-                 "fast stock code reads the weight bytes alone, cold"),
+    result["read_floor"] = {
+        "what": ("per projection, the library's streaming-read kernel (w4a8_read_floor: 256-thread workgroups, "
+                 "two 16-byte non-temporal loads per thread) over each pool copy's repacked weight tiles, "
+                 "graph-replayed back to back over the same rotation as the GEMMs: the time the weight bytes "
+                 "alone take to read cold; decode_shapes[*].vs_read_floor = read_floor_us / gemm_us"),
         "us": {p: round(reads[p], 3) for p in PROJS},
-        "GBs": {p: round(weights[p][0][0].numel() / reads[p] / 1e3, 1) for p in PROJS}}
+        "GBs": {p: round(weights[p][0][0].numel() / reads[p] / 1e3, 1) for p in PROJS},
+        "hbm_frac": {p: round(weights[p][0][0].numel() / reads[p] / 1e3 / HBM_PEAK_GBS, 4) for p in PROJS}}
     result["gpu_clocks"] = {"after_timed_region": clocks,
                             "note": "rocm-smi reading; the peaks above are MI355X's published figures (2.4 GHz)"}
 
@@ -455,10 +468,13 @@ def main():
     if not args.no_perchannel:
         result["perchannel_shapes"] = perchannel(pkg, dev, synth, make_pool, time_graph, T)
     # ---------------------------------------------------------------- mid-group variants
-    if args.config4:
+    if not args.no_config4:
         result["config4_shapes"] = config4(pkg, dev, synth, make_pool, time_graph, T)
-    if args.compat:
+    if not args.no_compat:
         result["compat_shapes"] = compat(pkg, dev, synth, time_graph, T, args.cold_bytes)
+    # ---------------------------------------------------------------- TP=4 shard shapes (one GPU's slice)
+    if not args.no_tp4:
+        result["tp4_shapes"] = tp4(pkg, dev, synth, make_pool, time_graph, T)
     # ---------------------------------------------------------------- decoder forward
     if not args.no_decoder:
         result["decoder"] = decoder_bench(pkg, dev, args.decoder_layers, steps=args.decoder_steps)
@@ -658,6 +674,68 @@ def perchannel(pkg, dev, synth, make_pool, time_graph, T, ms=(1, 4, 16, 64, 1024
     return rows
 
 
+# The reference's published mid-group W4A8 kernel times on its 910B4 (group 1024,
+# asymmetric weights, per-(token, group) activation scales: the compat pair's
+# arithmetic), int4_cube_lab/results/midgroup_w4a8_qwen.csv rows "w4a8_mg_asym".
+REF_MIDGROUP_US = {
+    ("qkv_proj", 1): (31.12, 4), ("qkv_proj", 16): (31.07, 10), ("qkv_proj", 64): (40.65, 13),
+    ("qkv_proj", 1024): (274.92, 22),
+    ("o_proj", 1): (26.33, 25), ("o_proj", 16): (26.27, 31), ("o_proj", 64): (32.67, 34),
+    ("o_proj", 1024): (197.95, 43),
+    ("gate_up_proj", 1): (148.48, 46), ("gate_up_proj", 16): (148.41, 52), ("gate_up_proj", 64): (206.43, 55),
+    ("gate_up_proj", 1024): (2225.47, 64),
+    ("down_proj", 1): (76.23, 67), ("down_proj", 16): (76.13, 73), ("down_proj", 64): (108.13, 76),
+    ("down_proj", 1024): (1012.92, 85),
+}
+
+
+# Tensor-parallel shards at TP=4 of QwQ-32B's projections (one GPU's slice;
+# the reference's open question about its kernel at per-rank shapes,
+# MGCKPT/P7_LOWDIM_KERNEL.md:13-21): column-parallel qkv/gate_up split N,
+# row-parallel o/down split K.  (K, N) per projection.
+TP4_SHAPES = {"qkv_proj": (5120, 1792), "o_proj": (1280, 5120), "gate_up_proj": (5120, 13824),
+              "down_proj": (6912, 5120)}
+
+
+def tp4(pkg, dev, synth, make_pool, time_graph, T, ms=(1, 16, 64, 1024)):
+    """One GPU's TP=4 slice of every projection, group 128, cold pools, through w4a8_linear
+    (quant + GEMM) and the GEMM alone."""
+    import numpy as np
+    import torch
+    rows = []
+    for pi, p in enumerate(PROJS):
+        K, N = TP4_SHAPES[p]
+        pool = make_pool(p, GROUP, "uniform", torch.float16, 90000 + 100 * pi, shape=(K, N))
+        for M in ms:
+            x = torch.from_numpy(synth.activations(M, K, seed=M + 70).view(np.int16)).view(torch.bfloat16).to(dev)
+            a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x)
+            Tm = T if M <= 64 else max(2, T // 8)
+
+            def gemms(a_q=a_q, a_s=a_s, K=K, N=N, Tm=Tm):
+                for i in range(Tm):
+                    wt, st = pool[i % len(pool)]
+                    torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP)
+
+            def linears(x=x, K=K, N=N, Tm=Tm):
+                for i in range(Tm):
+                    wt, st = pool[i % len(pool)]
+                    torch.ops.npu.w4a8_linear(x, wt, st, N, K, GROUP)
+
+            us, lus = time_graph(gemms) / Tm, time_graph(linears) / Tm
+            b = gemm_bytes(M, N, K)
+            tops = 2 * M * N * K / us / 1e6
+            rows.append({"proj": p, "shard": "N/4" if p in ("qkv_proj", "gate_up_proj") else "K/4", "M": M,
+                         "N": N, "K": K, "gemm_us": round(us, 3), "linear_us": round(lus, 3),
+                         "GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                         "TOPS": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)})
+            log(f"  tp4 {p:13s} N={N:5d} K={K:5d} M={M:5d}: gemm {us:9.2f} us {b / us / 1e3:7.1f} GB/s "
+                f"({b / us / 1e3 / HBM_PEAK_GBS:.1%}) {tops:7.1f} TOPS  linear {lus:9.2f} us")
+            del x, a_q, a_s
+        del pool
+        torch.cuda.empty_cache()
+    return rows
+
+
 def compat(pkg, dev, synth, time_graph, T, cold_bytes):
     """The reference-compat pair (midgroup_quant_a + midgroup_w4a8_gemm, group 1024, asymmetric) on
     the reference's packed tensors, cold pools as for the main path."""
@@ -695,9 +773,15 @@ def compat(pkg, dev, synth, time_graph, T, cold_bytes):
             Mp = a[0].shape[0]
             b = N * kb + ng * N * 6 + Mp * kb * 2 + ng * Mp * 6 + 2 * Mp * N
             tops = 2 * M * N * K / us / 1e6
-            rows.append({"proj": p, "M": M, "gemm_us": round(us, 2), "GBs": round(b / us / 1e3, 1),
-                         "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "TOPS": round(tops, 1),
-                         "mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "quant_a_us": round(qus, 2)})
+            row = {"proj": p, "M": M, "gemm_us": round(us, 2), "GBs": round(b / us / 1e3, 1),
+                   "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "TOPS": round(tops, 1),
+                   "mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "quant_a_us": round(qus, 2)}
+            if (p, M) in REF_MIDGROUP_US:
+                ref_us, line = REF_MIDGROUP_US[(p, M)]
+                row.update(reference_910b4_us=ref_us,
+                           reference_source=f"int4_cube_lab/results/midgroup_w4a8_qwen.csv:{line}",
+                           speedup_vs_reference=round(ref_us / us, 2))
+            rows.append(row)
             log(f"  compat {p:13s} M={M:5d}: gemm {us:9.2f} us {b / us / 1e3:7.1f} GB/s "
                 f"({b / us / 1e3 / HBM_PEAK_GBS:.1%}) {tops:7.1f} TOPS  quant_a {qus:7.2f} us")
             del x, a

@@ -64,6 +64,15 @@ const char* w4a8_last_error(void);
 int w4a8_stream_capture_id(void* stream, unsigned long long* id);
 
 /*
+ * Measurement kernel (no counterpart in the reference): a plain streaming
+ * read of [src, src + bytes), bytes % 16 == 0, src 16-byte aligned, sink a
+ * 4-byte device word written only for one improbable fold of the data.  The
+ * bench times it over the same cold weight rotation as the decode GEMMs, as
+ * the read floor those GEMMs are compared with.
+ */
+int w4a8_read_floor(const void* src, int64_t bytes, void* sink, void* stream);
+
+/*
  * Dynamic per-token int8 activation quant.
  *   x       bf16 [M, ldx]   (first K columns used)
  *   a_q     int8 [M, lda]   output: with group == 0 (or a geometry without

@@ -269,6 +269,73 @@ def test_qwq_width_layers_linears_match_oracle(pkg, dev, monkeypatch):
     assert rel < 2e-2, f"rel-L2 {rel}"
 
 
+def test_qwq_full_depth_concurrency8(pkg, dev, monkeypatch):
+    """configs[4] at its full depth: the 64-layer QwQ-32B-shaped decoder at concurrency 8
+    (8 prompts of 32 tokens: 256 prefill rows).  Every W4A8 linear of a sampled deep layer
+    inside the 64-layer prefill and the first decode step (8 rows) matches the oracle,
+    and four greedy decode steps replayed from the captured graph equal eager decode
+    (tokens and last logits)."""
+    D = pkg.decoder
+    cfg = D.DecoderConfig(layers=64)
+    layer = 41
+    say("decoder: QwQ-32B, 64 layers, concurrency 8")
+    m = D.W4A8Decoder(cfg, batch=8, max_len=40, device=dev, seed=17, keep_weights={layer})
+    sampled = {id(v) for v in m.layers[layer].values() if isinstance(v, D._Linear)}
+    assert len(sampled) == 4
+    calls = []
+    orig_gemm, orig_linear, orig_swiglu = D._Linear.gemm, D._Linear.linear, D._Linear.swiglu
+
+    def rec_gemm(self, a_q, a_s):
+        y = orig_gemm(self, a_q, a_s)
+        if id(self) in sampled:
+            calls.append((self, "gemm", (a_q.clone(), a_s.clone()), y.clone()))
+        return y
+
+    def rec_linear(self, x):
+        y = torch.ops.npu.w4a8_linear(x, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
+        if id(self) in sampled:
+            calls.append((self, "linear", x.clone(), y.clone()))
+        return y + self.bias if self.bias is not None else y
+
+    def rec_swiglu(self, a_q, a_s):
+        y = orig_swiglu(self, a_q, a_s)
+        if id(self) in sampled:
+            calls.append((self, "swiglu", (a_q.clone(), a_s.clone()), y.clone()))
+        return y
+
+    prompt = torch.randint(0, cfg.vocab, (8, 32), generator=torch.Generator().manual_seed(18)).to(dev)
+    monkeypatch.setattr(D._Linear, "gemm", rec_gemm)
+    monkeypatch.setattr(D._Linear, "linear", rec_linear)
+    monkeypatch.setattr(D._Linear, "swiglu", rec_swiglu)
+    first = m.prefill(prompt)
+    k0 = [k.clone() for k in m.k_cache]
+    v0 = [v.clone() for v in m.v_cache]
+    m.decode(first, 32, 1, graph=False)
+    torch.cuda.synchronize()
+    monkeypatch.setattr(D._Linear, "gemm", orig_gemm)
+    monkeypatch.setattr(D._Linear, "linear", orig_linear)
+    monkeypatch.setattr(D._Linear, "swiglu", orig_swiglu)
+    assert len(calls) == 2 * 4, len(calls)      # prefill + one decode step, 4 linears
+    say(f"  checking layer {layer}'s {len(calls)} linear calls against the oracle")
+    _check_linear_calls(pkg, calls)
+    del calls
+
+    def restore():
+        for k, kk in zip(m.k_cache, k0):
+            k.copy_(kk)
+        for v, vv in zip(m.v_cache, v0):
+            v.copy_(vv)
+
+    restore()
+    eager = m.decode(first, 32, 4, graph=False)
+    eager_logits = m.last_logits.clone()
+    restore()
+    graph = m.decode(first, 32, 4, graph=True)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(graph, eager)), "graph decode differs from eager"
+    assert torch.equal(m.last_logits, eager_logits), "graph logits differ from eager"
+
+
 def test_fused_score_scaling_equals_three_ops(dev):
     """The decoder's attention scores as one torch.add(bias, s, alpha=1/sqrt(D)) equal the
     separate s.float() * (1/sqrt(D)) + bias bit for bit when the bias holds only 0 and -inf

@@ -339,10 +339,12 @@ def test_gemm_qwq_prefill_column_sample(pkg, dev, proj):
     check_output(tensor_bf16_bits(y)[:, cols], y32, f"{proj} M{M}", exact_sym(q_ref, s_ref, w[cols], ws32[cols], 128))
 
 
-@pytest.mark.parametrize("M", [4096, 16384])
+@pytest.mark.parametrize("M", [4096, 16384, 65536])
 @pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
 def test_gemm_qwq_prefill_large_sample(pkg, dev, proj, M):
-    """configs[2]'s larger batches, M=4096 and 16384, at full shape and group 128; the
+    """configs[2]'s larger batches, M=4096 and 16384, and configs[4]'s prefill at
+    concurrency 64 (64 prompts of 1024 tokens: M=65536 through every linear), at full
+    shape and group 128; the
     oracle runs on 96 sampled rows x 160 sampled columns (per-token rows and output
     columns are independent), first and last row and column included."""
     synth = pkg.synth
@@ -454,6 +456,37 @@ def test_gemm_qwq_perchannel(pkg, dev, proj, M):
     y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], K)
     check_output(tensor_bf16_bits(y)[:, cols], y32, f"per-channel {proj} M{M}",
                  exact_sym(q_ref, s_ref, w[cols], ws32[cols], K))
+
+
+# One GPU's TP=4 slice of each QwQ-32B projection: column-parallel qkv/gate_up split N,
+# row-parallel o/down split K ((K, N) per projection; MGCKPT/P7_LOWDIM_KERNEL.md:13-21).
+TP4_SHAPES = {"qkv_proj": (5120, 1792), "o_proj": (1280, 5120), "gate_up_proj": (5120, 13824),
+              "down_proj": (6912, 5120)}
+
+
+@pytest.mark.parametrize("proj", sorted(TP4_SHAPES))
+@pytest.mark.parametrize("M", [1, 16, 64, 1024])
+def test_linear_tp4_shard_shapes(pkg, dev, proj, M):
+    """The TP=4 shard shapes at group 128 through w4a8_linear (quant + GEMM; one fused
+    launch at M=1), sampled columns against the oracle; the plain GEMM on the same
+    quantised rows returns the same bits."""
+    K, N = TP4_SHAPES[proj]
+    G = 128
+    say(f"tp4 shard {proj} M={M} N={N} K={K}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + K + N)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(torch.from_numpy(ow.pack_grouped(w, G)).to(dev),
+                                                 w_scale.to(dev), K, G)
+    x = bf16_bits_tensor(xb).to(dev)
+    y = torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, G)
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, G)
+    y2 = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), "linear differs from quant + gemm"
+    cols = np.sort(np.random.default_rng(M + 5).choice(N, 128, replace=False))
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    assert np.array_equal(a_q.cpu().numpy(), q_ref) and np.array_equal(tensor_bf16_bits(a_s), s_ref)
+    y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G)
+    check_output(tensor_bf16_bits(y)[:, cols], y32, f"tp4 {proj} M{M}", exact_sym(q_ref, s_ref, w[cols], ws32[cols], G))
 
 
 def test_gemm_perchannel_every_decode_row_count(pkg, dev):

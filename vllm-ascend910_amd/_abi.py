@@ -27,6 +27,7 @@ SIGNATURES = {
     "w4a8_abi_version": (_I, []),
     "w4a8_last_error": (ctypes.c_char_p, []),
     "w4a8_stream_capture_id": (_I, [_VP, ctypes.POINTER(ctypes.c_ulonglong)]),
+    "w4a8_read_floor": (_I, [_VP, _I64, _VP, _VP]),
     "w4a8_quant_act": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I64, _I64, _VP]),
     "w4a8_repacked_weight_bytes": (_I64, [_I64, _I64, _I64]),
     "w4a8_repacked_scale_bytes": (_I64, [_I64, _I64, _I64]),

@@ -212,6 +212,16 @@ int w4a8_abi_version(void) { return 6; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
+int w4a8_read_floor(const void* src, int64_t bytes, void* sink, void* stream) {
+    if (bytes < 0 || bytes % 16 != 0) return fail(W4A8_ERR_SHAPE, "bytes=%lld must be a multiple of 16", bytes);
+    if (bytes == 0) return W4A8_OK;
+    if (!src || !sink) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (!aligned(src, 16) || !aligned(sink, 4)) return fail(W4A8_ERR_ALIGN, "src must be 16-byte, sink 4-byte aligned");
+    if (bytes / 16 / 512 >= (1ll << 31)) return fail(W4A8_ERR_SHAPE, "bytes=%lld too large for one launch", bytes);
+    return hip_status(launch_read_floor(src, bytes, static_cast<uint32_t*>(sink), static_cast<hipStream_t>(stream)),
+                      "read_floor launch");
+}
+
 int w4a8_stream_capture_id(void* stream, unsigned long long* id) {
     if (id == nullptr) return fail(W4A8_ERR_NULL, "id is NULL");
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;

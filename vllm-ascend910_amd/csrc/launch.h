@@ -167,6 +167,10 @@ struct RopeKvArgs {
 };
 hipError_t launch_rope_kv(const RopeKvArgs& a, hipStream_t stream);
 
+// Streaming read of [src, src + bytes) (bytes a multiple of 16, src 16-byte
+// aligned); sink (4 bytes) is written only for one improbable fold value.
+hipError_t launch_read_floor(const void* src, int64_t bytes, uint32_t* sink, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace w4a8

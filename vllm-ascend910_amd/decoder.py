@@ -96,7 +96,9 @@ class W4A8Decoder:
     """The decoder with a static KV cache for ``batch`` sequences of up to ``max_len`` tokens."""
 
     def __init__(self, cfg: DecoderConfig, batch: int, max_len: int, device="cuda", seed: int = 0,
-                 keep_weights: bool = False):
+                 keep_weights=False):
+        """keep_weights: True keeps every linear's int8 codes and scales (reference
+        checks of small models), a collection of layer indices keeps those layers' only."""
         self.cfg, self.batch, self.max_len = cfg, batch, max_len
         dev = torch.device(device)
         self.device = dev
@@ -107,14 +109,15 @@ class W4A8Decoder:
         self.lm_head = (torch.randn((c.vocab, c.hidden), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
         self.final_norm = (1.0 + 0.1 * torch.randn((c.hidden,), device=dev, generator=gen)).to(torch.bfloat16)
         self.layers = []
-        for _ in range(c.layers):
+        for li in range(c.layers):
+            keep = keep_weights if isinstance(keep_weights, bool) else li in keep_weights
             self.layers.append({
                 "ln1": (1.0 + 0.1 * torch.randn((c.hidden,), device=dev, generator=gen)).to(torch.bfloat16),
                 "ln2": (1.0 + 0.1 * torch.randn((c.hidden,), device=dev, generator=gen)).to(torch.bfloat16),
-                "qkv": _Linear(c.qkv_out, c.hidden, c.group, gen, dev, bias=c.qkv_bias, keep=keep_weights),
-                "o": _Linear(c.hidden, c.heads * c.head_dim, c.group, gen, dev, keep=keep_weights),
-                "gate_up": _Linear(2 * c.ffn, c.hidden, c.group, gen, dev, keep=keep_weights),
-                "down": _Linear(c.hidden, c.ffn, c.group, gen, dev, keep=keep_weights),
+                "qkv": _Linear(c.qkv_out, c.hidden, c.group, gen, dev, bias=c.qkv_bias, keep=keep),
+                "o": _Linear(c.hidden, c.heads * c.head_dim, c.group, gen, dev, keep=keep),
+                "gate_up": _Linear(2 * c.ffn, c.hidden, c.group, gen, dev, keep=keep),
+                "down": _Linear(c.hidden, c.ffn, c.group, gen, dev, keep=keep),
             })
         kvh, d = c.kv_heads, c.head_dim
         # K stored transposed so that q @ K is a product of contiguous operands
