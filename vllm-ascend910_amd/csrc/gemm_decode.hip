@@ -12,9 +12,9 @@ namespace {
 
 using namespace dec;
 
-template <int KWMAX, int GM, bool SBF16>
+template <int KWMAX, int GM, bool SBF16, int QW>
 __global__ __launch_bounds__(64 * KWMAX) void linear_decode_kernel(const DecodeParams p) {
-    decode_body<1, 2, KWMAX, 4, GM, SBF16, false, false, 1>(p);
+    decode_body<1, 2, KWMAX, 4, GM, SBF16, false, false, 1, 0, QW>(p);
 }
 
 int gcd_i(int a, int b) {
@@ -84,7 +84,13 @@ DecodeParams make_params(const GemmArgs& a) {
 template <int GM, bool SBF16>
 hipError_t launch_fused_g(const DecodeParams& p, int kw, size_t lds, hipStream_t stream) {
     constexpr int KWM = kwmax_for(1, 2, 4);
-    linear_decode_kernel<KWM, GM, SBF16><<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
+    // rows of up to 8192 elements: every wave reads the whole row (16 chunks per lane at most)
+    if (p.K <= 64 * 8 * 10)
+        linear_decode_kernel<KWM, GM, SBF16, 10><<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
+    else if (p.K <= 64 * 8 * 16)
+        linear_decode_kernel<KWM, GM, SBF16, 16><<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
+    else
+        linear_decode_kernel<KWM, GM, SBF16, 0><<<dim3(static_cast<unsigned>(p.cgroups)), dim3(64 * kw), lds, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -106,13 +112,17 @@ struct FusedPlan {
 };
 
 bool plan_fused(const GemmArgs& a, const uint16_t* x, int64_t ldx, FusedPlan& f) {
-    // One row only: each workgroup quantises the rows of its K range, so the
-    // quant work is repeated per column group.  Measured on MI355X against
-    // the quant kernel + GEMM pair (graph replays, cold weights): qkv 8.4
-    // against 8.6 us, o 7.8 against 7.9, gate_up 24.8-25.0 against 27.6,
-    // down_proj (long K, eight waves of 27 tiles) 18.5 against 18.7 -- and one
-    // launch fewer where the linear runs inside a captured graph.  The
-    // four-row variant of the same kernel lost 2 us on qkv and o at M=4.
+    // One row only: every workgroup quantises the row again (each wave its
+    // own K range; up to 8192 elements each wave reads the whole row for the
+    // absmax, longer rows meet in LDS), so the quant work is repeated per
+    // column group.  Measured on MI355X against the quant kernel + GEMM pair
+    // (graph replays, cold weights): qkv 7.6 against 8.6 us, o 7.1 against
+    // 8.1, gate_up 25.9 against 28.0, down_proj (long K, eight waves of 27
+    // tiles) 19.3 against 19.5 -- and one launch fewer where the linear runs
+    // inside a captured graph.  What remains over the GEMM alone (qkv 5.7 us)
+    // is the round trip of the cold bf16 row, which the pair pays in its quant
+    // kernel.  The four-row variant of the LDS-exchange prologue lost 2 us on
+    // qkv and o at M=4.
     if (a.M != 1 || a.swiglu || a.partials || !geom::is_unpadded(a.K, a.group)) return false;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx % 8 != 0) return false;
     const DecodeConfig c = decode_config(a.M, a.N, a.K, a.group);
