@@ -892,10 +892,14 @@ def pmc_summary(fetch_db, write_db, out_json=None):
 
 def prefill_probe(pkg, dev, M, calls=3):
     """Each projection's prefill GEMM at M rows, `calls` times on distinct weight copies
-    (eager, group 128, activations drawn on the device), then a 256 MiB copy."""
+    (eager, group 128, activations drawn on the device), then a 256 MiB copy.  Before every
+    call a 512 MiB device copy evicts the caches (the 256 MB Infinity Cache included), so
+    the GEMM reads its weights from HBM, as the bench's cold rotation does."""
     import torch
     synth = pkg.synth
     gen = torch.Generator(device=dev)
+    fsrc = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
+    fdst = torch.empty_like(fsrc)
     for pi, p in enumerate(PROJS):
         K, N = synth.QWQ_SHAPES[p]
         x = synth.activations_device(M, K, seed=M + pi, device=dev)
@@ -906,6 +910,7 @@ def prefill_probe(pkg, dev, M, calls=3):
             ws = (torch.rand((K // GROUP, N), device=dev, generator=gen) * 0.018 + 0.002).to(torch.float16)
             wt, st = torch.ops.npu.w4a8_repack(pkg.packing.pack_int4(codes), ws, K, GROUP)
             del codes
+            fdst.copy_(fsrc)
             torch.ops.npu.w4a8_gemm(a_q, a_s, wt, st, N, K, GROUP)
             torch.cuda.synchronize()
             del wt, st
