@@ -104,6 +104,9 @@ def main():
     ap.add_argument("--decoder-trace-summary", metavar="DB",
                     help="summarize a --kernel-trace database of a --decoder-probe run: kernels per decode step "
                          "and their time, as markdown, and exit")
+    ap.add_argument("--decode-pmc-summary", nargs="+", metavar="DB",
+                    help="summarize rocprofv3 databases of a --pmc-probe run (counter passes, then a "
+                         "--kernel-trace database last) for the 16 decode GEMM calls as markdown and exit")
     ap.add_argument("--prefill-pmc-summary", nargs="+", metavar="DB",
                     help="summarize rocprofv3 databases of a --prefill-probe run (counter passes, then a "
                          "--kernel-trace database last) for the prefill GEMM kernels as markdown and exit")
@@ -116,6 +119,9 @@ def main():
         return
     if args.prefill_pmc_summary:
         prefill_pmc_summary(args.prefill_pmc_summary, args.pmc_json)
+        return
+    if args.decode_pmc_summary:
+        decode_pmc_summary(args.decode_pmc_summary)
         return
     if args.decoder_trace_summary:
         decoder_trace_summary(args.decoder_trace_summary)
@@ -888,6 +894,71 @@ def pmc_summary(fetch_db, write_db, out_json=None):
         with open(out_json, "w") as fh:
             json.dump(dict(factor_fetch=ff, factor_write=fw, per_shape=out, avg_traffic_bytes=tot_tr / n,
                            avg_alg_bytes=tot_alg / n), fh, indent=1)
+
+
+def decode_pmc_summary(dbs):
+    """Counter table of the 16 configs[1] decode GEMM calls of a --pmc-probe run: counter
+    databases (one pass each), then a --kernel-trace database of the same probe for the
+    durations.  A call's counters are those of its GEMM dispatch (gemm_decode_kernel,
+    gemm_wide_kernel or the split gemm_prefill_cols_kernel); the wide_reduce_kernel of the
+    K-split calls is left out."""
+    import collections
+    import sqlite3
+    *pmc_dbs, trace_db = dbs
+    import __graft_entry__ as ge
+    synth = ge.package().synth
+    is_gemm = lambda n: any(k in n for k in ("gemm_decode_kernel", "gemm_wide_kernel",  # noqa: E731
+                                             "gemm_prefill_cols_kernel"))
+    short = lambda n: n.split("<")[0].split("::")[-1].replace("void ", "")  # noqa: E731
+    shapes = [(M, p) for M in DECODE_MS for p in PROJS]
+    calls = [(n, d) for n, d in sqlite3.connect(trace_db).execute(
+        "select name, duration from kernels order by start").fetchall() if is_gemm(n)][-len(shapes):]
+    ctr = [collections.defaultdict(list) for _ in shapes]
+    for db in pmc_dbs:
+        ev = sqlite3.connect(db).execute("select dispatch_id, name, counter_name, counter_value from pmc_events "
+                                         "order by dispatch_id").fetchall()
+        ids = sorted({did for did, name, _, _ in ev if is_gemm(name)})[-len(shapes):]
+        pos = {did: i for i, did in enumerate(ids)}
+        for did, _, cname, val in ev:
+            if did in pos:
+                ctr[pos[did]][cname].append(val)
+    avg = lambda v: sum(v) / len(v) if v else float("nan")  # noqa: E731
+    print("Commands (run from /tmp with TMPDIR=/tmp; REPO is the repository root; one database per run):\n")
+    for i, db in enumerate(pmc_dbs):
+        names_db = [r[0] for r in sqlite3.connect(db).execute(
+            "select distinct counter_name from pmc_events order by counter_name")]
+        print(f"    rocprofv3 --pmc {' '.join(names_db)} -d /tmp/dp -o p{i + 1} -- python3 REPO/bench.py --pmc-probe")
+    print("    rocprofv3 --kernel-trace -d /tmp/dp -o kt -- python3 REPO/bench.py --pmc-probe")
+    print("    python3 REPO/bench.py --decode-pmc-summary " +
+          " ".join(f"p{i + 1}_results.db" for i in range(len(pmc_dbs))) + " kt_results.db\n")
+    names = sorted({c for d in ctr for c in d})
+    print("Per-dispatch values as rocprofv3 reports them (SQ_* per shader engine, 32 on MI355X; "
+          "GRBM_GUI_ACTIVE in GPU cycles).\n")
+    print("| M | proj | kernel | us | " + " | ".join(names) + " |")
+    print("|---:|---|---|---:|" + "---:|" * len(names))
+    for (M, p), (n, d), cd in zip(shapes, calls, ctr):
+        print(f"| {M} | {p} | {short(n)} | {d / 1e3:.2f} | " + " | ".join(f"{avg(cd[c]):.4g}" for c in names) + " |")
+
+    def frac(cd, a, b):
+        try:
+            return f"{100 * avg(cd[a]) / avg(cd[b]):.0f}%"
+        except ZeroDivisionError:
+            return "n/a"
+    print("\nDerived: issue and wait shares of the waves' resident cycles (SQ_ACTIVE_INST_ANY, SQ_WAIT_INST_ANY "
+          "over SQ_WAVE_CYCLES), VALU instructions per MFMA ((SQ_INSTS_VALU - SQ_INSTS_MFMA) / SQ_INSTS_MFMA), "
+          "MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES over 32 SIMDs per shader engine x SQ_BUSY_CYCLES), "
+          "SQ_BUSY_CYCLES / duration (the clock while waves are resident; GRBM_GUI_ACTIVE's window is "
+          "longer than these few-microsecond dispatches) and the weight stream (algorithmic bytes / duration, "
+          "eager calls under the profiler).\n")
+    print("| M | proj | issue | wait | VALU / MFMA | MFMA busy | SQ busy GHz | GB/s |\n|---:|---|---:|---:|---:|---:|---:|---:|")
+    for (M, p), (n, d), cd in zip(shapes, calls, ctr):
+        K, N = synth.QWQ_SHAPES[p]
+        g = lambda c: avg(cd[c])  # noqa: E731
+        vpm = (g("SQ_INSTS_VALU") - g("SQ_INSTS_MFMA")) / g("SQ_INSTS_MFMA") if g("SQ_INSTS_MFMA") else float("nan")
+        busy = 100 * g("SQ_VALU_MFMA_BUSY_CYCLES") / (32 * g("SQ_BUSY_CYCLES"))
+        print(f"| {M} | {p} | {frac(cd, 'SQ_ACTIVE_INST_ANY', 'SQ_WAVE_CYCLES')} | "
+              f"{frac(cd, 'SQ_WAIT_INST_ANY', 'SQ_WAVE_CYCLES')} | {vpm:.1f} | {busy:.1f}% | "
+              f"{g('SQ_BUSY_CYCLES') / d:.2f} | {gemm_bytes(M, N, K) / d:.0f} |")
 
 
 def prefill_probe(pkg, dev, M, calls=3):
