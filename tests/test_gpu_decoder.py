@@ -27,10 +27,17 @@ def tiny_cfg(pkg):
                                      group=64, rms_eps=1e-5, rope_theta=1.0e4, qkv_bias=True)
 
 
-def test_decode_graph_matches_eager(pkg, dev):
-    say("decoder: graph vs eager")
+# decode attention: "auto" is the batched-product path at these batch sizes,
+# "sdpa" the scaled_dot_product_attention path large batches take
+ATTENTION = ["auto", "sdpa"]
+
+
+@pytest.mark.parametrize("attention", ATTENTION)
+def test_decode_graph_matches_eager(pkg, dev, attention):
+    say(f"decoder: graph vs eager ({attention})")
     cfg = tiny_cfg(pkg)
-    m = pkg.decoder.W4A8Decoder(cfg, batch=3, max_len=40, device=dev, seed=1)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=3, max_len=40, device=dev, seed=1, attention=attention)
+    assert m.sdpa == (attention == "sdpa")
     prompt = torch.randint(0, cfg.vocab, (3, 12), generator=torch.Generator().manual_seed(0)).to(dev)
     first = m.prefill(prompt)
     k0 = [k.clone() for k in m.k_cache]
@@ -57,26 +64,30 @@ def test_decode_graph_matches_eager(pkg, dev):
     assert int(m.pos.item()) == 20
 
 
-def test_prefill_decode_consistency(pkg, dev):
+@pytest.mark.parametrize("attention", ATTENTION)
+def test_prefill_decode_consistency(pkg, dev, attention):
     """Decoding token t after a prefill of t tokens gives the same logits as a prefill
     of t+1 tokens ending in that token (KV cache, RoPE positions, masks)."""
-    say("decoder: prefill/decode consistency")
+    say(f"decoder: prefill/decode consistency ({attention})")
     cfg = tiny_cfg(pkg)
-    m = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=32, device=dev, seed=2)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=32, device=dev, seed=2, attention=attention)
     prompt = torch.randint(0, cfg.vocab, (2, 10), generator=torch.Generator().manual_seed(1)).to(dev)
     nxt = m.prefill(prompt)
     m.decode(nxt, 10, 1, graph=False)
     dec_logits = m.last_logits.float().clone()
-    m2 = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=32, device=dev, seed=2)
+    m2 = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=32, device=dev, seed=2, attention=attention)
     m2.prefill(torch.cat([prompt, nxt[:, None]], dim=1))
     pre_logits = m2.last_logits.float()
     rel = (dec_logits - pre_logits).norm() / pre_logits.norm()
+    say(f"  prefill/decode logits rel-L2 ({attention}): {rel:.5f}")
     assert rel < 2e-2, f"rel-L2 {rel}"
 
 
-def _ref_forward(m, tokens):
+def _ref_forward(m, tokens, bf16_probs=True):
     """float64 torch restatement of the same model on the CPU: dequantised weights and
-    the per-token activation quant (bf16 scale, round half to even) in front of every linear."""
+    the per-token activation quant (bf16 scale, round half to even) in front of every linear.
+    bf16_probs: the attention probabilities rounded to bf16 before the product with V (the
+    batched-product path) or kept exact (scaled_dot_product_attention's kernel)."""
     c = m.cfg
     f = lambda t: t.detach().double().cpu()  # noqa: E731
 
@@ -111,10 +122,12 @@ def _ref_forward(m, tokens):
         q, k, v = rope(qkv[:, :, :c.heads]), rope(qkv[:, :, c.heads:c.heads + c.kv_heads]), qkv[:, :, c.heads + c.kv_heads:]
         k = k.repeat_interleave(Gq, dim=2)
         v = v.repeat_interleave(Gq, dim=2)
-        # the model's attention rounds q.k to bf16 before scaling (a bf16 product)
-        sc = bf16(torch.einsum("bshd,bthd->bhst", q, k)) / math.sqrt(c.head_dim)
+        # the small-batch attention: fp32 scores (the batched product's fp32 output), bf16
+        # probabilities
+        sc = torch.einsum("bshd,bthd->bhst", q, k) / math.sqrt(c.head_dim)
         sc = sc + torch.full((S, S), float("-inf"), dtype=torch.float64).triu(1)
-        a = bf16(torch.einsum("bhst,bthd->bshd", bf16(torch.softmax(sc, -1)), v)).reshape(B * S, -1)
+        pr = torch.softmax(sc, -1)
+        a = bf16(torch.einsum("bhst,bthd->bshd", bf16(pr) if bf16_probs else pr, v)).reshape(B * S, -1)
         x = bf16(x + qlinear(a, L["o"]))
         h = rms(x, L["ln2"])
         gu = qlinear(h, L["gate_up"])
@@ -125,26 +138,35 @@ def _ref_forward(m, tokens):
     return rms(last, m.final_norm) @ f(m.lm_head).t()
 
 
-def test_forward_matches_float_reference(pkg, dev):
-    say("decoder: vs float64 reference")
+@pytest.mark.parametrize("attention", ATTENTION)
+def test_forward_matches_float_reference(pkg, dev, attention):
+    say(f"decoder: vs float64 reference ({attention})")
     cfg = tiny_cfg(pkg)
-    m = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=24, device=dev, seed=3, keep_weights=True)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=24, device=dev, seed=3, keep_weights=True,
+                                attention=attention)
     prompt = torch.randint(0, cfg.vocab, (2, 16), generator=torch.Generator().manual_seed(2)).to(dev)
     m.prefill(prompt)
     got = m.last_logits.double().cpu()
-    ref = _ref_forward(m, prompt)
+    ref = _ref_forward(m, prompt, bf16_probs=not m.sdpa)
     rel = (got - ref).norm() / ref.norm()
-    say(f"decoder logits rel-L2 vs float64 reference: {rel:.5f}")
-    assert rel < 2e-2, f"rel-L2 {rel}"
+    say(f"decoder logits rel-L2 vs float64 reference ({attention}): {rel:.5f}")
+    # The reference rounds as the batched-product path does (0.17% here).  The SDPA
+    # kernel accumulates in its own order: its attention outputs are within 2.6e-3
+    # rel-L2 of the batched-product path's (test_attention_paths_agree), and those
+    # last-bit differences flip int8 activation codes of the next projections, which
+    # moves this two-layer model's logits by 3.4-3.6% -- a wrong mask, position or
+    # cache write moves them by O(1).
+    assert rel < (5e-2 if m.sdpa else 2e-2), f"rel-L2 {rel}"
 
 
-def test_resize_then_capture_after_full_decode(pkg, dev):
+@pytest.mark.parametrize("attention", ATTENTION)
+def test_resize_then_capture_after_full_decode(pkg, dev, attention):
     """Regression: a decode that runs to max_len leaves the position at max_len; a later
     resize + prefill + capture must neither index past the cache nor disturb the prefilled
     cache (the captured step then matches eager decode)."""
-    say("decoder: resize after a full decode")
+    say(f"decoder: resize after a full decode ({attention})")
     cfg = tiny_cfg(pkg)
-    m = pkg.decoder.W4A8Decoder(cfg, batch=1, max_len=16, device=dev, seed=4)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=1, max_len=16, device=dev, seed=4, attention=attention)
     p1 = torch.randint(0, cfg.vocab, (1, 8), generator=torch.Generator().manual_seed(5)).to(dev)
     m.decode(m.prefill(p1), 8, 8, graph=True)                  # position ends at max_len
     assert int(m.pos.item()) == 16
@@ -156,9 +178,42 @@ def test_resize_then_capture_after_full_decode(pkg, dev):
     m.capture()
     assert all(torch.equal(a, b) for a, b in zip(m.k_cache, k0)), "capture changed the KV cache"
     graph_out = m.decode(first, 8, 8, graph=True)
-    m2 = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=16, device=dev, seed=4)
+    m2 = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=16, device=dev, seed=4, attention=attention)
     eager_out = m2.decode(m2.prefill(p2), 8, 8, graph=False)
     assert all(torch.equal(a, b) for a, b in zip(graph_out, eager_out))
+
+
+def test_attention_paths_agree(pkg, dev):
+    """The two attention paths on the same queries and cache contents -- batched products
+    over the transposed K cache, scaled_dot_product_attention over the [L, D] cache -- agree
+    to the bf16 rounding of their outputs, at decode (masked positions past pos) and at
+    prefill (causal rows of every query head)."""
+    say("decoder: attention paths")
+    cfg = tiny_cfg(pkg)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=3, max_len=48, device=dev, seed=7, attention="matmul")
+    g = torch.Generator(device=dev).manual_seed(8)
+    B, KVH, D, L = 3, cfg.kv_heads, cfg.head_dim, 48
+    G = cfg.heads // cfg.kv_heads
+    k = torch.randn((B, KVH, L, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, KVH, L, D), generator=g, device=dev).to(torch.bfloat16)
+    kt = k.transpose(2, 3).contiguous()
+    cases = []
+    q = torch.randn((B, KVH, G, D), generator=g, device=dev).to(torch.bfloat16)
+    cases.append(("decode", q, torch.where(torch.arange(L, device=dev) > 30, float("-inf"), 0.0).view(1, 1, 1, L)))
+    S = L
+    q = torch.randn((B, KVH, G * S, D), generator=g, device=dev).to(torch.bfloat16)
+    cases.append(("prefill", q, torch.full((S, S), float("-inf"), device=dev).triu_(1).repeat(G, 1)))
+    for name, q, bias in cases:
+        a = m._attend(q, kt, v, bias).double()
+        b = pkg.decoder._sdpa(q, k, v, bias.to(torch.bfloat16).view(1, 1, *bias.shape[-2:])).double()
+        rel = float((a - b).norm() / b.norm())
+        say(f"  {name}: rel-L2 {rel:.2e}")
+        assert rel < 4e-3, f"{name}: rel-L2 {rel}"
+
+
+def test_decoder_rejects_unknown_attention(pkg):
+    with pytest.raises(ValueError, match="attention"):
+        pkg.decoder.W4A8Decoder(tiny_cfg(pkg), batch=1, max_len=8, device="cpu", attention="flash")
 
 
 # ------------------------------------------------------------------ configs[4] at its real widths
@@ -338,15 +393,34 @@ def test_qwq_full_depth_concurrency8(pkg, dev, monkeypatch):
 
 def test_fused_score_scaling_equals_three_ops(dev):
     """The decoder's attention scores as one torch.add(bias, s, alpha=1/sqrt(D)) equal the
-    separate s.float() * (1/sqrt(D)) + bias bit for bit when the bias holds only 0 and -inf
-    (bf16 scores of every magnitude, masked and unmasked positions)."""
+    separate s * (1/sqrt(D)) + bias bit for bit when the bias holds only 0 and -inf (fp32
+    scores of every magnitude, as the batched product returns them, and bf16 ones;
+    masked and unmasked positions)."""
     g = torch.Generator(device=dev).manual_seed(3)
-    s = (torch.randn((2, 8, 5, 1200), generator=g, device=dev) * 40).to(torch.bfloat16)
-    s[0, 0, 0, :8] = torch.tensor([0.0, -0.0, 1e-38, -3e38, 448.0, 1.0, -1.0, 65504.0], device=dev).to(torch.bfloat16)
+    s32 = torch.randn((2, 8, 5, 1200), generator=g, device=dev) * 40
+    s32[0, 0, 0, :9] = torch.tensor([0.0, -0.0, 1e-38, -3e38, 448.0, 1.0, -1.0, 65504.0, 1e-45], device=dev)
     pos = torch.arange(1200, device=dev)
     bias = torch.where(pos > 700, float("-inf"), 0.0).view(1, 1, 1, 1200)
-    for d in (64, 128):
-        a = 1.0 / math.sqrt(d)
-        ref = s.float() * a + bias
-        got = torch.add(bias, s, alpha=a)
-        assert got.dtype == torch.float32 and torch.equal(got, ref), f"head_dim {d}"
+    for s in (s32, s32.to(torch.bfloat16)):
+        for d in (64, 128):
+            a = 1.0 / math.sqrt(d)
+            ref = s.float() * a + bias
+            got = torch.add(bias, s, alpha=a)
+            assert got.dtype == torch.float32 and torch.equal(got, ref), f"{s.dtype} head_dim {d}"
+
+
+def test_attend_scores_are_fp32_products(pkg, dev):
+    """The batched-product decode attention keeps q.k in fp32 (within fp32 accumulation of
+    the exact products), not rounded to bf16."""
+    cfg = tiny_cfg(pkg)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=64, device=dev, seed=5, attention="matmul")
+    g = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn((2, cfg.kv_heads, 2, cfg.head_dim), generator=g, device=dev).to(torch.bfloat16)
+    kc = torch.randn((2, cfg.kv_heads, cfg.head_dim, 64), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((2, cfg.kv_heads, 64, cfg.head_dim), generator=g, device=dev).to(torch.bfloat16)
+    bias = torch.zeros((1, 1, 1, 64), device=dev)
+    got = m._attend(q, kc, vc, bias).double()
+    sc = (q.double() @ kc.double()) / math.sqrt(cfg.head_dim)
+    ref = torch.softmax(sc, -1).to(torch.bfloat16).double() @ vc.double()
+    # bf16 probabilities and output: within a few bf16 ulps of the float64 attention
+    assert float((got - ref).abs().max()) < 4 * 2.0 ** -8 * float(ref.abs().max())

@@ -14,10 +14,20 @@ embeddings, RMSNorm) on this build's ops:
 * the rotary embedding of q and k and the KV-cache append run as one kernel
   (``torch.ops.npu.w4a8_rope_kv``, fp32 products and sums rounded to bf16 as
   torch rounds them on float tensors);
-* attention stays on PyTorch-ROCm in bf16, written with contiguous batched
-  products only: the K cache is stored transposed ``[B, KVH, D, L]`` and the
-  query heads of one KV head form the rows of one product, so grouped-query
-  attention needs no head repeat and no transposed operand;
+* attention stays on PyTorch-ROCm in bf16.  The query heads of one KV head
+  form the rows of one attention problem, so grouped-query attention needs no
+  head repeat.  From ``SDPA_MIN_BATCH`` sequences on, prefill and decode call
+  ``torch.nn.functional.scaled_dot_product_attention`` on its efficient
+  backend only (the reference's own call,
+  npu_ops/python/bench_decode_layer.py:73; the math backend, whose batched
+  products take a transposed bf16 operand, is never used), over a K cache
+  stored ``[B, KVH, L, D]``.  Smaller batches use two contiguous batched
+  products over a K cache stored transposed ``[B, KVH, D, L]``, the scores
+  returned in fp32 as SDPA keeps them.  Measured on MI355X (graph replays,
+  one layer's decode attention over 1280 positions, us): products / SDPA 25
+  / 60 at 1 sequence, 28 / 65 at 8, 55 / 66 at 32, 83 / 81 at 48, 120 / 93
+  at 64; prefill of one 1024-token sequence 233 / 93.  Prefill follows the
+  batch's path so that a prefill and the decode after it round alike;
 * the decode step is shape-static -- position, RoPE row, KV write index and
   mask are device tensors -- so it is captured once per batch size in a HIP
   graph and replayed, the greedy token feeding the next step inside the graph.
@@ -92,13 +102,35 @@ class _Linear:
         return torch.ops.npu.w4a8_gemm_swiglu(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
 
 
+# Batches from this size on attend through scaled_dot_product_attention (the
+# K cache then stored [B, KVH, L, D]); smaller ones through two batched products
+# over the transposed K cache.
+SDPA_MIN_BATCH = 48
+
+
+def _sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """softmax(q k^T / sqrt(D) + mask) v on the efficient backend (an error, not a fallback,
+    where it cannot run).  q [B, KVH, R, D], k and v [B, KVH, L, D], mask bf16 broadcastable
+    to [B, KVH, R, L] with 0 and -inf."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+        return torch.nn.functional.scaled_dot_product_attention(
+            q, k, v, attn_mask=mask.expand(q.shape[0], q.shape[1], q.shape[2], k.shape[2]))
+
+
 class W4A8Decoder:
     """The decoder with a static KV cache for ``batch`` sequences of up to ``max_len`` tokens."""
 
     def __init__(self, cfg: DecoderConfig, batch: int, max_len: int, device="cuda", seed: int = 0,
-                 keep_weights=False):
+                 keep_weights=False, attention: str = "auto"):
         """keep_weights: True keeps every linear's int8 codes and scales (reference
-        checks of small models), a collection of layer indices keeps those layers' only."""
+        checks of small models), a collection of layer indices keeps those layers' only.
+        attention: "sdpa", "matmul", or "auto" (sdpa from SDPA_MIN_BATCH sequences on), for
+        prefill and decode alike (the two paths round differently, so a prefill and the
+        decode after it share one).  The choice is made again by resize()."""
+        if attention not in ("auto", "sdpa", "matmul"):
+            raise ValueError(f"attention must be 'auto', 'sdpa' or 'matmul', not {attention!r}")
+        self.attention = attention
         self.cfg, self.batch, self.max_len = cfg, batch, max_len
         dev = torch.device(device)
         self.device = dev
@@ -119,10 +151,8 @@ class W4A8Decoder:
                 "gate_up": _Linear(2 * c.ffn, c.hidden, c.group, gen, dev, keep=keep),
                 "down": _Linear(c.hidden, c.ffn, c.group, gen, dev, keep=keep),
             })
-        kvh, d = c.kv_heads, c.head_dim
-        # K stored transposed so that q @ K is a product of contiguous operands
-        self.k_cache = [torch.zeros((batch, kvh, d, max_len), dtype=torch.bfloat16, device=dev) for _ in self.layers]
-        self.v_cache = [torch.zeros((batch, kvh, max_len, d), dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        d = c.head_dim
+        self._alloc_cache(batch, max_len)
         inv = 1.0 / (c.rope_theta ** (torch.arange(0, d, 2, device=dev, dtype=torch.float32) / d))
         ang = torch.arange(max_len, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)          # [L, d/2] fp32
@@ -138,18 +168,32 @@ class W4A8Decoder:
         c, dev = self.cfg, self.device
         self.batch, self.max_len = batch, max_len
         self._graph = None
-        self.k_cache = self.v_cache = None
+        self.k_cache = self.v_cache = self._k_ld = None
         torch.cuda.empty_cache()
-        self.k_cache = [torch.zeros((batch, c.kv_heads, c.head_dim, max_len), dtype=torch.bfloat16, device=dev)
-                        for _ in self.layers]
-        self.v_cache = [torch.zeros((batch, c.kv_heads, max_len, c.head_dim), dtype=torch.bfloat16, device=dev)
-                        for _ in self.layers]
+        self._alloc_cache(batch, max_len)
         inv = 1.0 / (c.rope_theta ** (torch.arange(0, c.head_dim, 2, device=dev, dtype=torch.float32) / c.head_dim))
         ang = torch.arange(max_len, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)
         self.positions = torch.arange(max_len, device=dev)
         self.tokens = torch.zeros((batch,), dtype=torch.long, device=dev)
         self.pos.zero_()
+
+    def _alloc_cache(self, batch: int, max_len: int) -> None:
+        """KV caches for the batch size's attention path.  k_cache[li] is always a
+        [B, KVH, D, L] tensor (what w4a8_rope_kv writes through): the storage itself for
+        the batched-product decode, else a transposed view of _k_ld[li] [B, KVH, L, D],
+        the layout scaled_dot_product_attention reads.  v_cache[li] is [B, KVH, L, D]."""
+        c, dev = self.cfg, self.device
+        kvh, d = c.kv_heads, c.head_dim
+        self.sdpa = self.attention == "sdpa" or (self.attention == "auto" and batch >= SDPA_MIN_BATCH)
+        if self.sdpa:
+            self._k_ld = [torch.zeros((batch, kvh, max_len, d), dtype=torch.bfloat16, device=dev) for _ in self.layers]
+            self.k_cache = [k.transpose(2, 3) for k in self._k_ld]
+        else:
+            self._k_ld = None
+            self.k_cache = [torch.zeros((batch, kvh, d, max_len), dtype=torch.bfloat16, device=dev)
+                            for _ in self.layers]
+        self.v_cache = [torch.zeros((batch, kvh, max_len, d), dtype=torch.bfloat16, device=dev) for _ in self.layers]
 
     # ------------------------------------------------------------ pieces
     def _rope_kv(self, li: int, L: dict, aq: torch.Tensor, as_: torch.Tensor, T: int,
@@ -167,10 +211,15 @@ class W4A8Decoder:
         """q [B, KVH, R, D] (R = query heads per KV head x query tokens), kc [B, KVH, D, L],
         vc [B, KVH, L, D], additive bias broadcast to [B, KVH, R, L] -> [B, KVH, R, D].
 
-        The scores are fp32(bf16(q.k)) * 1/sqrt(D) + bias, as one torch.add with alpha: the
-        bias holds only 0 and -inf, so the one rounding of the product is that of the separate
-        .float(), multiply and add (three launches), fused multiply-add or not."""
-        scores = torch.add(bias, torch.matmul(q, kc), alpha=1.0 / math.sqrt(self.cfg.head_dim))
+        The scores q.k leave the batched product in fp32 (``out_dtype``: the precision
+        scaled_dot_product_attention keeps them in, which prefill uses), then 1/sqrt(D) and
+        the bias apply as one torch.add with alpha: the bias holds only 0 and -inf, so the one
+        rounding of the product is that of a separate multiply and add, fused multiply-add or
+        not.  The probabilities are rounded to bf16 for the second product."""
+        B, H, R, D = q.shape
+        L = kc.shape[-1]
+        s = torch.bmm(q.reshape(B * H, R, D), kc.reshape(B * H, D, L), out_dtype=torch.float32).view(B, H, R, L)
+        scores = torch.add(bias, s, alpha=1.0 / math.sqrt(self.cfg.head_dim))
         p = torch.softmax(scores, dim=-1).to(torch.bfloat16)
         return torch.matmul(p, vc)
 
@@ -190,23 +239,27 @@ class W4A8Decoder:
         S = tokens.shape[1]
         assert tokens.shape[0] == B and S <= self.max_len
         G = c.heads // c.kv_heads
-        causal = torch.full((S, S), float("-inf"), device=self.device).triu_(1)
+        # rows of one KV head's problem are (query head g, token s) = g * S + s
+        bias = torch.full((S, S), float("-inf"), device=self.device).triu_(1).repeat(G, 1)
+        mask = bias.to(torch.bfloat16).view(1, 1, G * S, S)
         x = self.embed[tokens.reshape(-1)]                               # [B*S, hidden]
         delta = None
         for li, L in enumerate(self.layers):
             aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
             x = s if delta is not None else x
             q = self._rope_kv(li, L, aq, as_, S, self._pos0)        # [B, S, H, D]; caches filled for [0, S)
-            kc = self.k_cache[li][:, :, :, :S].contiguous()
-            vc = self.v_cache[li][:, :, :S, :].contiguous()
-            out = torch.empty((B, S, c.heads, c.head_dim), dtype=torch.bfloat16, device=self.device)
-            for b in range(B):                                        # one sequence at a time bounds the scores
-                qb = q[b].view(S, c.kv_heads, G, c.head_dim).permute(1, 2, 0, 3).reshape(1, c.kv_heads, G * S,
-                                                                                        c.head_dim)
-                bias = causal.repeat(G, 1)                               # rows are (query head, token)
-                ob = self._attend(qb.contiguous(), kc[b:b + 1], vc[b:b + 1], bias)   # [1, KVH, G*S, D]
-                out[b] = ob.view(c.kv_heads, G, S, c.head_dim).permute(2, 0, 1, 3).reshape(S, c.heads, c.head_dim)
-            x, delta = self._mlp_and_next(L, x, out.view(B * S, c.heads * c.head_dim))
+            qg = q.view(B, S, c.kv_heads, G, c.head_dim).permute(0, 2, 3, 1, 4).reshape(B, c.kv_heads, G * S,
+                                                                                       c.head_dim)
+            if self.sdpa:
+                o = _sdpa(qg, self._k_ld[li][:, :, :S, :], self.v_cache[li][:, :, :S, :], mask)   # [B, KVH, G*S, D]
+            else:
+                kc = self.k_cache[li][:, :, :, :S].contiguous()
+                vc = self.v_cache[li][:, :, :S, :].contiguous()
+                o = torch.empty((B, c.kv_heads, G * S, c.head_dim), dtype=torch.bfloat16, device=self.device)
+                for b in range(B):                                    # one sequence at a time bounds the scores
+                    o[b:b + 1] = self._attend(qg[b:b + 1].contiguous(), kc[b:b + 1], vc[b:b + 1], bias)
+            out = o.view(B, c.kv_heads, G, S, c.head_dim).permute(0, 3, 1, 2, 4).reshape(B * S, c.heads * c.head_dim)
+            x, delta = self._mlp_and_next(L, x, out)
         last = (x + delta).view(B, S, c.hidden)[:, -1]
         return self._logits_argmax(last)
 
@@ -227,6 +280,8 @@ class W4A8Decoder:
         c, B = self.cfg, self.batch
         G = c.heads // c.kv_heads
         bias = torch.where(self.positions > self.pos, float("-inf"), 0.0).view(1, 1, 1, self.max_len)
+        if self.sdpa:
+            bias = bias.to(torch.bfloat16)
         x = self.embed.index_select(0, self.tokens)                      # [B, hidden]
         delta = None
         for li, L in enumerate(self.layers):
@@ -234,7 +289,10 @@ class W4A8Decoder:
             x = s if delta is not None else x
             q = self._rope_kv(li, L, aq, as_, 1, self.pos)               # [B, 1, H, D]
             qg = q.view(B, c.kv_heads, G, c.head_dim)
-            o = self._attend(qg, self.k_cache[li], self.v_cache[li], bias)          # [B, KVH, G, D]
+            if self.sdpa:
+                o = _sdpa(qg, self._k_ld[li], self.v_cache[li], bias)              # [B, KVH, G, D]
+            else:
+                o = self._attend(qg, self.k_cache[li], self.v_cache[li], bias)      # [B, KVH, G, D]
             x, delta = self._mlp_and_next(L, x, o.reshape(B, c.heads * c.head_dim))
         self.tokens.copy_(self._logits_argmax(x + delta))
         self.pos.add_(1)
