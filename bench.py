@@ -98,7 +98,7 @@ def main():
                          "(eager, group 128), then a 256 MiB device copy of known size")
     ap.add_argument("--decoder-probe", type=int, metavar="B", default=0,
                     help="for rocprofv3 runs: the --decoder-layers decoder at concurrency B, a 1024-token prefill "
-                         "(cache of 1024 + 64 positions, as the decoder leg), then its captured decode step "
+                         "(cache of 1024 + 256 positions, as the decoder leg), then its captured decode step "
                          "replayed 5 + 10 times (the 10 between two marker launches are the ones "
                          "--decoder-trace-summary reads)")
     ap.add_argument("--decoder-trace-summary", metavar="DB",
@@ -535,7 +535,7 @@ def config4(pkg, dev, synth, make_pool, time_graph, T):
     return rows
 
 
-def decoder_probe(pkg, dev, layers, B, prompt=1024, steps=64, warm=5, timed=10):
+def decoder_probe(pkg, dev, layers, B, prompt=1024, steps=256, warm=5, timed=10):
     """configs[4]'s decode step for a kernel trace, on the cache the bench's decoder leg uses
     (`prompt` + `steps` positions): a prefill of `prompt` tokens, the step captured once, `warm`
     graph replays, then `timed` replays between two marker launches (a tiny weight repack, a
