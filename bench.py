@@ -467,6 +467,11 @@ def main():
                     traffic=round(tj["avg_traffic_bytes"]), alg_bytes_avg=round(tj["avg_alg_bytes"]),
                     traffic_source=str(tsrc.relative_to(ROOT)))
 
+        # the vendor library's plain int8 GEMM on the same shapes and M (no group
+        # scales, no fold, no unpack; int8 weights, int32 output): what the
+        # matrix cores give a library kernel under the same sustained load
+        result["int8_library_ref"] = int8_library_ref(dev, synth, at[0]["M"], time_graph, prefill)
+
     # the decode pools are not needed past this point
     weights = None
     torch.cuda.empty_cache()
@@ -894,6 +899,41 @@ def pmc_summary(fetch_db, write_db, out_json=None):
         with open(out_json, "w") as fh:
             json.dump(dict(factor_fetch=ff, factor_write=fw, per_shape=out, avg_traffic_bytes=tot_tr / n,
                            avg_alg_bytes=tot_alg / n), fh, indent=1)
+
+
+def int8_library_ref(dev, synth, M, time_graph, prefill):
+    """hipBLASLt's int8 x int8 -> int32 GEMM (torch._int_mm) at the four projections' shapes and
+    M rows, two weight copies alternating, back-to-back graph replays; beside this build's W4A8
+    GEMM at the same M."""
+    import torch
+    out = {"kernel": "torch._int_mm (hipBLASLt): int8 A [M, K] x int8 W [K, N] -> int32, no group scales",
+           "M": M, "shapes": {}}
+    ours = {r["proj"]: r for r in prefill if r["M"] == M}
+    for p in PROJS:
+        K, N = synth.QWQ_SHAPES[p]
+        try:
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(11)
+            a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=gen)
+            ws = [torch.randint(-8, 8, (N, K), dtype=torch.int8, device=dev, generator=gen).t() for _ in range(2)]
+
+            def mms(a=a, ws=ws, T=6):
+                for i in range(T):
+                    torch._int_mm(a, ws[i % 2])
+
+            us = time_graph(mms) / 6
+            tops = 2 * M * N * K / us / 1e6
+            row = {"us": round(us, 2), "TOPS": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
+            if p in ours:
+                row["w4a8_gemm_us"] = ours[p]["gemm_us"]
+                row["w4a8_speed_vs_int8"] = round(us / ours[p]["gemm_us"], 3)
+            out["shapes"][p] = row
+            log(f"  int8 library GEMM {p:13s} M={M:5d}: {us:9.1f} us {tops:7.1f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of "
+                f"int8 peak); W4A8 GEMM at {row.get('w4a8_speed_vs_int8', float('nan')):.2f}x its speed")
+            del a, ws
+        except (RuntimeError, AttributeError) as ex:
+            out["shapes"][p] = {"error": f"{type(ex).__name__}: {str(ex)[:160]}"}
+    return out
 
 
 def decode_pmc_summary(dbs):
