@@ -533,13 +533,15 @@ def test_gemm_every_decode_row_count(pkg, dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 5120, 5120), (16, 5120, 27648), (48, 5120, 27648), (64, 5120, 27648),
-                                   (1024, 7168, 5120)])
+                                   (4, 5120, 27648), (16, 55296, 5120), (64, 55296, 5120), (1024, 7168, 5120)])
 def test_gemm_deterministic_and_stress(pkg, dev, M, N, K):
     """Repeated launches give identical bits (the reference's --stress relaunch check,
     int4_cube_lab/host/mg_harness.h:307-334): the decode kernel's in-workgroup K split,
     the K split over workgroups with its reduce kernel and workspace (down_proj M=16),
     the 64-row prefill tile split along K with the same reduce (down_proj M=48 and 64),
-    and a prefill shape; every relaunch is compared, and the first against the oracle."""
+    the staged activations (M=4), the wide kernel's LDS-shared activations (gate_up
+    M=16 and 64), and a prefill shape; every relaunch is compared, and the first against
+    the oracle."""
     G = 128
     say(f"gemm stress M={M} N={N} K={K}")
     xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=5)
@@ -556,6 +558,36 @@ def test_gemm_deterministic_and_stress(pkg, dev, M, N, K):
     q_ref, s_ref = ow.quant_act_per_token(xb)
     y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G)
     check_output(tensor_bf16_bits(first)[:, cols], y32, f"stress M{M} N{N} K{K}",
+                 exact_sym(q_ref, s_ref, w[cols], ws32[cols], G))
+
+
+@pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 27648)])
+def test_linear_fused_deterministic_and_stress(pkg, dev, N, K):
+    """The fused single-row linear (quant prologue in every workgroup: every wave reading the
+    whole row at K=5120, the waves' absmax meeting in LDS behind a barrier at K=27648)
+    relaunched 30 times with other work between: identical output, a_q and a_scale bits,
+    the first equal to quant + GEMM and within the oracle bar."""
+    G = 128
+    say(f"fused linear stress N={N} K={K}")
+    xb, w, ws32, w_scale = make_problem(pkg, 1, N, K, G, seed=6)
+    w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+    x = bf16_bits_tensor(xb).to(dev)
+    lib = pkg._abi.lib()
+    assert lib.w4a8_linear_fused(x.data_ptr(), K, 1, N, K, G) == 1, "this shape should take the fused launch"
+    first = torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, G)
+    for i in range(30):
+        y = torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, G)
+        junk = torch.full((1 << 20,), i, dtype=torch.int32, device=dev)
+        assert torch.equal(y, first), f"relaunch {i} differs"
+        del junk
+    a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x)
+    pair = torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G)
+    assert torch.equal(first, pair), "fused linear differs from quant + GEMM"
+    cols = np.sort(np.random.default_rng(2).choice(N, 128, replace=False))
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    y32 = ow.gemm_fp32(q_ref, s_ref, w[cols], ws32[cols], G)
+    check_output(tensor_bf16_bits(first)[:, cols], y32, f"fused stress N{N} K{K}",
                  exact_sym(q_ref, s_ref, w[cols], ws32[cols], G))
 
 
