@@ -722,6 +722,70 @@ def test_linear_equals_quant_then_gemm(pkg, dev, M, N, K, G, sd, note):
     assert np.array_equal(tensor_bf16_bits(y3), tensor_bf16_bits(y))
 
 
+def random_shapes(seed: int, n: int, max_mnk: float = 3e8, max_gmn: float = 1.2e7):
+    """n seeded random (M, N, K, group, scale dtype) draws spread over the plans:
+    M mostly decode-sized with a tail into the prefill tiles, N and K anywhere
+    from 1 up (N not a multiple of 16, K not a multiple of the group), the group
+    half the time a common stride and otherwise any value up to past K (one short
+    group).  N and K are drawn under caps that keep the oracle to a few seconds
+    (M*N*K <= max_mnk, groups*M*N <= max_gmn)."""
+    rng = np.random.default_rng(seed)
+    strides = [32, 64, 96, 128, 192, 256, 320, 512, 640, 1024]
+    out = []
+    while len(out) < n:
+        u = rng.random()
+        M = int(rng.integers(1, 17)) if u < 0.5 else int(rng.integers(17, 97)) if u < 0.8 else \
+            int(rng.integers(97, 700))
+        N = int(rng.integers(1, min(4096, int(max_mnk / (M * 64))) + 1))
+        K = int(rng.integers(1, min(6000, int(max_mnk / (M * N))) + 1))
+        G = int(rng.choice(strides)) if rng.random() < 0.5 else int(rng.integers(1, K + 300))
+        if ow.num_groups(K, G) * M * N > max_gmn:
+            continue
+        out.append((M, N, K, G, "f16" if rng.random() < 0.5 else "bf16"))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,G,sd", random_shapes(20261202, 64))
+def test_gemm_random_shapes(pkg, dev, M, N, K, G, sd):
+    """Seeded random shapes through the GEMM: partials bit-exact, padded a_q and a_scale
+    byte-exact, output within the bars, the production launch equal to the dump."""
+    say(f"gemm random M={M} N={N} K={K} G={G} scales={sd}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M * 7 + N + K, scale_dtype=sd)
+    y, P, a_q, a_s = run_hip(dev, xb, w, w_scale, N, K, G)
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    assert np.array_equal(a_q.cpu().numpy(), ow.pad_groups(q_ref, G)), "padded activation layout"
+    assert np.array_equal(tensor_bf16_bits(a_s), s_ref)
+    P_ref = ow.group_partials(q_ref, w, G)
+    assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
+    y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G, P_ref)
+    check_output(tensor_bf16_bits(y), y32, f"random M{M} N{N} K{K} G{G}", exact_sym(q_ref, s_ref, w, ws32, G))
+    assert_production_equals_dump(pkg, dev, a_q, a_s, w, w_scale, y, N, K, G)
+
+
+@pytest.mark.parametrize("M,N,K,G,sd", [(int(m) % 4 + 1, n, k, g, sd)
+                                        for m, n, k, g, sd in random_shapes(77, 24)])
+def test_linear_random_shapes(pkg, dev, M, N, K, G, sd):
+    """Seeded random shapes through w4a8_linear at one to four rows (the fused launch
+    where it applies): equal to quant + GEMM bit for bit, and within the bars."""
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + 3 * K, scale_dtype=sd)
+    x = bf16_bits_tensor(xb).to(dev)
+    fused = pkg._abi.lib().w4a8_linear_fused(x.data_ptr(), x.stride(0), M, N, K, G)
+    say(f"linear random M={M} N={N} K={K} G={G} scales={sd} fused={fused}")
+    w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+    y, a_q, a_s = run_linear_abi(pkg, dev, x, w_tiles, s_tiles, N, K, G)
+    a_q2, a_s2 = torch.ops.npu.w4a8_quant_pertoken(x, G)
+    y2 = torch.ops.npu.w4a8_gemm(a_q2, a_s2, w_tiles, s_tiles, N, K, G)
+    torch.cuda.synchronize()
+    assert torch.equal(a_q, a_q2), "quantised activations differ"
+    assert np.array_equal(tensor_bf16_bits(a_s), tensor_bf16_bits(a_s2))
+    assert np.array_equal(tensor_bf16_bits(y), tensor_bf16_bits(y2)), "y differs from quant + gemm"
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G)
+    check_output(tensor_bf16_bits(y), y32, f"linear random M{M} N{N} K{K} G{G}",
+                 exact_sym(q_ref, s_ref, w, ws32, G))
+
+
 def test_linear_unaligned_and_strided_input(pkg, dev):
     """x rows not 16-byte aligned or ldx % 8 != 0 take the two-kernel path; a row-strided
     aligned x takes the fused one; the results are the same."""
@@ -921,6 +985,24 @@ def test_gemm_swiglu(pkg, dev, M, I, K, G, sd):
     y, yf = run_swiglu_pair(dev, xb, w, w_scale, N, K, G)
     assert yf.shape == (M, I)
     check_swiglu(yf, ow.silu_mul_bf16(y[:, :I], y[:, I:]), 0.999, f"fused vs unfused M{M} I{I}")
+    q_ref, s_ref = ow.quant_act_per_token(xb)
+    y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G)
+    full = ow.silu_mul_bf16(ow.f32_to_bf16_bits(y32[:, :I]), ow.f32_to_bf16_bits(y32[:, I:]))
+    got, exp = ow.bf16_bits_to_f32(yf).astype(np.float64), ow.bf16_bits_to_f32(full).astype(np.float64)
+    assert np.linalg.norm(got - exp) / np.linalg.norm(exp) <= 1e-3
+    assert np.mean(got == exp) > 0.99
+
+
+@pytest.mark.parametrize("M,I,K,G,sd", [(m, max(16, n // 32 * 16), k, g, sd)
+                                        for m, n, k, g, sd in random_shapes(4242, 16)])
+def test_gemm_swiglu_random_shapes(pkg, dev, M, I, K, G, sd):
+    """Seeded random shapes (I a multiple of 16) through the fused SwiGLU epilogue:
+    within the bar of the unfused GPU output and of the oracle."""
+    N = 2 * I
+    say(f"gemm swiglu random M={M} I={I} K={K} G={G} scales={sd}")
+    xb, w, ws32, w_scale = make_problem(pkg, M, N, K, G, seed=M + I + 5 * K, scale_dtype=sd)
+    y, yf = run_swiglu_pair(dev, xb, w, w_scale, N, K, G)
+    check_swiglu(yf, ow.silu_mul_bf16(y[:, :I], y[:, I:]), 0.99, f"fused vs unfused M{M} I{I}")
     q_ref, s_ref = ow.quant_act_per_token(xb)
     y32 = ow.gemm_fp32(q_ref, s_ref, w, ws32, G)
     full = ow.silu_mul_bf16(ow.f32_to_bf16_bits(y32[:, :I]), ow.f32_to_bf16_bits(y32[:, I:]))
