@@ -596,9 +596,8 @@ def decoder_trace_summary(db, timed=10):
 
 def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
     """prefill tokens/s and greedy decode tokens/s of the QwQ-32B-shaped decoder
-    (random W4A8 weights at group 128, bf16 attention on PyTorch-ROCm -- batched products below
-    decoder.SDPA_MIN_BATCH sequences, scaled_dot_product_attention from it on -- decode steps
-    replayed from a HIP graph)."""
+    (random W4A8 weights at group 128, attention on this build's bf16 MFMA kernel
+    w4a8_attention, decode steps replayed from a HIP graph)."""
     import torch
     cfg = pkg.decoder.DecoderConfig(layers=layers)
     t0 = time.perf_counter()
@@ -628,7 +627,8 @@ def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
         rows.append({"concurrency": B, "prompt_tokens": prompt, "decode_steps": steps,
                      "prefill_ms": round(pre_ms, 1), "prefill_tok_s": round(B * prompt / pre_ms * 1e3, 1),
                      "decode_ms_per_step": round(dec_ms / steps, 3), "decode_tok_s": round(B * steps / dec_ms * 1e3, 1),
-                     "attention": "scaled_dot_product_attention" if m.sdpa else "batched products",
+                     "attention": {"hip": "w4a8_attention", "sdpa": "scaled_dot_product_attention",
+                                   "matmul": "batched products"}[m.attention],
                      "last_tokens": [int(t) for t in out[-1][:4].tolist()]})
         log(f"  decoder B={B:3d}: prefill {pre_ms:9.1f} ms ({B * prompt / pre_ms * 1e3:9.0f} tok/s), decode "
             f"{dec_ms / steps:7.3f} ms/step ({B * steps / dec_ms * 1e3:8.1f} tok/s)")

@@ -47,7 +47,7 @@ enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
 /* Library ABI version (bumped on any signature or contract change: 4 = the
  * first build whose GEMM asks a workspace of some decode shapes; 5 adds
  * w4a8_rope_kv; 6 adds w4a8_stream_capture_id and requires 4-byte aligned
- * s_tiles). */
+ * s_tiles; 7 adds w4a8_attention and its two size queries). */
 int w4a8_abi_version(void);
 
 /* Message for the calling thread's last failed call ("" if none). */
@@ -272,6 +272,43 @@ int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t
 int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* bias, const void* cos_tab, const void* sin_tab, int64_t ldc,
                  int64_t L, const void* pos, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
                  const int64_t* v_strides, int64_t B, int64_t T, int64_t H, int64_t KVH, int64_t D, void* stream);
+
+/*
+ * Grouped-query attention of T query tokens per sequence over the KV cache,
+ * the attention of the decoder forward around the W4A8 linears.  Replaces the
+ * reference decoder layer's `F.scaled_dot_product_attention(q, k, v,
+ * enable_gqa=True)` over its in-place KV cache
+ * (npu_ops/python/bench_decode_layer.py:70-73), with the causal mask of a
+ * prefill and the cache length of a captured decode step read on the device.
+ *   q        bf16 [B, T, H, D]     (w4a8_rope_kv's q_out)
+ *   k_cache  bf16 [B, KVH, Lc, D]  keys, position-major
+ *   vt_cache bf16 [B, KVH, D, Lc]  values transposed (position fastest)
+ *   out      bf16 [B, T, H, D]
+ *   pos      int64 [1] (device)    token t attends to positions 0 .. pos[0] + t
+ *                                  (clamped to [0, L)); query head h*G + g reads
+ *                                  KV head h, G = H / KVH
+ * D = 64 or 128; Lc a multiple of 64, L <= Lc.  Per query row: scores in fp32
+ * times `scale`, softmax in base 2 over chunks of 64 positions with a running
+ * maximum, the probabilities rounded to bf16 for the product with V (fp32
+ * accumulation), chunks grouped into splits of `chunks_per_split` whose states
+ * are combined in split order, output bf16(O / l).  With `workspace` NULL one
+ * workgroup walks all splits of its rows (prefill); with a workspace of
+ * w4a8_attention_workspace_bytes bytes each split runs in its own workgroup and
+ * a second kernel combines them (decode).  Both return the same bits for the
+ * same row, cache and chunks_per_split.
+ */
+int w4a8_attention(const void* q, const void* k_cache, const void* vt_cache, void* out, const void* pos, int64_t B,
+                   int64_t T, int64_t H, int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t chunks_per_split,
+                   float scale, void* workspace, int64_t ws_bytes, void* stream);
+
+/* chunks_per_split for a decode step of B sequences (-1 for a bad shape): no split
+ * once B * KVH * ceil(G / 16) single-token row tiles give every CU one, otherwise
+ * splits up to about one workgroup per CU, at most max(8, Lc / 1024) of them. */
+int64_t w4a8_attention_chunks_per_split(int64_t B, int64_t H, int64_t KVH, int64_t Lc);
+
+/* Workspace bytes of the split launch (0 with a single split, -1 for a bad shape). */
+int64_t w4a8_attention_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int64_t Lc,
+                                       int64_t chunks_per_split);
 
 /*
  * ---- Reference-compat mid-group path ----

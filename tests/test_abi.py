@@ -32,7 +32,7 @@ def test_header_symbols_are_exported(pkg, lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.w4a8_abi_version() == 6
+    assert lib.w4a8_abi_version() == 7
     # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
     assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
@@ -171,3 +171,36 @@ def test_offset_limits_are_refused_on_every_path(lib):
     # 64 rows at a stride too large for one launch cannot be chunked
     lda = (1 << 31) // 150 // 16 * 16
     assert lib.w4a8_gemm(16, lda, 16, 16, 16, 0, 16, 64, 64, 64, 256, G, None, 0, None) == 5
+
+
+def test_attention_sizes_and_rejects_bad_arguments(lib):
+    # decode splits (256 CUs assumed without a GPU): 8 row tiles split 8 ways (3 chunks
+    # each), 64 tiles 4 ways, 512 tiles (one per CU at least) not at all; a long
+    # cache of one sequence into up to Lc / 1024 splits
+    assert lib.w4a8_attention_chunks_per_split(1, 40, 8, 1280) == 3
+    assert lib.w4a8_attention_chunks_per_split(8, 40, 8, 1280) == 5
+    assert lib.w4a8_attention_chunks_per_split(64, 40, 8, 1280) == 20
+    assert lib.w4a8_attention_chunks_per_split(1, 40, 8, 32768) == 16
+    assert lib.w4a8_attention_chunks_per_split(1, 40, 8, 1000) == -1      # cache axis not a multiple of 64
+    assert lib.w4a8_attention_chunks_per_split(1, 40, 7, 1280) == -1      # H not a multiple of KVH
+    # workspace: one state of D + 4 floats per row and split, none with a single split
+    assert lib.w4a8_attention_workspace_bytes(2, 1, 40, 128, 1280, 5) == 2 * 40 * 4 * 132 * 4
+    assert lib.w4a8_attention_workspace_bytes(2, 1, 40, 128, 1280, 3) == 2 * 40 * 7 * 132 * 4
+    assert lib.w4a8_attention_workspace_bytes(2, 1, 40, 128, 1280, 20) == 0
+
+    def call(**kw):
+        a = dict(q=16, k=16, vt=16, out=16, pos=16, B=1, T=1, H=40, KVH=8, D=128, L=1280, Lc=1280, cps=1,
+                 scale=0.088, ws=None, wsb=0)
+        a.update(kw)
+        return lib.w4a8_attention(a["q"], a["k"], a["vt"], a["out"], a["pos"], a["B"], a["T"], a["H"], a["KVH"],
+                                  a["D"], a["L"], a["Lc"], a["cps"], a["scale"], a["ws"], a["wsb"], None)
+    assert call(D=96) == 5 and b"64 or 128" in lib.w4a8_last_error()
+    assert call(KVH=7) == 2
+    assert call(Lc=1000) == 2 and b"multiple of 64" in lib.w4a8_last_error()
+    assert call(L=1300) == 2
+    assert call(cps=21) == 2 and b"chunks_per_split" in lib.w4a8_last_error()
+    assert call(scale=float("inf")) == 2
+    assert call(q=None) == 1
+    assert call(k=24) == 4
+    assert call(ws=16, wsb=100) == 6 and b"workspace needs" in lib.w4a8_last_error()
+    assert call(B=0, q=None) == 0

@@ -27,9 +27,10 @@ def tiny_cfg(pkg):
                                      group=64, rms_eps=1e-5, rope_theta=1.0e4, qkv_bias=True)
 
 
-# decode attention: "auto" is the batched-product path at these batch sizes,
-# "sdpa" the scaled_dot_product_attention path large batches take
-ATTENTION = ["auto", "sdpa"]
+# decoder attention paths: "auto" is this build's attention kernel (w4a8_attention);
+# "sdpa" (scaled_dot_product_attention) and "matmul" (two batched products) are the
+# PyTorch paths kept for comparison
+ATTENTION = ["auto", "sdpa", "matmul"]
 
 
 @pytest.mark.parametrize("attention", ATTENTION)
@@ -81,13 +82,19 @@ def test_prefill_decode_consistency(pkg, dev, attention):
     rel = (dec_logits - pre_logits).norm() / pre_logits.norm()
     say(f"  prefill/decode logits rel-L2 ({attention}): {rel:.5f}")
     assert rel < 2e-2, f"rel-L2 {rel}"
+    if m.attention == "hip":
+        # the attention kernel's decode and prefill launches return the same bits per
+        # row, and every other op here is row-wise at these sizes: exact agreement
+        assert torch.equal(dec_logits, pre_logits)
 
 
-def _ref_forward(m, tokens, bf16_probs=True):
+def _ref_forward(m, tokens, probs="bf16"):
     """float64 torch restatement of the same model on the CPU: dequantised weights and
     the per-token activation quant (bf16 scale, round half to even) in front of every linear.
-    bf16_probs: the attention probabilities rounded to bf16 before the product with V (the
-    batched-product path) or kept exact (scaled_dot_product_attention's kernel)."""
+    probs: how the attention probabilities meet V -- "bf16": the softmax rounded to bf16
+    (the batched-product path); "exact": unrounded (scaled_dot_product_attention's kernel);
+    "kernel": exp(s - max) rounded to bf16, the product divided by the unrounded sum (the
+    attention kernel when a row's positions fit one chunk of 64)."""
     c = m.cfg
     f = lambda t: t.detach().double().cpu()  # noqa: E731
 
@@ -126,8 +133,13 @@ def _ref_forward(m, tokens, bf16_probs=True):
         # probabilities
         sc = torch.einsum("bshd,bthd->bhst", q, k) / math.sqrt(c.head_dim)
         sc = sc + torch.full((S, S), float("-inf"), dtype=torch.float64).triu(1)
-        pr = torch.softmax(sc, -1)
-        a = bf16(torch.einsum("bhst,bthd->bshd", bf16(pr) if bf16_probs else pr, v)).reshape(B * S, -1)
+        if probs == "kernel":
+            e = torch.exp(sc - sc.amax(-1, keepdim=True))
+            a = torch.einsum("bhst,bthd->bshd", bf16(e), v) / e.sum(-1).transpose(1, 2)[..., None]
+            a = bf16(a).reshape(B * S, -1)
+        else:
+            pr = torch.softmax(sc, -1)
+            a = bf16(torch.einsum("bhst,bthd->bshd", bf16(pr) if probs == "bf16" else pr, v)).reshape(B * S, -1)
         x = bf16(x + qlinear(a, L["o"]))
         h = rms(x, L["ln2"])
         gu = qlinear(h, L["gate_up"])
@@ -147,15 +159,16 @@ def test_forward_matches_float_reference(pkg, dev, attention):
     prompt = torch.randint(0, cfg.vocab, (2, 16), generator=torch.Generator().manual_seed(2)).to(dev)
     m.prefill(prompt)
     got = m.last_logits.double().cpu()
-    ref = _ref_forward(m, prompt, bf16_probs=not m.sdpa)
+    assert m.attention != "hip" or m.max_len <= 64      # "kernel" emulates the one-chunk case
+    ref = _ref_forward(m, prompt, probs={"hip": "kernel", "sdpa": "exact", "matmul": "bf16"}[m.attention])
     rel = (got - ref).norm() / ref.norm()
     say(f"decoder logits rel-L2 vs float64 reference ({attention}): {rel:.5f}")
-    # The reference rounds as the batched-product path does (0.17% here).  The SDPA
-    # kernel accumulates in its own order: its attention outputs are within 2.6e-3
-    # rel-L2 of the batched-product path's (test_attention_paths_agree), and those
-    # last-bit differences flip int8 activation codes of the next projections, which
-    # moves this two-layer model's logits by 3.4-3.6% -- a wrong mask, position or
-    # cache write moves them by O(1).
+    # The reference rounds as the batched-product path and the attention kernel do
+    # (0.17% here for the products).  The SDPA kernel accumulates in its own order: its
+    # attention outputs are within 2.6e-3 rel-L2 of the other paths'
+    # (test_attention_paths_agree), and those last-bit differences flip int8 activation
+    # codes of the next projections, which moves this two-layer model's logits by
+    # 3.4-3.6% -- a wrong mask, position or cache write moves them by O(1).
     assert rel < (5e-2 if m.sdpa else 2e-2), f"rel-L2 {rel}"
 
 
@@ -184,31 +197,44 @@ def test_resize_then_capture_after_full_decode(pkg, dev, attention):
 
 
 def test_attention_paths_agree(pkg, dev):
-    """The two attention paths on the same queries and cache contents -- batched products
-    over the transposed K cache, scaled_dot_product_attention over the [L, D] cache -- agree
-    to the bf16 rounding of their outputs, at decode (masked positions past pos) and at
-    prefill (causal rows of every query head)."""
+    """The three attention paths on the same queries and cache contents -- the attention
+    kernel over the [Lc, D] / transposed-V cache, batched products over the transposed K
+    cache, scaled_dot_product_attention over the [L, D] cache -- agree to the bf16 rounding
+    of their outputs, at decode (masked positions past pos) and at prefill (causal rows of
+    every query head)."""
     say("decoder: attention paths")
     cfg = tiny_cfg(pkg)
     m = pkg.decoder.W4A8Decoder(cfg, batch=3, max_len=48, device=dev, seed=7, attention="matmul")
     g = torch.Generator(device=dev).manual_seed(8)
     B, KVH, D, L = 3, cfg.kv_heads, cfg.head_dim, 48
     G = cfg.heads // cfg.kv_heads
+    H = cfg.heads
     k = torch.randn((B, KVH, L, D), generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn((B, KVH, L, D), generator=g, device=dev).to(torch.bfloat16)
     kt = k.transpose(2, 3).contiguous()
+    k_store = torch.zeros((B, KVH, 64, D), dtype=torch.bfloat16, device=dev)
+    vt_store = torch.zeros((B, KVH, D, 64), dtype=torch.bfloat16, device=dev)
+    k_store[:, :, :L] = k
+    vt_store[..., :L] = v.transpose(2, 3)
     cases = []
     q = torch.randn((B, KVH, G, D), generator=g, device=dev).to(torch.bfloat16)
-    cases.append(("decode", q, torch.where(torch.arange(L, device=dev) > 30, float("-inf"), 0.0).view(1, 1, 1, L)))
+    cases.append(("decode", q, torch.where(torch.arange(L, device=dev) > 30, float("-inf"), 0.0).view(1, 1, 1, L),
+                  q.reshape(B, 1, H, D), 30, True))
     S = L
     q = torch.randn((B, KVH, G * S, D), generator=g, device=dev).to(torch.bfloat16)
-    cases.append(("prefill", q, torch.full((S, S), float("-inf"), device=dev).triu_(1).repeat(G, 1)))
-    for name, q, bias in cases:
+    cases.append(("prefill", q, torch.full((S, S), float("-inf"), device=dev).triu_(1).repeat(G, 1),
+                  q.view(B, KVH, G, S, D).permute(0, 3, 1, 2, 4).reshape(B, S, H, D).contiguous(), 0, False))
+    for name, q, bias, qh, p0, split in cases:
         a = m._attend(q, kt, v, bias).double()
         b = pkg.decoder._sdpa(q, k, v, bias.to(torch.bfloat16).view(1, 1, *bias.shape[-2:])).double()
-        rel = float((a - b).norm() / b.norm())
-        say(f"  {name}: rel-L2 {rel:.2e}")
-        assert rel < 4e-3, f"{name}: rel-L2 {rel}"
+        T = qh.shape[1]
+        pos = torch.full((1,), p0, dtype=torch.int64, device=dev)
+        c = torch.ops.npu.w4a8_attention(qh, k_store, vt_store, pos, L, 1, split)
+        c = c.view(B, T, KVH, G, D).permute(0, 2, 3, 1, 4).reshape(B, KVH, G * T, D).double()
+        for tag, x, y in (("products vs sdpa", a, b), ("kernel vs products", c, a), ("kernel vs sdpa", c, b)):
+            rel = float((x - y).norm() / y.norm())
+            say(f"  {name} {tag}: rel-L2 {rel:.2e}")
+            assert rel < 4e-3, f"{name} {tag}: rel-L2 {rel}"
 
 
 def test_decoder_rejects_unknown_attention(pkg):

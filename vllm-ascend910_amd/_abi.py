@@ -15,7 +15,7 @@ from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "_lib" / "libw4a8_amd.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1
@@ -48,6 +48,10 @@ SIGNATURES = {
                                       _VP, _I64, _VP]),
     "w4a8_rope_kv": (_I, [_VP, _I64, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, ctypes.POINTER(_I64), _VP,
                           ctypes.POINTER(_I64), _I64, _I64, _I64, _I64, _I64, _VP]),
+    "w4a8_attention": (_I, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                            ctypes.c_float, _VP, _I64, _VP]),
+    "w4a8_attention_chunks_per_split": (_I64, [_I64, _I64, _I64, _I64]),
+    "w4a8_attention_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
 }
 
 STATUS_NAMES = {0: "OK", 1: "NULL", 2: "SHAPE", 3: "DTYPE", 4: "ALIGN", 5: "UNSUPPORTED", 6: "WORKSPACE",

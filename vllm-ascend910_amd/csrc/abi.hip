@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdio>
 #include <mutex>
 #include <string>
@@ -208,7 +209,7 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 6; }
+int w4a8_abi_version(void) { return 7; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
@@ -512,6 +513,81 @@ int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* bias, const void* cos
     a.D = static_cast<int>(D);
     a.L = L;
     return hip_status(launch_rope_kv(a, static_cast<hipStream_t>(stream)), "w4a8_rope_kv launch");
+}
+
+int64_t w4a8_attention_chunks_per_split(int64_t B, int64_t H, int64_t KVH, int64_t Lc) {
+    if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || Lc <= 0 || Lc % 64 != 0) return -1;
+    // A single-token step has only B * KVH * ceil(G / 16) row tiles.  With at
+    // least one per CU the cache is streamed unsplit (more splits only add
+    // workspace traffic and the combine launch: measured on MI355X, 64 x 8 tiles
+    // over 1280 positions 54 us unsplit against 63-86 us split 4-20 ways).
+    // Fewer tiles are split until there is about one workgroup per CU, but
+    // into at most max(8, chunks / 16) splits, the combine's sequential fold
+    // being the price of each (one tile per KV head of one sequence: 10.6 us at
+    // 7 splits against 13.9 us at 20).
+    const int64_t nch = Lc / 64;
+    const int64_t tiles = B * KVH * ((H / KVH + 15) / 16);
+    const int64_t cus = device_cu_count();
+    int64_t splits = 1;
+    if (tiles < cus) splits = std::min({(cus + tiles - 1) / tiles, std::max<int64_t>(8, nch / 16), nch});
+    return (nch + splits - 1) / splits;
+}
+
+int64_t w4a8_attention_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int64_t Lc, int64_t cps) {
+    if (B <= 0 || T <= 0 || H <= 0 || D <= 0 || Lc <= 0 || Lc % 64 != 0 || cps <= 0) return -1;
+    const int64_t ns = (Lc / 64 + cps - 1) / cps;
+    return ns > 1 ? B * T * H * ns * (D + 4) * 4 : 0;
+}
+
+int w4a8_attention(const void* q, const void* k_cache, const void* vt_cache, void* out, const void* pos, int64_t B,
+                   int64_t T, int64_t H, int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t cps, float scale,
+                   void* workspace, int64_t ws_bytes, void* stream) {
+    if (B < 0 || T < 0 || B * T >= (1ll << 31))
+        return fail(W4A8_ERR_SHAPE, "bad shape: B=%lld T=%lld", B, T);
+    if (H <= 0 || KVH <= 0 || H % KVH != 0 || H / KVH > 65535 || H >= (1ll << 20))
+        return fail(W4A8_ERR_SHAPE, "bad heads: H=%lld KVH=%lld (H a multiple of KVH)", H, KVH);
+    if (D != 64 && D != 128) return fail(W4A8_ERR_UNSUPPORTED, "head_dim D=%lld: 64 or 128 supported", D);
+    if (Lc <= 0 || Lc % 64 != 0 || L <= 0 || L > Lc || Lc * D * 2 >= (1ll << 31))
+        return fail(W4A8_ERR_SHAPE, "cache: need 0 < L=%lld <= Lc=%lld, Lc a multiple of 64, Lc*D*2 < 2^31", L, Lc);
+    if (cps <= 0 || cps > Lc / 64) return fail(W4A8_ERR_SHAPE, "chunks_per_split=%lld must be in [1, Lc/64]", cps);
+    if (!std::isfinite(scale)) return fail(W4A8_ERR_SHAPE, "scale must be finite");
+    if (B * T == 0) return W4A8_OK;
+    if (!q || !k_cache || !vt_cache || !out || !pos) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(vt_cache, 16) || !aligned(out, 16) || !aligned(pos, 8) ||
+        !aligned(workspace, 16))
+        return fail(W4A8_ERR_ALIGN, "q, caches, out and workspace 16-byte aligned, pos 8-byte aligned");
+    const int64_t pairs = B * KVH, G = H / KVH;
+    const int64_t tiles = (G * T + 15) / 16;
+    const int64_t ns = (Lc / 64 + cps - 1) / cps;
+    const bool split = workspace != nullptr;
+    if (split) {
+        const int64_t need = w4a8_attention_workspace_bytes(B, T, H, D, Lc, cps);
+        if (ws_bytes < need) return fail(W4A8_ERR_WORKSPACE, "workspace needs %lld bytes (got %lld)", need, ws_bytes);
+        if (pairs > 65535 || tiles > 65535 || pairs * G * T >= (1ll << 31))
+            return fail(W4A8_ERR_UNSUPPORTED, "split launch: B*KVH=%lld and row tiles %lld must be <= 65535", pairs,
+                        tiles);
+    } else if (pairs * tiles >= (1ll << 31)) {
+        return fail(W4A8_ERR_SHAPE, "too many row tiles: %lld", pairs * tiles);
+    }
+    AttnArgs a{};
+    a.q = static_cast<const uint16_t*>(q);
+    a.k = static_cast<const uint16_t*>(k_cache);
+    a.vt = static_cast<const uint16_t*>(vt_cache);
+    a.out = static_cast<uint16_t*>(out);
+    a.ws = static_cast<float*>(workspace);
+    a.pos = static_cast<const int64_t*>(pos);
+    a.B = static_cast<int>(B);
+    a.T = static_cast<int>(T);
+    a.H = static_cast<int>(H);
+    a.KVH = static_cast<int>(KVH);
+    a.G = static_cast<int>(G);
+    a.D = static_cast<int>(D);
+    a.L = static_cast<int>(L);
+    a.Lc = static_cast<int>(Lc);
+    a.cps = static_cast<int>(cps);
+    a.ns = static_cast<int>(ns);
+    a.cs = static_cast<float>(1.4426950408889634 * static_cast<double>(scale));
+    return hip_status(launch_attention(a, split, static_cast<hipStream_t>(stream)), "w4a8_attention launch");
 }
 
 }  // extern "C"

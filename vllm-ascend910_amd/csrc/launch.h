@@ -167,6 +167,22 @@ struct RopeKvArgs {
 };
 hipError_t launch_rope_kv(const RopeKvArgs& a, hipStream_t stream);
 
+// Grouped-query attention of the query rows of a decode step or a prefill over
+// the KV cache (attention.hip).
+struct AttnArgs {
+    const uint16_t* q;      // bf16 [B, T, H, D]
+    const uint16_t* k;      // bf16 [B, KVH, Lc, D]
+    const uint16_t* vt;     // bf16 [B, KVH, D, Lc]
+    uint16_t* out;          // bf16 [B, T, H, D]
+    float* ws;              // split launch with ns > 1: B * H * T * ns states of D + 4 floats
+    const int64_t* pos;     // device: position of token 0 of every sequence
+    int B, T, H, KVH, G, D; // G = H / KVH query heads per KV head; D = 64 or 128
+    int L, Lc;              // attended positions are clamped to [0, L); Lc = cache axis, multiple of 64
+    int cps, ns;            // chunks of 64 positions per split; splits = ceil(Lc / 64 / cps)
+    float cs;               // log2(e) * softmax scale
+};
+hipError_t launch_attention(const AttnArgs& a, bool split, hipStream_t stream);
+
 // Streaming read of [src, src + bytes) (bytes a multiple of 16, src 16-byte
 // aligned); sink (4 bytes) is written only for one improbable fold value.
 hipError_t launch_read_floor(const void* src, int64_t bytes, uint32_t* sink, hipStream_t stream);

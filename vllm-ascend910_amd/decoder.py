@@ -14,20 +14,28 @@ embeddings, RMSNorm) on this build's ops:
 * the rotary embedding of q and k and the KV-cache append run as one kernel
   (``torch.ops.npu.w4a8_rope_kv``, fp32 products and sums rounded to bf16 as
   torch rounds them on float tensors);
-* attention stays on PyTorch-ROCm in bf16.  The query heads of one KV head
-  form the rows of one attention problem, so grouped-query attention needs no
-  head repeat.  From ``SDPA_MIN_BATCH`` sequences on, prefill and decode call
+* attention runs on this build's grouped-query attention kernel
+  (``torch.ops.npu.w4a8_attention``, bf16 MFMA, csrc/attention.hip): the
+  query heads of one KV head form the rows of one problem (no head repeat),
+  the causal limit of every row and the cache length of a captured decode
+  step are read on the device, so a decode step reads only the positions
+  written so far.  Decode launches one workgroup per split of the cache plus a
+  combine kernel; prefill walks all splits per workgroup; both return the
+  same bits for the same row, so a prefill of t + 1 tokens and a prefill of t
+  tokens followed by a decode step agree exactly.  The K cache is stored
+  ``[B, KVH, Lc, D]`` and V transposed ``[B, KVH, D, Lc]`` (Lc = max_len
+  rounded up to 64).  The earlier PyTorch paths stay selectable for
+  comparison: ``attention="sdpa"`` calls
   ``torch.nn.functional.scaled_dot_product_attention`` on its efficient
   backend only (the reference's own call,
   npu_ops/python/bench_decode_layer.py:73; the math backend, whose batched
-  products take a transposed bf16 operand, is never used), over a K cache
-  stored ``[B, KVH, L, D]``.  Smaller batches use two contiguous batched
+  products take a transposed bf16 operand, is never used) over a K cache
+  stored ``[B, KVH, L, D]``; ``attention="matmul"`` two contiguous batched
   products over a K cache stored transposed ``[B, KVH, D, L]``, the scores
-  returned in fp32 as SDPA keeps them.  Measured on MI355X (graph replays,
-  one layer's decode attention over 1280 positions, us): products / SDPA 25
-  / 60 at 1 sequence, 28 / 65 at 8, 55 / 66 at 32, 83 / 81 at 48, 120 / 93
-  at 64; prefill of one 1024-token sequence 233 / 93.  Prefill follows the
-  batch's path so that a prefill and the decode after it round alike;
+  returned in fp32.  Measured on MI355X (graph replays, one layer's decode
+  attention at position 1100 of a 1280-position cache, us): kernel / products
+  / SDPA 10.6 / 25 / 60 at 1 sequence, 14.8 / 28 / 65 at 8, 53.9 / 120 / 93 at
+  64; prefill of one 1024-token sequence 34.7 / 233 / 94.5;
 * the decode step is shape-static -- position, RoPE row, KV write index and
   mask are device tensors -- so it is captured once per batch size in a HIP
   graph and replayed, the greedy token feeding the next step inside the graph.
@@ -102,12 +110,6 @@ class _Linear:
         return torch.ops.npu.w4a8_gemm_swiglu(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
 
 
-# Batches from this size on attend through scaled_dot_product_attention (the
-# K cache then stored [B, KVH, L, D]); smaller ones through two batched products
-# over the transposed K cache.
-SDPA_MIN_BATCH = 48
-
-
 def _sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
     """softmax(q k^T / sqrt(D) + mask) v on the efficient backend (an error, not a fallback,
     where it cannot run).  q [B, KVH, R, D], k and v [B, KVH, L, D], mask bf16 broadcastable
@@ -125,12 +127,13 @@ class W4A8Decoder:
                  keep_weights=False, attention: str = "auto"):
         """keep_weights: True keeps every linear's int8 codes and scales (reference
         checks of small models), a collection of layer indices keeps those layers' only.
-        attention: "sdpa", "matmul", or "auto" (sdpa from SDPA_MIN_BATCH sequences on), for
-        prefill and decode alike (the two paths round differently, so a prefill and the
-        decode after it share one).  The choice is made again by resize()."""
-        if attention not in ("auto", "sdpa", "matmul"):
-            raise ValueError(f"attention must be 'auto', 'sdpa' or 'matmul', not {attention!r}")
-        self.attention = attention
+        attention: "hip" (this build's attention kernel; "auto" is the same), "sdpa" or
+        "matmul", for prefill and decode alike (the paths round differently, so a prefill and
+        the decode after it share one)."""
+        if attention not in ("auto", "hip", "sdpa", "matmul"):
+            raise ValueError(f"attention must be 'auto', 'hip', 'sdpa' or 'matmul', not {attention!r}")
+        self.attention = "hip" if attention == "auto" else attention
+        self.sdpa = self.attention == "sdpa"
         self.cfg, self.batch, self.max_len = cfg, batch, max_len
         dev = torch.device(device)
         self.device = dev
@@ -168,7 +171,7 @@ class W4A8Decoder:
         c, dev = self.cfg, self.device
         self.batch, self.max_len = batch, max_len
         self._graph = None
-        self.k_cache = self.v_cache = self._k_ld = None
+        self.k_cache = self.v_cache = self._k_ld = self._k_store = self._vt_store = None
         torch.cuda.empty_cache()
         self._alloc_cache(batch, max_len)
         inv = 1.0 / (c.rope_theta ** (torch.arange(0, c.head_dim, 2, device=dev, dtype=torch.float32) / c.head_dim))
@@ -179,18 +182,29 @@ class W4A8Decoder:
         self.pos.zero_()
 
     def _alloc_cache(self, batch: int, max_len: int) -> None:
-        """KV caches for the batch size's attention path.  k_cache[li] is always a
-        [B, KVH, D, L] tensor (what w4a8_rope_kv writes through): the storage itself for
-        the batched-product decode, else a transposed view of _k_ld[li] [B, KVH, L, D],
-        the layout scaled_dot_product_attention reads.  v_cache[li] is [B, KVH, L, D]."""
+        """KV caches in the layout of the attention path.  k_cache[li] is always a
+        [B, KVH, D, L] tensor and v_cache[li] a [B, KVH, L, D] tensor (what w4a8_rope_kv
+        writes through):
+          hip     views of _k_store[li] [B, KVH, Lc, D] and _vt_store[li] [B, KVH, D, Lc]
+                  (Lc = max_len rounded up to 64; positions past max_len stay zero);
+          sdpa    a transposed view of _k_ld[li] [B, KVH, L, D]; v_cache itself;
+          matmul  both caches themselves."""
         c, dev = self.cfg, self.device
         kvh, d = c.kv_heads, c.head_dim
-        self.sdpa = self.attention == "sdpa" or (self.attention == "auto" and batch >= SDPA_MIN_BATCH)
+        self._k_ld = self._k_store = self._vt_store = None
+        if self.attention == "hip":
+            lc = -(-max_len // 64) * 64
+            self._k_store = [torch.zeros((batch, kvh, lc, d), dtype=torch.bfloat16, device=dev) for _ in self.layers]
+            self._vt_store = [torch.zeros((batch, kvh, d, lc), dtype=torch.bfloat16, device=dev)
+                              for _ in self.layers]
+            self.k_cache = [k[:, :, :max_len].transpose(2, 3) for k in self._k_store]
+            self.v_cache = [v[..., :max_len].transpose(2, 3) for v in self._vt_store]
+            self.cps = ops.attention_chunks_per_split(batch, c.heads, kvh, lc)
+            return
         if self.sdpa:
             self._k_ld = [torch.zeros((batch, kvh, max_len, d), dtype=torch.bfloat16, device=dev) for _ in self.layers]
             self.k_cache = [k.transpose(2, 3) for k in self._k_ld]
         else:
-            self._k_ld = None
             self.k_cache = [torch.zeros((batch, kvh, d, max_len), dtype=torch.bfloat16, device=dev)
                             for _ in self.layers]
         self.v_cache = [torch.zeros((batch, kvh, max_len, d), dtype=torch.bfloat16, device=dev) for _ in self.layers]
@@ -239,15 +253,21 @@ class W4A8Decoder:
         S = tokens.shape[1]
         assert tokens.shape[0] == B and S <= self.max_len
         G = c.heads // c.kv_heads
-        # rows of one KV head's problem are (query head g, token s) = g * S + s
-        bias = torch.full((S, S), float("-inf"), device=self.device).triu_(1).repeat(G, 1)
-        mask = bias.to(torch.bfloat16).view(1, 1, G * S, S)
+        if self.attention != "hip":
+            # rows of one KV head's problem are (query head g, token s) = g * S + s
+            bias = torch.full((S, S), float("-inf"), device=self.device).triu_(1).repeat(G, 1)
+            mask = bias.to(torch.bfloat16).view(1, 1, G * S, S)
         x = self.embed[tokens.reshape(-1)]                               # [B*S, hidden]
         delta = None
         for li, L in enumerate(self.layers):
             aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
             x = s if delta is not None else x
             q = self._rope_kv(li, L, aq, as_, S, self._pos0)        # [B, S, H, D]; caches filled for [0, S)
+            if self.attention == "hip":
+                out = torch.ops.npu.w4a8_attention(q, self._k_store[li], self._vt_store[li], self._pos0,
+                                                   self.max_len, self.cps, False).view(B * S, -1)
+                x, delta = self._mlp_and_next(L, x, out)
+                continue
             qg = q.view(B, S, c.kv_heads, G, c.head_dim).permute(0, 2, 3, 1, 4).reshape(B, c.kv_heads, G * S,
                                                                                        c.head_dim)
             if self.sdpa:
@@ -279,9 +299,10 @@ class W4A8Decoder:
         """One greedy step at self.pos for self.tokens, updating both in place (capturable)."""
         c, B = self.cfg, self.batch
         G = c.heads // c.kv_heads
-        bias = torch.where(self.positions > self.pos, float("-inf"), 0.0).view(1, 1, 1, self.max_len)
-        if self.sdpa:
-            bias = bias.to(torch.bfloat16)
+        if self.attention != "hip":
+            bias = torch.where(self.positions > self.pos, float("-inf"), 0.0).view(1, 1, 1, self.max_len)
+            if self.sdpa:
+                bias = bias.to(torch.bfloat16)
         x = self.embed.index_select(0, self.tokens)                      # [B, hidden]
         delta = None
         for li, L in enumerate(self.layers):
@@ -289,7 +310,10 @@ class W4A8Decoder:
             x = s if delta is not None else x
             q = self._rope_kv(li, L, aq, as_, 1, self.pos)               # [B, 1, H, D]
             qg = q.view(B, c.kv_heads, G, c.head_dim)
-            if self.sdpa:
+            if self.attention == "hip":
+                o = torch.ops.npu.w4a8_attention(q, self._k_store[li], self._vt_store[li], self.pos, self.max_len,
+                                                 self.cps, True)
+            elif self.sdpa:
                 o = _sdpa(qg, self._k_ld[li], self.v_cache[li], bias)              # [B, KVH, G, D]
             else:
                 o = self._attend(qg, self.k_cache[li], self.v_cache[li], bias)      # [B, KVH, G, D]

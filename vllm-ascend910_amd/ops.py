@@ -17,6 +17,7 @@ and two producer-side helpers of the decoder forward that drives them:
     torch.ops.npu.w4a8_rmsnorm_quant(x, weight, eps, residual=None, group=0, want_normed=False)
         -> (a_q, a_scale, s, h)
     torch.ops.npu.w4a8_rope_kv(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads, bias=None) -> q
+    torch.ops.npu.w4a8_attention(q, k_cache, vt_cache, pos, L, chunks_per_split, split=False, scale=None) -> out
 
 and, with the reference's own names and schemas (group appended with the
 reference's fixed value as default), its mid-group compat pair:
@@ -56,6 +57,8 @@ _LIB.define("w4a8_rmsnorm_quant(Tensor x, Tensor weight, float eps, Tensor? resi
             "bool want_normed=False) -> (Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("w4a8_rope_kv(Tensor qkv, Tensor cos, Tensor sin, Tensor pos, Tensor(a!) k_cache, Tensor(b!) v_cache, "
             "int heads, int kv_heads, Tensor? bias=None) -> Tensor")
+_LIB.define("w4a8_attention(Tensor q, Tensor k_cache, Tensor vt_cache, Tensor pos, int L, int chunks_per_split, "
+            "bool split=False, float? scale=None) -> Tensor")
 _LIB.define("midgroup_quant_a(Tensor x, int group=1024) -> Tensor[]")
 _LIB.define("midgroup_w4a8_gemm(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
             "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> Tensor")
@@ -388,6 +391,56 @@ def _rope_kv_cuda(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: 
 def _rope_kv_fake(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads, bias=None):
     B, T, W = qkv.shape
     return qkv.new_empty((B, T, heads, W // (heads + 2 * kv_heads)))
+
+
+# ---------------------------------------------------------------- attention over the KV cache
+def attention_chunks_per_split(batch: int, heads: int, kv_heads: int, cache_len: int) -> int:
+    """The split size (in chunks of 64 positions) the library picks for a decode step of
+    `batch` sequences over a cache axis of cache_len positions (a multiple of 64)."""
+    cps = _abi.lib().w4a8_attention_chunks_per_split(batch, heads, kv_heads, cache_len)
+    _require(cps > 0, f"w4a8_attention: bad shape for the split size (B={batch}, H={heads}, KVH={kv_heads}, "
+             f"Lc={cache_len})")
+    return int(cps)
+
+
+@torch.library.impl(_LIB, "w4a8_attention", "CUDA")
+def _attention_cuda(q: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor, pos: torch.Tensor, L: int,
+                    chunks_per_split: int, split: bool = False, scale=None) -> torch.Tensor:
+    """out [B, T, H, D]: query rows q [B, T, H, D] over k_cache [B, KVH, Lc, D] and the
+    transposed values vt_cache [B, KVH, D, Lc]; token t attends to positions 0 .. pos[0] + t
+    (clamped to [0, L)).  split=True runs one workgroup per split plus a combine kernel
+    (decode), split=False one workgroup per row tile (prefill): the same bits either way."""
+    _require(q.dim() == 4 and q.dtype == torch.bfloat16, "w4a8_attention: q must be bfloat16 [B, T, H, D]")
+    B, T, H, D = q.shape
+    _require(k_cache.dim() == 4 and vt_cache.dim() == 4 and k_cache.dtype == torch.bfloat16
+             and vt_cache.dtype == torch.bfloat16, "w4a8_attention: caches must be 4-D bfloat16")
+    KVH, Lc = k_cache.shape[1], k_cache.shape[2]
+    _require(tuple(k_cache.shape) == (B, KVH, Lc, D) and tuple(vt_cache.shape) == (B, KVH, D, Lc),
+             "w4a8_attention: caches must be k [B, kv_heads, Lc, D] and vt [B, kv_heads, D, Lc]")
+    _require(k_cache.is_contiguous() and vt_cache.is_contiguous(), "w4a8_attention: caches must be contiguous")
+    _require(pos.dtype == torch.int64 and pos.numel() == 1 and pos.device == q.device,
+             "w4a8_attention: pos must be one int64 on the device")
+    q = q.contiguous()
+    out = torch.empty_like(q)
+    if B * T == 0:
+        return out
+    sc = float(scale) if scale is not None else 1.0 / float(D) ** 0.5
+    lib = _abi.lib()
+    ws_ptr, ws_bytes = None, 0
+    if split:
+        need = lib.w4a8_attention_workspace_bytes(B, T, H, D, Lc, chunks_per_split)
+        _require(need >= 0, "w4a8_attention: bad shape for the workspace size")
+        ws = _workspace(q.device, max(need, 16))
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    _abi.check(lib.w4a8_attention(q.data_ptr(), k_cache.data_ptr(), vt_cache.data_ptr(), out.data_ptr(),
+                                  pos.data_ptr(), B, T, H, KVH, D, L, Lc, chunks_per_split, sc, ws_ptr, ws_bytes,
+                                  _stream(q.device)), "w4a8_attention")
+    return out
+
+
+@torch.library.register_fake("npu::w4a8_attention")
+def _attention_fake(q, k_cache, vt_cache, pos, L, chunks_per_split, split=False, scale=None):
+    return torch.empty_like(q)
 
 
 # ---------------------------------------------------------------- mid-group compat pair
