@@ -80,6 +80,10 @@ def main():
                     help="skip the tensor-parallel shard shapes (TP=4 slices of the four projections)")
     ap.add_argument("--no-perchannel", action="store_true",
                     help="skip the per-channel (group = K) points beside the reference's published ones")
+    ap.add_argument("--no-attention", action="store_true",
+                    help="skip the decoder's attention kernel (w4a8_attention) at concurrency 1/8/64")
+    ap.add_argument("--attention-sweep", action="store_true",
+                    help="with the attention leg: also every split size (chunks per split 1-20) per concurrency")
     ap.add_argument("--no-detail", action="store_true", help="only the timed steps (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -486,6 +490,9 @@ def main():
     # ---------------------------------------------------------------- TP=4 shard shapes (one GPU's slice)
     if not args.no_tp4:
         result["tp4_shapes"] = tp4(pkg, dev, synth, make_pool, time_graph, T)
+    # ---------------------------------------------------------------- decoder attention
+    if not args.no_attention:
+        result["attention_shapes"] = attention_bench(pkg, dev, time_graph, args.cold_bytes, args.attention_sweep)
     # ---------------------------------------------------------------- decoder forward
     if not args.no_decoder:
         result["decoder"] = decoder_bench(pkg, dev, args.decoder_layers, steps=args.decoder_steps)
@@ -592,6 +599,85 @@ def decoder_trace_summary(db, timed=10):
     print("| kernel | per step | calls per step | us per call |\n|---|---:|---:|---:|")
     for k, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:24]:
         print(f"| `{k}` | {t / timed:.1f} us | {c / timed:.0f} | {t / c:.2f} |")
+
+
+def attention_bench(pkg, dev, time_graph, cold_gib, sweep=False, batches=(1, 8, 64)):
+    """The decoder's attention kernel at QwQ-32B heads (40 query heads, 8 KV heads, head_dim
+    128) over the bench decoder's cache (1024 + 256 positions).  Decode: one query token per
+    sequence at position 1100 (a split launch and, with more than one split, the combine),
+    cold -- each launch reads its own copy of the cache from a pool of >= cold_gib GiB --
+    against the attended K and V bytes B * 8 * 1101 * 128 * 2 * 2; beside it
+    scaled_dot_product_attention (efficient backend) on the same cache in [L, D] layout.
+    Prefill: a 1024-token prompt per sequence (causal), against the MFMA work
+    4 * B * 40 * 128 * S (S + 1) / 2 flops and the 2.5 PFLOP/s bf16 peak."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    H, KVH, D, L, P = 40, 8, 128, 1280, 1100
+    G = H // KVH
+    rows = []
+    for B in batches:
+        per = B * KVH * L * D * 2 * 2
+        n = max(4, min(256, math.ceil(cold_gib * 2 ** 30 / per)))
+        kp = torch.randn((n, B, KVH, L, D), device=dev).to(torch.bfloat16)
+        vp = torch.randn((n, B, KVH, D, L), device=dev).to(torch.bfloat16)
+        q = torch.randn((B, 1, H, D), device=dev).to(torch.bfloat16)
+        pos = torch.full((1,), P, dtype=torch.int64, device=dev)
+        base = pkg.ops.attention_chunks_per_split(B, H, KVH, L)
+        attended = B * KVH * (P + 1) * D * 2 * 2
+
+        def run(cps):
+            for i in range(n):
+                torch.ops.npu.w4a8_attention(q, kp[i], vp[i], pos, L, cps, True)
+        row = {"phase": "decode", "concurrency": B, "position": P, "cache": L, "chunks_per_split": base,
+               "splits": -(-(L // 64) // base)}
+        us = time_graph(lambda: run(base)) / n
+        row.update({"us": round(us, 2), "attended_MB": round(attended / 1e6, 2),
+                    "TB_s": round(attended / us / 1e6, 3), "frac_8TBs": round(attended / us / 1e6 / 8.0, 3)})
+        if sweep:
+            row["sweep_us"] = {c: round(time_graph(lambda c=c: run(c)) / n, 2) for c in range(1, 21)}
+        # scaled_dot_product_attention over the same positions ([L, D] values, a bf16 mask)
+        ks, vs = kp[: min(n, 8)], vp[: min(n, 8)].transpose(3, 4).contiguous()
+        mask = torch.where(torch.arange(L, device=dev) > P, float("-inf"), 0.0).to(torch.bfloat16)
+        qg = q.view(B, KVH, G, D)
+
+        def sd():
+            with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+                for i in range(ks.shape[0]):
+                    torch.nn.functional.scaled_dot_product_attention(qg, ks[i], vs[i],
+                                                                     attn_mask=mask.expand(B, KVH, G, L))
+        row["sdpa_us"] = round(time_graph(sd) / ks.shape[0], 2)
+        rows.append(row)
+        log(f"  attention decode B={B:3d}: {us:7.2f} us ({row['TB_s']:.2f} TB/s of attended K/V, "
+            f"{row['splits']} splits), sdpa {row['sdpa_us']:.2f} us")
+        del kp, vp, ks, vs
+        torch.cuda.empty_cache()
+    for B, S in ((1, 1024), (8, 1024), (64, 1024)):
+        k = torch.randn((B, KVH, L, D), device=dev).to(torch.bfloat16)
+        vt = torch.randn((B, KVH, D, L), device=dev).to(torch.bfloat16)
+        q = torch.randn((B, S, H, D), device=dev).to(torch.bfloat16)
+        pos = torch.zeros((1,), dtype=torch.int64, device=dev)
+        cps = pkg.ops.attention_chunks_per_split(B, H, KVH, L)
+        us = time_graph(lambda: torch.ops.npu.w4a8_attention(q, k, vt, pos, L, cps, False))
+        flops = 4 * B * H * D * S * (S + 1) / 2
+        row = {"phase": "prefill", "concurrency": B, "prompt": S, "us": round(us, 1),
+               "us_per_sequence": round(us / B, 1), "TFLOP_s": round(flops / us / 1e6, 1),
+               "frac_bf16_peak": round(flops / us / 1e6 / 2500.0, 3)}
+        if B == 1:
+            qs = q.view(B, S, KVH, G, D).permute(0, 2, 3, 1, 4).reshape(B, KVH, G * S, D).contiguous()
+            kk, vv = k[:, :, :S].contiguous(), vt[..., :S].transpose(2, 3).contiguous()
+            pmask = torch.full((S, S), float("-inf"), device=dev).triu_(1).repeat(G, 1).to(torch.bfloat16)
+
+            def sdp():
+                with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+                    torch.nn.functional.scaled_dot_product_attention(
+                        qs, kk, vv, attn_mask=pmask.view(1, 1, G * S, S).expand(B, KVH, G * S, S))
+            row["sdpa_us"] = round(time_graph(sdp), 1)
+        rows.append(row)
+        log(f"  attention prefill B={B:3d} S={S}: {us:9.1f} us ({row['TFLOP_s']:.0f} TFLOP/s causal)"
+            + (f", sdpa {row['sdpa_us']:.1f} us" if "sdpa_us" in row else ""))
+        del k, vt, q
+        torch.cuda.empty_cache()
+    return rows
 
 
 def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
