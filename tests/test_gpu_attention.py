@@ -183,6 +183,38 @@ def test_decode_launch_in_a_graph(pkg, dev):
         assert torch.equal(out, eager), f"replay at position {p} differs"
 
 
+def random_attention_shapes(seed: int, n: int):
+    """n seeded (B, T, H, KVH, D, L, pos0) draws: 1-6 sequences, 1-40 tokens, 1-20 query
+    heads per KV head (tiles of 16 rows straddled or not), head_dim 64 or 128, caches of
+    1-700 positions (one chunk to eleven), the first token anywhere in the cache."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        KVH = int(rng.integers(1, 5))
+        G = int(rng.integers(1, 21))
+        D = int(rng.choice([64, 128]))
+        L = int(rng.integers(1, 701))
+        T = int(rng.integers(1, min(40, L) + 1))
+        pos0 = int(rng.integers(0, L - T + 1))
+        out.append((int(rng.integers(1, 7)), T, KVH * G, KVH, D, L, pos0))
+    return out
+
+
+@pytest.mark.parametrize("B,T,H,KVH,D,L,pos0", random_attention_shapes(5, 16))
+def test_attention_random_shapes(pkg, dev, B, T, H, KVH, D, L, pos0):
+    """Seeded random shapes: both launches within the bound of the float64 attention and
+    equal to each other bit for bit, at the library's split size and at one chunk per split."""
+    say(f"attention random B={B} T={T} H={H} KVH={KVH} D={D} L={L} pos0={pos0}")
+    q, k, vt, Lc = make_inputs(dev, B, T, H, KVH, D, L, seed=B * 31 + T + L)
+    pos = torch.full((1,), pos0, dtype=torch.int64, device=dev)
+    ref, mag = reference(q, k, vt, pos0, L)
+    for cps in sorted({1, pkg.ops.attention_chunks_per_split(B, H, KVH, Lc)}):
+        pre = attn(q, k, vt, pos, L, cps, split=False)
+        check(pre, ref, mag, f"cps={cps}")
+        assert torch.equal(pre, attn(q, k, vt, pos, L, cps, split=True)), f"split launch differs (cps={cps})"
+
+
 def test_attention_rejects_bad_arguments(pkg, dev):
     q, k, vt, Lc = make_inputs(dev, 1, 1, 4, 2, 64, 64, seed=1)
     pos = torch.zeros((1,), dtype=torch.int64, device=dev)
