@@ -47,7 +47,8 @@ enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
 /* Library ABI version (bumped on any signature or contract change: 4 = the
  * first build whose GEMM asks a workspace of some decode shapes; 5 adds
  * w4a8_rope_kv; 6 adds w4a8_stream_capture_id and requires 4-byte aligned
- * s_tiles; 7 adds w4a8_attention and its two size queries). */
+ * s_tiles; 7 adds w4a8_attention and its two size queries; 8 adds
+ * w4a8_attention_rope). */
 int w4a8_abi_version(void);
 
 /* Message for the calling thread's last failed call ("" if none). */
@@ -300,6 +301,25 @@ int w4a8_rope_kv(const void* qkv, int64_t ldq, const void* bias, const void* cos
 int w4a8_attention(const void* q, const void* k_cache, const void* vt_cache, void* out, const void* pos, int64_t B,
                    int64_t T, int64_t H, int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t chunks_per_split,
                    float scale, void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * A decode step's attention (one query token per sequence, split launch) with
+ * w4a8_rope_kv's work fused in: the q heads are taken from the qkv projection
+ * output and rotated in the attention kernel, and the step's rotated k and raw v
+ * (+ bias) are used for position pos[0] and appended to the caches there -- the
+ * bits w4a8_rope_kv followed by w4a8_attention give, in one launch fewer.
+ *   qkv      bf16 [B, ldq]  (H q heads, KVH k heads, KVH v heads of D; 16-byte aligned, ldq % 8 == 0)
+ *   bias     bf16 [(H + 2 KVH) * D] or NULL
+ *   cos_tab, sin_tab  fp32 [>= L, ldc]  angle tables (columns 0 .. D/2-1 used)
+ *   k_cache, vt_cache, out, pos, ... as w4a8_attention (T = 1); the caches are written at pos[0]
+ * A position outside [0, L) writes nothing and attends with a zero query, as
+ * w4a8_rope_kv leaves it.  Replaces the reference layer's in-place KV append and
+ * SDPA call (npu_ops/python/bench_decode_layer.py:70-73) for a decode step.
+ */
+int w4a8_attention_rope(const void* qkv, int64_t ldq, const void* bias, const void* cos_tab, const void* sin_tab,
+                        int64_t ldc, void* k_cache, void* vt_cache, void* out, const void* pos, int64_t B, int64_t H,
+                        int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t chunks_per_split, float scale,
+                        void* workspace, int64_t ws_bytes, void* stream);
 
 /* chunks_per_split for a decode step of B sequences (-1 for a bad shape): no split
  * once B * KVH * ceil(G / 16) single-token row tiles give every CU one, otherwise

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported(pkg, lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.w4a8_abi_version() == 7
+    assert lib.w4a8_abi_version() == 8
     # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
     assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
@@ -204,3 +204,20 @@ def test_attention_sizes_and_rejects_bad_arguments(lib):
     assert call(k=24) == 4
     assert call(ws=16, wsb=100) == 6 and b"workspace needs" in lib.w4a8_last_error()
     assert call(B=0, q=None) == 0
+
+
+def test_attention_rope_rejects_bad_arguments(lib):
+    def call(**kw):
+        a = dict(qkv=16, ldq=7168, bias=None, cos=16, sin=16, ldc=64, k=16, vt=16, out=16, pos=16, B=1, H=40, KVH=8,
+                 D=128, L=1280, Lc=1280, cps=3, scale=0.088, ws=16, wsb=1 << 20)
+        a.update(kw)
+        return lib.w4a8_attention_rope(a["qkv"], a["ldq"], a["bias"], a["cos"], a["sin"], a["ldc"], a["k"], a["vt"],
+                                       a["out"], a["pos"], a["B"], a["H"], a["KVH"], a["D"], a["L"], a["Lc"],
+                                       a["cps"], a["scale"], a["ws"], a["wsb"], None)
+    assert call(qkv=None) == 1
+    assert call(ldq=7000) == 2 and b"ldq" in lib.w4a8_last_error()
+    assert call(ldc=63) == 2
+    assert call(qkv=24) == 4                        # qkv rows read 16 bytes at a time
+    assert call(cos=18) == 4
+    assert call(ws=None, wsb=0) == 6                # 7 splits: the combine needs its workspace
+    assert call(D=96, ldq=96 * 56) == 5

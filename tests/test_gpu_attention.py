@@ -183,6 +183,44 @@ def test_decode_launch_in_a_graph(pkg, dev):
         assert torch.equal(out, eager), f"replay at position {p} differs"
 
 
+@pytest.mark.parametrize("B,H,KVH,D,L,bias", [
+    (1, 40, 8, 128, 1280, True),     # QwQ decode, one sequence
+    (8, 40, 8, 128, 1280, True),
+    (64, 40, 8, 128, 1280, True),    # one split
+    (2, 4, 2, 64, 40, False),        # tiny decoder shape
+    (3, 48, 2, 128, 300, True),      # 24 query heads per KV head: two row tiles per pair
+])
+def test_attention_rope_equals_rope_kv_then_attention(pkg, dev, B, H, KVH, D, L, bias):
+    """The fused decode launch (rotary embedding of q and of the step's k, KV append, attention)
+    returns the bits of w4a8_rope_kv followed by w4a8_attention(split=True), and leaves the
+    caches as w4a8_rope_kv leaves them, at positions on and off chunk and split boundaries,
+    the last one, and one past the cache (nothing written, zero query)."""
+    say(f"attention + rope B={B} H={H} KVH={KVH} D={D} L={L} bias={bias}")
+    g = torch.Generator(device=dev).manual_seed(B + H + L)
+    W = (H + 2 * KVH) * D
+    Lc = -(-L // 64) * 64
+    k0 = torch.randn((B, KVH, Lc, D), generator=g, device=dev).to(torch.bfloat16)
+    v0 = torch.randn((B, KVH, D, Lc), generator=g, device=dev).to(torch.bfloat16)
+    inv = 1.0 / (1.0e4 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    ang = torch.arange(L, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    bvec = ((torch.rand((W,), generator=g, device=dev) - 0.5) * 0.2).to(torch.bfloat16) if bias else None
+    cps = pkg.ops.attention_chunks_per_split(B, H, KVH, Lc)
+    for p in sorted({0, 63, 64, L // 2, L - 1, L}):
+        qkv = torch.randn((B, W), generator=g, device=dev).to(torch.bfloat16)
+        pos = torch.full((1,), p, dtype=torch.int64, device=dev)
+        # reference: rope_kv into copies of the caches, then the split attention
+        k1, v1 = k0.clone(), v0.clone()
+        q = torch.ops.npu.w4a8_rope_kv(qkv.view(B, 1, W), cos, sin, pos, k1[:, :, :L].transpose(2, 3),
+                                       v1[..., :L].transpose(2, 3), H, KVH, bvec)
+        ref = torch.ops.npu.w4a8_attention(q, k1, v1, pos, L, cps, True)
+        k2, v2 = k0.clone(), v0.clone()
+        got = torch.ops.npu.w4a8_attention_rope(qkv, cos, sin, pos, k2, v2, H, KVH, L, cps, bvec)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"position {p}: output differs from rope_kv + attention"
+        assert torch.equal(k2, k1) and torch.equal(v2, v1), f"position {p}: caches differ from rope_kv's"
+
+
 def random_attention_shapes(seed: int, n: int):
     """n seeded (B, T, H, KVH, D, L, pos0) draws: 1-6 sequences, 1-40 tokens, 1-20 query
     heads per KV head (tiles of 16 rows straddled or not), head_dim 64 or 128, caches of

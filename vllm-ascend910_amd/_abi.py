@@ -15,7 +15,7 @@ from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "_lib" / "libw4a8_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1
@@ -50,6 +50,8 @@ SIGNATURES = {
                           ctypes.POINTER(_I64), _I64, _I64, _I64, _I64, _I64, _VP]),
     "w4a8_attention": (_I, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                             ctypes.c_float, _VP, _I64, _VP]),
+    "w4a8_attention_rope": (_I, [_VP, _I64, _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64,
+                                 _I64, _I64, ctypes.c_float, _VP, _I64, _VP]),
     "w4a8_attention_chunks_per_split": (_I64, [_I64, _I64, _I64, _I64]),
     "w4a8_attention_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
 }

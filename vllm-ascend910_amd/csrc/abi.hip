@@ -209,7 +209,7 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 7; }
+int w4a8_abi_version(void) { return 8; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
@@ -539,9 +539,9 @@ int64_t w4a8_attention_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t 
     return ns > 1 ? B * T * H * ns * (D + 4) * 4 : 0;
 }
 
-int w4a8_attention(const void* q, const void* k_cache, const void* vt_cache, void* out, const void* pos, int64_t B,
-                   int64_t T, int64_t H, int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t cps, float scale,
-                   void* workspace, int64_t ws_bytes, void* stream) {
+static int attention_impl(const void* q, const void* k_cache, const void* vt_cache, void* out, const void* pos,
+                          int64_t B, int64_t T, int64_t H, int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t cps,
+                          float scale, void* workspace, int64_t ws_bytes, void* stream, const AttnArgs* rope) {
     if (B < 0 || T < 0 || B * T >= (1ll << 31))
         return fail(W4A8_ERR_SHAPE, "bad shape: B=%lld T=%lld", B, T);
     if (H <= 0 || KVH <= 0 || H % KVH != 0 || H / KVH > 65535 || H >= (1ll << 20))
@@ -552,14 +552,14 @@ int w4a8_attention(const void* q, const void* k_cache, const void* vt_cache, voi
     if (cps <= 0 || cps > Lc / 64) return fail(W4A8_ERR_SHAPE, "chunks_per_split=%lld must be in [1, Lc/64]", cps);
     if (!std::isfinite(scale)) return fail(W4A8_ERR_SHAPE, "scale must be finite");
     if (B * T == 0) return W4A8_OK;
-    if (!q || !k_cache || !vt_cache || !out || !pos) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if ((!q && !rope) || !k_cache || !vt_cache || !out || !pos) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
     if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(vt_cache, 16) || !aligned(out, 16) || !aligned(pos, 8) ||
         !aligned(workspace, 16))
         return fail(W4A8_ERR_ALIGN, "q, caches, out and workspace 16-byte aligned, pos 8-byte aligned");
     const int64_t pairs = B * KVH, G = H / KVH;
     const int64_t tiles = (G * T + 15) / 16;
     const int64_t ns = (Lc / 64 + cps - 1) / cps;
-    const bool split = workspace != nullptr;
+    const bool split = workspace != nullptr || rope != nullptr;   // the fused rotary path is a decode launch
     if (split) {
         const int64_t need = w4a8_attention_workspace_bytes(B, T, H, D, Lc, cps);
         if (ws_bytes < need) return fail(W4A8_ERR_WORKSPACE, "workspace needs %lld bytes (got %lld)", need, ws_bytes);
@@ -587,7 +587,45 @@ int w4a8_attention(const void* q, const void* k_cache, const void* vt_cache, voi
     a.cps = static_cast<int>(cps);
     a.ns = static_cast<int>(ns);
     a.cs = static_cast<float>(1.4426950408889634 * static_cast<double>(scale));
+    if (rope) {
+        a.qkv = rope->qkv;
+        a.ldq = rope->ldq;
+        a.bias = rope->bias;
+        a.cos = rope->cos;
+        a.sin = rope->sin;
+        a.ldc = rope->ldc;
+        a.kw = static_cast<uint16_t*>(const_cast<void*>(k_cache));
+        a.vtw = static_cast<uint16_t*>(const_cast<void*>(vt_cache));
+    }
     return hip_status(launch_attention(a, split, static_cast<hipStream_t>(stream)), "w4a8_attention launch");
+}
+
+int w4a8_attention(const void* q, const void* k_cache, const void* vt_cache, void* out, const void* pos, int64_t B,
+                   int64_t T, int64_t H, int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t cps, float scale,
+                   void* workspace, int64_t ws_bytes, void* stream) {
+    return attention_impl(q, k_cache, vt_cache, out, pos, B, T, H, KVH, D, L, Lc, cps, scale, workspace, ws_bytes,
+                          stream, nullptr);
+}
+
+int w4a8_attention_rope(const void* qkv, int64_t ldq, const void* bias, const void* cos_tab, const void* sin_tab,
+                        int64_t ldc, void* k_cache, void* vt_cache, void* out, const void* pos, int64_t B, int64_t H,
+                        int64_t KVH, int64_t D, int64_t L, int64_t Lc, int64_t cps, float scale, void* workspace,
+                        int64_t ws_bytes, void* stream) {
+    if (B > 0 && (!qkv || !cos_tab || !sin_tab)) return fail(W4A8_ERR_NULL, "a required pointer is NULL");
+    if (KVH > 0 && H > 0 && D > 0 && (ldq < (H + 2 * KVH) * D || ldq % 8 != 0 || ldc < D / 2))
+        return fail(W4A8_ERR_SHAPE, "qkv rows need ldq >= (H + 2 KVH) * D = %lld (a multiple of 8), cos/sin ldc >= D/2",
+                    (H + 2 * KVH) * D);
+    if (!aligned(qkv, 16) || !aligned(bias, 2) || !aligned(cos_tab, 4) || !aligned(sin_tab, 4))
+        return fail(W4A8_ERR_ALIGN, "qkv 16-byte, bias 2-byte, cos/sin 4-byte aligned");
+    AttnArgs r{};
+    r.qkv = static_cast<const uint16_t*>(qkv);
+    r.ldq = ldq;
+    r.bias = static_cast<const uint16_t*>(bias);
+    r.cos = static_cast<const float*>(cos_tab);
+    r.sin = static_cast<const float*>(sin_tab);
+    r.ldc = ldc;
+    return attention_impl(nullptr, k_cache, vt_cache, out, pos, B, 1, H, KVH, D, L, Lc, cps, scale, workspace,
+                          ws_bytes, stream, &r);
 }
 
 }  // extern "C"

@@ -276,11 +276,96 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t pair_rsrc(const uint16_t* base
     return make_rsrc(base + pair * n, static_cast<uint32_t>(n * 2));
 }
 
+// ---- decode with the rotary embedding and the KV-cache append fused in ----
+// x (+ bias, rounded as a bf16 add), as w4a8_rope_kv reads an input element.
+__device__ __forceinline__ float rope_in(uint32_t xbits, uint32_t bbits, bool has_bias) {
+#pragma clang fp contract(off)
+    const float v = bf16_bits_to_f32(xbits);
+    return has_bias ? bf16_bits_to_f32(f32_to_bf16_bits(v + bf16_bits_to_f32(bbits))) : v;
+}
+
+// The elements 32 i + 8 j .. +8 (i < D/32) of head `hd` of one row (16-byte loads).
+template <int D>
+__device__ __forceinline__ void rope_load(const uint16_t* row, int hd, int j, uint4 (&x)[D / 32]) {
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) x[i] = *reinterpret_cast<const uint4*>(row + hd * D + 32 * i + 8 * j);
+}
+
+// The angle-table entries of the lane's pair indices 32 i + 8 j .. +8, i < D/64.
+template <int D>
+__device__ __forceinline__ void rope_angles(const float* row, int j, float4 (&t)[D / 64][2]) {
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) {
+        t[i][0] = *reinterpret_cast<const float4*>(row + 32 * i + 8 * j);
+        t[i][1] = *reinterpret_cast<const float4*>(row + 32 * i + 8 * j + 4);
+    }
+}
+
+// Rotate-half of the lane's elements as w4a8_rope_kv computes them: for pair index
+// d < D/2 (x1 = x[d], x2 = x[d + D/2], c = cos[p, d], s = sin[p, d]) y[d] = bf16(fl(x1 c)
+// - fl(x2 s)), y[d + D/2] = bf16(fl(x2 c) + fl(x1 s)), no fused multiply-add.  Lane group
+// j holds elements 32 i + 8 j + e; the partner of i < D/64 is i + D/64, in the same lane.
+// Everything is in registers (x, the bias elements bx, the angle entries).
+template <int D>
+__device__ __forceinline__ void rope_rotate(const uint4 (&x)[D / 32], const uint4 (&bx)[D / 32], bool has_bias,
+                                            const float4 (&cs)[D / 64][2], const float4 (&sn)[D / 64][2],
+                                            uint4 (&y)[D / 32]) {
+#pragma clang fp contract(off)
+    constexpr int HI = D / 64;
+#pragma unroll
+    for (int i = 0; i < HI; ++i) {
+        const uint32_t x1w[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+        const uint32_t x2w[4] = {x[i + HI].x, x[i + HI].y, x[i + HI].z, x[i + HI].w};
+        const uint32_t b1w[4] = {bx[i].x, bx[i].y, bx[i].z, bx[i].w};
+        const uint32_t b2w[4] = {bx[i + HI].x, bx[i + HI].y, bx[i + HI].z, bx[i + HI].w};
+        const float cv[8] = {cs[i][0].x, cs[i][0].y, cs[i][0].z, cs[i][0].w, cs[i][1].x, cs[i][1].y, cs[i][1].z,
+                             cs[i][1].w};
+        const float sv[8] = {sn[i][0].x, sn[i][0].y, sn[i][0].z, sn[i][0].w, sn[i][1].x, sn[i][1].y, sn[i][1].z,
+                             sn[i][1].w};
+        uint32_t o1[4], o2[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            float r1[2], r2[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float x1 = rope_in(h ? (x1w[w] >> 16) : (x1w[w] & 0xffffu), h ? (b1w[w] >> 16) : (b1w[w] & 0xffffu),
+                                         has_bias);
+                const float x2 = rope_in(h ? (x2w[w] >> 16) : (x2w[w] & 0xffffu), h ? (b2w[w] >> 16) : (b2w[w] & 0xffffu),
+                                         has_bias);
+                const float c = cv[2 * w + h], sn1 = sv[2 * w + h];
+                r1[h] = x1 * c - x2 * sn1;
+                r2[h] = x2 * c + x1 * sn1;
+            }
+            o1[w] = f32x2_to_bf16x2_bits(r1[0], r1[1]);
+            o2[w] = f32x2_to_bf16x2_bits(r2[0], r2[1]);
+        }
+        y[i] = make_uint4(o1[0], o1[1], o1[2], o1[3]);
+        y[i + HI] = make_uint4(o2[0], o2[1], o2[2], o2[3]);
+    }
+}
+
+// One bf16 of a 16-byte operand replaced (slot e of 8).
+__device__ __forceinline__ uint4 put_bf16(uint4 v, int e, uint32_t bits) {
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = (e == 2 * k) ? bits : (w[k] & 0xffffu);
+        const uint32_t hi = (e == 2 * k + 1) ? bits : (w[k] >> 16);
+        w[k] = lo | (hi << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // Decode launch: workgroup (split, row tile, pair) folds the chunks of its split,
 // each chunk's operands requested while the previous one is computed.  With one
 // split it writes the output; otherwise its state goes to the workspace (m, l,
-// then O) for attn_combine_kernel.
-template <int D>
+// then O) for attn_combine_kernel.  ROPE (one query token per sequence): the
+// query rows are rotated here from the qkv projection output, and the workgroup
+// whose chunk holds the step's position puts the step's rotated k and raw v into
+// its operands in place of the cache's (row tile 0 also writes them to the
+// caches), so that the separate w4a8_rope_kv launch is not needed; the values
+// are the bits w4a8_rope_kv would have written.
+template <int D, bool ROPE>
 __global__ __launch_bounds__(64) void attn_split_kernel(const AttnArgs a) {
     const int lane = static_cast<int>(threadIdx.x);
     const int c = lane & 15, j = lane >> 4;
@@ -295,15 +380,88 @@ __global__ __launch_bounds__(64) void attn_split_kernel(const AttnArgs a) {
     VOps<D> va, vb;
     load_chunk_global<D>(ka, va, kr, vr, a.Lc, first * kChunk, c, j, 0u);
     bf16x8 qop[D / 32];
-    load_q<D>(a, t, j, qop);
+    const int b = t.pair / a.KVH, h = t.pair - b * a.KVH;
+    const int qhead = h * a.G + rt * 16 + c;                 // T = 1: row r = g
+    const int khead = a.H + h, vhead = a.H + a.KVH + h;
+    // ROPE: the query row, the step's k head and v elements (16 dt + c) and their bias
+    // elements, all requested with the first chunk
+    uint4 xq[D / 32], xk[D / 32], bq[D / 32], bk[D / 32];
+    uint32_t xv[D / 16], bv[D / 16];
+    const bool has_bias = ROPE && a.bias != nullptr;
+    if constexpr (ROPE) {
+        const uint16_t* row = a.qkv + static_cast<int64_t>(b) * a.ldq;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) xq[i] = bq[i] = bk[i] = make_uint4(0, 0, 0, 0);
+        if (t.real) rope_load<D>(row, qhead, j, xq);
+        rope_load<D>(row, khead, j, xk);
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) xv[dt] = row[vhead * D + 16 * dt + c];
+        if (has_bias) {
+            if (t.real) rope_load<D>(a.bias, qhead, j, bq);
+            rope_load<D>(a.bias, khead, j, bk);
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) bv[dt] = a.bias[vhead * D + 16 * dt + c];
+        }
+    } else {
+        load_q<D>(a, t, j, qop);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const int64_t pos0 = a.pos[0];
     const int p_row = clamp_pos(pos0 + t.tok, a.L);
     const int p_max = last_pos(a, pos0, rt * 16 + 15);
+    // ROPE: the step's position (inside the cache, else nothing is written and q is zero,
+    // as w4a8_rope_kv does), the rotated q rows, and the step's rotated k / v (+ bias)
+    const bool inside = ROPE && pos0 >= 0 && pos0 < a.L;
+    uint4 knew[D / 32];
+    uint32_t vnew[D / 16];
+    if constexpr (ROPE) {
+        float4 cs[D / 64][2], sn[D / 64][2];
+        rope_angles<D>(a.cos + (inside ? pos0 : 0) * a.ldc, j, cs);
+        rope_angles<D>(a.sin + (inside ? pos0 : 0) * a.ldc, j, sn);
+        uint4 yq[D / 32];
+        rope_rotate<D>(xq, bq, has_bias, cs, sn, yq);
+        rope_rotate<D>(xk, bk, has_bias, cs, sn, knew);
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+            qop[i] = __builtin_bit_cast(bf16x8, (inside && t.real) ? yq[i] : make_uint4(0, 0, 0, 0));
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+            vnew[dt] = has_bias ? f32_to_bf16_bits(rope_in(xv[dt], bv[dt], true)) : xv[dt];
+    }
     if (first * kChunk > p_max) {                    // no position of the split is attended by the tile
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return;
     }
+    // the chunk holding the step's position: its operand slots for that position
+    const int pch = inside ? static_cast<int>(pos0) / kChunk : -1;
+    const int pp = static_cast<int>(pos0) & (kChunk - 1);
+    auto inject = [&](KOps<D>& ko, VOps<D>& vo) __attribute__((always_inline)) {
+        const int kt_p = 2 * (pp >> 5) + ((pp & 7) >> 2), c_p = 4 * ((pp & 31) >> 3) + (pp & 3);
+        const int s_p = pp >> 5, j_p = (pp & 31) >> 3, e_p = pp & 7;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+                if (kt == kt_p && c == c_p) ko.k[kt][i] = knew[i];
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+                if (s == s_p && j == j_p) vo.v[dt][s] = put_bf16(vo.v[dt][s], e_p, vnew[dt]);
+        if (rt == 0) {                               // one workgroup per pair appends the step's k and v
+            const int64_t n = static_cast<int64_t>(a.Lc) * D;
+            if (c == c_p) {
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i)
+                    *reinterpret_cast<uint4*>(a.kw + t.pair * n + pos0 * D + 32 * i + 8 * j) = knew[i];
+            }
+            if (j == j_p) {
+#pragma unroll
+                for (int dt = 0; dt < D / 16; ++dt)
+                    a.vtw[t.pair * n + static_cast<int64_t>(16 * dt + c) * a.Lc + pos0] = static_cast<uint16_t>(vnew[dt]);
+            }
+        }
+    };
     RowState<D> st;
     state_clear(st);
     f32x4 sc[4];
@@ -311,6 +469,7 @@ __global__ __launch_bounds__(64) void attn_split_kernel(const AttnArgs a) {
         const bool more = ch + 1 < last && (ch + 1) * kChunk <= p_max;
         load_chunk_global<D>(kb, vb, kr, vr, a.Lc, (ch + 1) * kChunk, c, j, more ? 0u : kSkip);
         __builtin_amdgcn_sched_barrier(0);
+        if (ROPE && ch == pch) inject(ka, va);
         chunk_scores<D>(sc, qop, ka);
         chunk_update<D>(st, sc, va, ch * kChunk, p_row, a.cs, j);
         if (!more) break;
@@ -318,6 +477,7 @@ __global__ __launch_bounds__(64) void attn_split_kernel(const AttnArgs a) {
         const bool more2 = ch + 1 < last && (ch + 1) * kChunk <= p_max;
         load_chunk_global<D>(ka, va, kr, vr, a.Lc, (ch + 1) * kChunk, c, j, more2 ? 0u : kSkip);
         __builtin_amdgcn_sched_barrier(0);
+        if (ROPE && ch == pch) inject(kb, vb);
         chunk_scores<D>(sc, qop, kb);
         chunk_update<D>(st, sc, vb, ch * kChunk, p_row, a.cs, j);
         if (!more2) break;
@@ -530,9 +690,9 @@ hipError_t launch_attention_d(const AttnArgs& a, bool split, hipStream_t stream)
     const int pairs = a.B * a.KVH;
     if (split) {
         const int tiles = static_cast<int>((R + 15) / 16);
-        attn_split_kernel<D><<<dim3(static_cast<unsigned>(a.ns), static_cast<unsigned>(tiles),
-                                    static_cast<unsigned>(pairs)),
-                               dim3(64), 0, stream>>>(a);
+        const dim3 grid(static_cast<unsigned>(a.ns), static_cast<unsigned>(tiles), static_cast<unsigned>(pairs));
+        if (a.qkv) attn_split_kernel<D, true><<<grid, dim3(64), 0, stream>>>(a);
+        else attn_split_kernel<D, false><<<grid, dim3(64), 0, stream>>>(a);
         if (a.ns > 1)
             attn_combine_kernel<D><<<dim3(static_cast<unsigned>(pairs * R)), dim3(64), 0, stream>>>(a);
     } else {

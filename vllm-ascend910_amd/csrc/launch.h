@@ -180,6 +180,17 @@ struct AttnArgs {
     int L, Lc;              // attended positions are clamped to [0, L); Lc = cache axis, multiple of 64
     int cps, ns;            // chunks of 64 positions per split; splits = ceil(Lc / 64 / cps)
     float cs;               // log2(e) * softmax scale
+    // Decode (T = 1) with the rotary embedding and the KV-cache append fused in
+    // (qkv set; q unused): the q heads and the step's k and v come from the qkv
+    // projection output, rotated as w4a8_rope_kv rotates them.
+    const uint16_t* qkv;    // bf16 [B, ldq]: H q heads, KVH k heads, KVH v heads of D
+    int64_t ldq;
+    const uint16_t* bias;   // optional bf16 [(H + 2 KVH) * D], added before the rotation
+    const float* cos;       // fp32 [>= L, ldc], columns 0 .. D/2-1 used
+    const float* sin;
+    int64_t ldc;
+    uint16_t* kw;           // the caches (k, vt above), written at the step's position
+    uint16_t* vtw;
 };
 hipError_t launch_attention(const AttnArgs& a, bool split, hipStream_t stream);
 

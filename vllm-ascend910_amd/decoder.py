@@ -15,7 +15,9 @@ embeddings, RMSNorm) on this build's ops:
   (``torch.ops.npu.w4a8_rope_kv``, fp32 products and sums rounded to bf16 as
   torch rounds them on float tensors);
 * attention runs on this build's grouped-query attention kernel
-  (``torch.ops.npu.w4a8_attention``, bf16 MFMA, csrc/attention.hip): the
+  (``torch.ops.npu.w4a8_attention``, bf16 MFMA, csrc/attention.hip; a decode
+  step calls ``w4a8_attention_rope``, which also rotates q and appends the
+  step's k and v, in place of ``w4a8_rope_kv`` + ``w4a8_attention``): the
   query heads of one KV head form the rows of one problem (no head repeat),
   the causal limit of every row and the cache length of a captured decode
   step are read on the device, so a decode step reads only the positions
@@ -308,12 +310,17 @@ class W4A8Decoder:
         for li, L in enumerate(self.layers):
             aq, as_, s, _ = torch.ops.npu.w4a8_rmsnorm_quant(x, L["ln1"], c.rms_eps, delta, c.group)
             x = s if delta is not None else x
+            if self.attention == "hip":
+                # qkv projection, then one launch for the rotary embedding, the KV append and attention
+                qkv = L["qkv"].gemm(aq, as_)
+                o = torch.ops.npu.w4a8_attention_rope(qkv, self.cos, self.sin, self.pos, self._k_store[li],
+                                                      self._vt_store[li], c.heads, c.kv_heads, self.max_len,
+                                                      self.cps, L["qkv"].bias)
+                x, delta = self._mlp_and_next(L, x, o.view(B, c.heads * c.head_dim))
+                continue
             q = self._rope_kv(li, L, aq, as_, 1, self.pos)               # [B, 1, H, D]
             qg = q.view(B, c.kv_heads, G, c.head_dim)
-            if self.attention == "hip":
-                o = torch.ops.npu.w4a8_attention(q, self._k_store[li], self._vt_store[li], self.pos, self.max_len,
-                                                 self.cps, True)
-            elif self.sdpa:
+            if self.sdpa:
                 o = _sdpa(qg, self._k_ld[li], self.v_cache[li], bias)              # [B, KVH, G, D]
             else:
                 o = self._attend(qg, self.k_cache[li], self.v_cache[li], bias)      # [B, KVH, G, D]

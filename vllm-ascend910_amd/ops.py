@@ -18,6 +18,8 @@ and two producer-side helpers of the decoder forward that drives them:
         -> (a_q, a_scale, s, h)
     torch.ops.npu.w4a8_rope_kv(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads, bias=None) -> q
     torch.ops.npu.w4a8_attention(q, k_cache, vt_cache, pos, L, chunks_per_split, split=False, scale=None) -> out
+    torch.ops.npu.w4a8_attention_rope(qkv, cos, sin, pos, k_cache, vt_cache, heads, kv_heads, L,
+                                      chunks_per_split, bias=None, scale=None) -> out   (decode step: rope_kv fused in)
 
 and, with the reference's own names and schemas (group appended with the
 reference's fixed value as default), its mid-group compat pair:
@@ -59,6 +61,9 @@ _LIB.define("w4a8_rope_kv(Tensor qkv, Tensor cos, Tensor sin, Tensor pos, Tensor
             "int heads, int kv_heads, Tensor? bias=None) -> Tensor")
 _LIB.define("w4a8_attention(Tensor q, Tensor k_cache, Tensor vt_cache, Tensor pos, int L, int chunks_per_split, "
             "bool split=False, float? scale=None) -> Tensor")
+_LIB.define("w4a8_attention_rope(Tensor qkv, Tensor cos, Tensor sin, Tensor pos, Tensor(a!) k_cache, "
+            "Tensor(b!) vt_cache, int heads, int kv_heads, int L, int chunks_per_split, Tensor? bias=None, "
+            "float? scale=None) -> Tensor")
 _LIB.define("midgroup_quant_a(Tensor x, int group=1024) -> Tensor[]")
 _LIB.define("midgroup_w4a8_gemm(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
             "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> Tensor")
@@ -441,6 +446,61 @@ def _attention_cuda(q: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tens
 @torch.library.register_fake("npu::w4a8_attention")
 def _attention_fake(q, k_cache, vt_cache, pos, L, chunks_per_split, split=False, scale=None):
     return torch.empty_like(q)
+
+
+@torch.library.impl(_LIB, "w4a8_attention_rope", "CUDA")
+def _attention_rope_cuda(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
+                         k_cache: torch.Tensor, vt_cache: torch.Tensor, heads: int, kv_heads: int, L: int,
+                         chunks_per_split: int, bias=None, scale=None) -> torch.Tensor:
+    """A decode step's attention with w4a8_rope_kv fused in: qkv [B, (heads + 2 kv_heads) * D]
+    (one token per sequence), the q heads rotated in the kernel, the step's rotated k and raw
+    v (+ bias) used at position pos[0] and appended to k_cache [B, KVH, Lc, D] / vt_cache
+    [B, KVH, D, Lc] there; returns out [B, 1, heads, D] -- the bits of w4a8_rope_kv followed
+    by w4a8_attention(split=True)."""
+    _require(qkv.dim() == 2 and qkv.dtype == torch.bfloat16, "w4a8_attention_rope: qkv must be bfloat16 [B, W]")
+    B, W = qkv.shape
+    _require(heads > 0 and kv_heads > 0 and W % (heads + 2 * kv_heads) == 0,
+             "w4a8_attention_rope: qkv width must be (heads + 2 kv_heads) * head_dim")
+    D = W // (heads + 2 * kv_heads)
+    _require(k_cache.dim() == 4 and vt_cache.dim() == 4 and k_cache.dtype == torch.bfloat16
+             and vt_cache.dtype == torch.bfloat16, "w4a8_attention_rope: caches must be 4-D bfloat16")
+    Lc = k_cache.shape[2]
+    _require(tuple(k_cache.shape) == (B, kv_heads, Lc, D) and tuple(vt_cache.shape) == (B, kv_heads, D, Lc)
+             and k_cache.is_contiguous() and vt_cache.is_contiguous(),
+             "w4a8_attention_rope: caches must be contiguous k [B, kv_heads, Lc, D] and vt [B, kv_heads, D, Lc]")
+    for t, name in ((cos, "cos"), (sin, "sin")):
+        _require(t.dim() == 2 and t.dtype == torch.float32 and t.shape[0] >= L and t.shape[1] >= D // 2
+                 and t.stride(1) == 1, f"w4a8_attention_rope: {name} must be float32 [>= L, >= head_dim / 2]")
+    _require(cos.stride(0) == sin.stride(0), "w4a8_attention_rope: cos and sin must share a row stride")
+    _require(pos.dtype == torch.int64 and pos.numel() == 1 and pos.device == qkv.device,
+             "w4a8_attention_rope: pos must be one int64 on the device")
+    if qkv.stride(1) != 1 or qkv.stride(0) % 8:
+        qkv = qkv.contiguous()
+    if bias is not None:
+        _require(bias.dtype == torch.bfloat16 and bias.numel() == W and bias.device == qkv.device,
+                 "w4a8_attention_rope: bias must be bfloat16 [(heads + 2 kv_heads) * head_dim] on the device")
+        bias = bias.contiguous()
+    out = torch.empty((B, 1, heads, D), dtype=torch.bfloat16, device=qkv.device)
+    if B == 0:
+        return out
+    sc = float(scale) if scale is not None else 1.0 / float(D) ** 0.5
+    lib = _abi.lib()
+    need = lib.w4a8_attention_workspace_bytes(B, 1, heads, D, Lc, chunks_per_split)
+    _require(need >= 0, "w4a8_attention_rope: bad shape for the workspace size")
+    ws = _workspace(qkv.device, max(need, 16))
+    _abi.check(lib.w4a8_attention_rope(qkv.data_ptr(), qkv.stride(0), bias.data_ptr() if bias is not None else None,
+                                       cos.data_ptr(), sin.data_ptr(), cos.stride(0), k_cache.data_ptr(),
+                                       vt_cache.data_ptr(), out.data_ptr(), pos.data_ptr(), B, heads, kv_heads, D, L,
+                                       Lc, chunks_per_split, sc, ws.data_ptr(), ws.numel(), _stream(qkv.device)),
+               "w4a8_attention_rope")
+    return out
+
+
+@torch.library.register_fake("npu::w4a8_attention_rope")
+def _attention_rope_fake(qkv, cos, sin, pos, k_cache, vt_cache, heads, kv_heads, L, chunks_per_split, bias=None,
+                         scale=None):
+    B, W = qkv.shape
+    return qkv.new_empty((B, 1, heads, W // (heads + 2 * kv_heads)))
 
 
 # ---------------------------------------------------------------- mid-group compat pair
