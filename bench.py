@@ -495,7 +495,9 @@ def main():
         result["attention_shapes"] = attention_bench(pkg, dev, time_graph, args.cold_bytes, args.attention_sweep)
     # ---------------------------------------------------------------- decoder forward
     if not args.no_decoder:
-        result["decoder"] = decoder_bench(pkg, dev, args.decoder_layers, steps=args.decoder_steps)
+        result["decoder"] = decoder_bench(pkg, dev, args.decoder_layers, steps=args.decoder_steps, attention="torch")
+        result["decoder_attention_kernel"] = decoder_bench(pkg, dev, args.decoder_layers, steps=args.decoder_steps,
+                                                           attention="hip")
 
     # ---------------------------------------------------------------- CPU baseline
     if not args.no_cpu_baseline:
@@ -680,14 +682,18 @@ def attention_bench(pkg, dev, time_graph, cold_gib, sweep=False, batches=(1, 8, 
     return rows
 
 
-def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
+def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64), attention="torch"):
     """prefill tokens/s and greedy decode tokens/s of the QwQ-32B-shaped decoder
-    (random W4A8 weights at group 128, attention on this build's bf16 MFMA kernel
-    w4a8_attention, decode steps replayed from a HIP graph)."""
+    (random W4A8 weights at group 128, decode steps replayed from a HIP graph).  attention
+    "torch" is the config as stated -- bf16 attention left on PyTorch-ROCm (batched products
+    below decoder.SDPA_MIN_BATCH sequences, scaled_dot_product_attention from it on); "hip"
+    runs the same model on this build's attention kernel (w4a8_attention, the decode step
+    with the rotary embedding and the KV append fused in)."""
     import torch
     cfg = pkg.decoder.DecoderConfig(layers=layers)
     t0 = time.perf_counter()
-    m = pkg.decoder.W4A8Decoder(cfg, batch=batches[0], max_len=prompt + steps, device=dev, seed=7)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=batches[0], max_len=prompt + steps, device=dev, seed=7,
+                                attention=attention)
     torch.cuda.synchronize()
     log(f"  decoder: {layers} layers built in {time.perf_counter() - t0:.1f} s")
     # one untimed short prefill first: the first call loads the torch/BLAS code paths
@@ -716,7 +722,7 @@ def decoder_bench(pkg, dev, layers, prompt=1024, steps=256, batches=(1, 8, 64)):
                      "attention": {"hip": "w4a8_attention", "sdpa": "scaled_dot_product_attention",
                                    "matmul": "batched products"}[m.attention],
                      "last_tokens": [int(t) for t in out[-1][:4].tolist()]})
-        log(f"  decoder B={B:3d}: prefill {pre_ms:9.1f} ms ({B * prompt / pre_ms * 1e3:9.0f} tok/s), decode "
+        log(f"  decoder ({m.attention}) B={B:3d}: prefill {pre_ms:9.1f} ms ({B * prompt / pre_ms * 1e3:9.0f} tok/s), decode "
             f"{dec_ms / steps:7.3f} ms/step ({B * steps / dec_ms * 1e3:8.1f} tok/s)")
     del m
     torch.cuda.empty_cache()

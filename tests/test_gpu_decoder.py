@@ -237,6 +237,20 @@ def test_attention_paths_agree(pkg, dev):
             assert rel < 4e-3, f"{name} {tag}: rel-L2 {rel}"
 
 
+def test_torch_attention_picks_the_pytorch_path_by_batch(pkg, dev):
+    """attention="torch" (configs[4] as stated): batched products below SDPA_MIN_BATCH
+    sequences, scaled_dot_product_attention from it on, chosen again by resize()."""
+    cfg = tiny_cfg(pkg)
+    m = pkg.decoder.W4A8Decoder(cfg, batch=2, max_len=16, device=dev, seed=9, attention="torch")
+    assert m.attention == "matmul" and not m.sdpa
+    m.resize(pkg.decoder.SDPA_MIN_BATCH, 16)
+    assert m.attention == "sdpa" and m.sdpa
+    m.resize(3, 16)
+    assert m.attention == "matmul"
+    first = m.prefill(torch.randint(0, cfg.vocab, (3, 6), generator=torch.Generator().manual_seed(3)).to(dev))
+    assert first.shape == (3,)
+
+
 def test_decoder_rejects_unknown_attention(pkg):
     with pytest.raises(ValueError, match="attention"):
         pkg.decoder.W4A8Decoder(tiny_cfg(pkg), batch=1, max_len=8, device="cpu", attention="flash")

@@ -26,8 +26,10 @@ embeddings, RMSNorm) on this build's ops:
   same bits for the same row, so a prefill of t + 1 tokens and a prefill of t
   tokens followed by a decode step agree exactly.  The K cache is stored
   ``[B, KVH, Lc, D]`` and V transposed ``[B, KVH, D, Lc]`` (Lc = max_len
-  rounded up to 64).  The earlier PyTorch paths stay selectable for
-  comparison: ``attention="sdpa"`` calls
+  rounded up to 64).  The PyTorch paths stay selectable --
+  ``attention="torch"`` is configs[4]'s own setting (bf16 attention left on
+  PyTorch-ROCm: batched products below ``SDPA_MIN_BATCH`` sequences, SDPA from
+  it on): ``attention="sdpa"`` calls
   ``torch.nn.functional.scaled_dot_product_attention`` on its efficient
   backend only (the reference's own call,
   npu_ops/python/bench_decode_layer.py:73; the math backend, whose batched
@@ -112,6 +114,11 @@ class _Linear:
         return torch.ops.npu.w4a8_gemm_swiglu(a_q, a_s, self.w_tiles, self.s_tiles, self.N, self.K, self.group)
 
 
+# attention="torch": batches from this size on attend through scaled_dot_product_attention,
+# smaller ones through the two batched products (the faster PyTorch path on either side).
+SDPA_MIN_BATCH = 48
+
+
 def _sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
     """softmax(q k^T / sqrt(D) + mask) v on the efficient backend (an error, not a fallback,
     where it cannot run).  q [B, KVH, R, D], k and v [B, KVH, L, D], mask bf16 broadcastable
@@ -129,13 +136,14 @@ class W4A8Decoder:
                  keep_weights=False, attention: str = "auto"):
         """keep_weights: True keeps every linear's int8 codes and scales (reference
         checks of small models), a collection of layer indices keeps those layers' only.
-        attention: "hip" (this build's attention kernel; "auto" is the same), "sdpa" or
-        "matmul", for prefill and decode alike (the paths round differently, so a prefill and
-        the decode after it share one)."""
-        if attention not in ("auto", "hip", "sdpa", "matmul"):
-            raise ValueError(f"attention must be 'auto', 'hip', 'sdpa' or 'matmul', not {attention!r}")
-        self.attention = "hip" if attention == "auto" else attention
-        self.sdpa = self.attention == "sdpa"
+        attention: "hip" (this build's attention kernel; "auto" is the same), "sdpa",
+        "matmul", or "torch" (PyTorch-ROCm as configs[4] states it: "matmul" below
+        SDPA_MIN_BATCH sequences, "sdpa" from it on, chosen again by resize()), for prefill
+        and decode alike (the paths round differently, so a prefill and the decode after it
+        share one).  self.attention is the path in use."""
+        if attention not in ("auto", "hip", "torch", "sdpa", "matmul"):
+            raise ValueError(f"attention must be 'auto', 'hip', 'torch', 'sdpa' or 'matmul', not {attention!r}")
+        self.attention_mode = "hip" if attention == "auto" else attention
         self.cfg, self.batch, self.max_len = cfg, batch, max_len
         dev = torch.device(device)
         self.device = dev
@@ -193,6 +201,10 @@ class W4A8Decoder:
           matmul  both caches themselves."""
         c, dev = self.cfg, self.device
         kvh, d = c.kv_heads, c.head_dim
+        mode = self.attention_mode
+        self.attention = mode if mode in ("hip", "sdpa", "matmul") else (
+            "sdpa" if batch >= SDPA_MIN_BATCH else "matmul")
+        self.sdpa = self.attention == "sdpa"
         self._k_ld = self._k_store = self._vt_store = None
         if self.attention == "hip":
             lc = -(-max_len // 64) * 64
