@@ -13,6 +13,7 @@ Bars:
 from __future__ import annotations
 
 import math
+import os
 import sys
 
 import pytest
@@ -239,7 +240,8 @@ def random_attention_shapes(seed: int, n: int):
     return out
 
 
-@pytest.mark.parametrize("B,T,H,KVH,D,L,pos0", random_attention_shapes(5, 16))
+@pytest.mark.parametrize("B,T,H,KVH,D,L,pos0",
+                         random_attention_shapes(5, 16 * max(1, int(os.environ.get("W4A8_RANDOM_SCALE", "1")))))
 def test_attention_random_shapes(pkg, dev, B, T, H, KVH, D, L, pos0):
     """Seeded random shapes: both launches within the bound of the float64 attention and
     equal to each other bit for bit, at the library's split size and at one chunk per split."""

@@ -10,6 +10,7 @@ Bars (stated per test):
 """
 from __future__ import annotations
 
+import os
 import sys
 
 import numpy as np
@@ -745,7 +746,12 @@ def random_shapes(seed: int, n: int, max_mnk: float = 3e8, max_gmn: float = 1.2e
     return out
 
 
-@pytest.mark.parametrize("M,N,K,G,sd", random_shapes(20261202, 64))
+# W4A8_RANDOM_SCALE multiplies the number of random draws (a longer campaign than the
+# default suite runs; the draws of the default count are its first ones)
+RANDOM_SCALE = max(1, int(os.environ.get("W4A8_RANDOM_SCALE", "1")))
+
+
+@pytest.mark.parametrize("M,N,K,G,sd", random_shapes(20261202, 64 * RANDOM_SCALE))
 def test_gemm_random_shapes(pkg, dev, M, N, K, G, sd):
     """Seeded random shapes through the GEMM: partials bit-exact, padded a_q and a_scale
     byte-exact, output within the bars, the production launch equal to the dump."""
@@ -763,7 +769,7 @@ def test_gemm_random_shapes(pkg, dev, M, N, K, G, sd):
 
 
 @pytest.mark.parametrize("M,N,K,G,sd", [(int(m) % 4 + 1, n, k, g, sd)
-                                        for m, n, k, g, sd in random_shapes(77, 24)])
+                                        for m, n, k, g, sd in random_shapes(77, 24 * RANDOM_SCALE)])
 def test_linear_random_shapes(pkg, dev, M, N, K, G, sd):
     """Seeded random shapes through w4a8_linear at one to four rows (the fused launch
     where it applies): equal to quant + GEMM bit for bit, and within the bars."""
@@ -994,7 +1000,7 @@ def test_gemm_swiglu(pkg, dev, M, I, K, G, sd):
 
 
 @pytest.mark.parametrize("M,I,K,G,sd", [(m, max(16, n // 32 * 16), k, g, sd)
-                                        for m, n, k, g, sd in random_shapes(4242, 16)])
+                                        for m, n, k, g, sd in random_shapes(4242, 16 * RANDOM_SCALE)])
 def test_gemm_swiglu_random_shapes(pkg, dev, M, I, K, G, sd):
     """Seeded random shapes (I a multiple of 16) through the fused SwiGLU epilogue:
     within the bar of the unfused GPU output and of the oracle."""
