@@ -222,6 +222,34 @@ def test_attention_rope_equals_rope_kv_then_attention(pkg, dev, B, H, KVH, D, L,
         assert torch.equal(k2, k1) and torch.equal(v2, v1), f"position {p}: caches differ from rope_kv's"
 
 
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_attention_relaunch_deterministic(pkg, dev, B):
+    """The decode launches (split + combine, split alone, the fused rotary form) and the
+    prefill launch relaunched 20 times with other work between: identical bits."""
+    H, KVH, D, L = 40, 8, 128, 1280
+    say(f"attention relaunch B={B}")
+    q, k, vt, Lc = make_inputs(dev, B, 1, H, KVH, D, L, seed=B + 3)
+    pos = torch.full((1,), 1000, dtype=torch.int64, device=dev)
+    cps = pkg.ops.attention_chunks_per_split(B, H, KVH, Lc)
+    qp, kp, vp, _ = make_inputs(dev, 1 if B == 64 else B, 200, H, KVH, D, 256, seed=B + 4)
+    pos0 = torch.zeros((1,), dtype=torch.int64, device=dev)
+    g = torch.Generator(device=dev).manual_seed(B)
+    qkv = torch.randn((B, (H + 2 * KVH) * D), generator=g, device=dev).to(torch.bfloat16)
+    inv = 1.0 / (1.0e4 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    ang = torch.arange(L, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    runs = [lambda: attn(q, k, vt, pos, L, cps, True), lambda: attn(qp, kp, vp, pos0, 256, 1, False),
+            lambda: torch.ops.npu.w4a8_attention_rope(qkv, cos, sin, pos, k, vt, H, KVH, L, cps)]
+    for fn in runs:
+        first = fn()
+        for i in range(20):
+            y = fn()
+            junk = torch.full((1 << 18,), i, dtype=torch.int32, device=dev)
+            assert torch.equal(y, first), f"B={B}: relaunch {i} differs"
+            del junk
+    torch.cuda.synchronize()
+
+
 def random_attention_shapes(seed: int, n: int):
     """n seeded (B, T, H, KVH, D, L, pos0) draws: 1-6 sequences, 1-40 tokens, 1-20 query
     heads per KV head (tiles of 16 rows straddled or not), head_dim 64 or 128, caches of

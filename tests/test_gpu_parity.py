@@ -562,6 +562,37 @@ def test_gemm_deterministic_and_stress(pkg, dev, M, N, K):
                  exact_sym(q_ref, s_ref, w[cols], ws32[cols], G))
 
 
+@pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
+def test_decode_plans_relaunch_deterministic(pkg, dev, proj):
+    """Every decode plan of a QwQ-32B projection (1 to 64 rows: fused single-row linear,
+    staged activations, per-tile rings, row groups, the wide kernel with and without its K
+    split, the split 64-row prefill tile, the SwiGLU epilogue on gate_up) relaunched 20
+    times with other work between: identical bits every time (the reference's --stress
+    check, int4_cube_lab/host/mg_harness.h:307-334, over all plans)."""
+    K, N = pkg.synth.QWQ_SHAPES[proj]
+    G = 128
+    xb_all, w, ws32, w_scale = make_problem(pkg, 64, N, K, G, seed=11)
+    w_q = torch.from_numpy(ow.pack_grouped(w, G)).to(dev)
+    w_tiles, s_tiles = torch.ops.npu.w4a8_repack(w_q, w_scale.to(dev), K, G)
+    x_all = bf16_bits_tensor(xb_all).to(dev)
+    for M in (1, 2, 4, 8, 12, 16, 24, 32, 48, 64):
+        say(f"relaunch {proj} M={M}")
+        x = x_all[:M].contiguous()
+        a_q, a_s = torch.ops.npu.w4a8_quant_pertoken(x, G)
+        runs = [lambda: torch.ops.npu.w4a8_gemm(a_q, a_s, w_tiles, s_tiles, N, K, G),
+                lambda: torch.ops.npu.w4a8_linear(x, w_tiles, s_tiles, N, K, G)]
+        if proj == "gate_up_proj":
+            runs.append(lambda: torch.ops.npu.w4a8_gemm_swiglu(a_q, a_s, w_tiles, s_tiles, N, K, G))
+        for fn in runs:
+            first = fn()
+            for i in range(20):
+                y = fn()
+                junk = torch.full((1 << 18,), i, dtype=torch.int32, device=dev)
+                assert torch.equal(y, first), f"{proj} M={M}: relaunch {i} differs"
+                del junk
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 27648)])
 def test_linear_fused_deterministic_and_stress(pkg, dev, N, K):
     """The fused single-row linear (quant prologue in every workgroup: every wave reading the
