@@ -48,7 +48,7 @@ enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
  * first build whose GEMM asks a workspace of some decode shapes; 5 adds
  * w4a8_rope_kv; 6 adds w4a8_stream_capture_id and requires 4-byte aligned
  * s_tiles; 7 adds w4a8_attention and its two size queries; 8 adds
- * w4a8_attention_rope). */
+ * w4a8_attention_rope; 9 adds w4a8_midgroup_gemm_ws and its size query). */
 int w4a8_abi_version(void);
 
 /* Message for the calling thread's last failed call ("" if none). */
@@ -373,6 +373,26 @@ int w4a8_midgroup_quant_a(const void* x, int64_t ldx, void* a_hi, void* a_lo, vo
 int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
                        int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y, int64_t ldy,
                        void* partials, int64_t N, int64_t K, int64_t group, void* stream);
+
+/*
+ * The same GEMM with a caller-owned workspace, as the reference host allocates
+ * its GEMM workspace per call (npu_ops/host/midgroup_w4a8_gemm.cpp:116-118).
+ * Where w4a8_midgroup_gemm_workspace_bytes(Ma, N, K, group) is non-zero (more
+ * than 64 rows, group stride ceil_to(group, 64) a multiple of 128 and at
+ * least 256, offsets below 2^31) and no partials are asked for, a call with
+ * workspace_bytes > 0
+ * rebuilds the activation bytes from the two planes into the workspace
+ * (256-byte aligned, at least that many bytes; W4A8_ERR_WORKSPACE otherwise)
+ * and runs the LDS-tiled prefill kernel on w_q as stored.  Every output is the
+ * same fp32 fold in group order as ReferenceMidGroupGemm's.  Any other call
+ * (workspace_bytes == 0, a partial dump, a shape the query gives 0) runs as
+ * w4a8_midgroup_gemm.
+ */
+int64_t w4a8_midgroup_gemm_workspace_bytes(int64_t Ma, int64_t N, int64_t K, int64_t group);
+int w4a8_midgroup_gemm_ws(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
+                          int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y,
+                          int64_t ldy, void* partials, int64_t N, int64_t K, int64_t group, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,7 +7,8 @@ runs one seeded case per kernel path of this build (activation quant, the
 staged, per-tile and row-group decode plans, the wide and K-split decode
 kernels, the fused single-row linear, the SwiGLU epilogue, per-channel scales,
 both prefill tile shapes at group 128 and the prefill at group 256, the
-reference-compat pair at decode sizes, on wide N and at prefill sizes) and
+reference-compat pair at decode sizes, on wide N and at prefill sizes, with
+and without the partial dump) and
 records the SHA-256 of each output's bytes.
 tests/test_gpu_regress.py recomputes them and fails on any changed bit.
 
@@ -82,7 +83,7 @@ def _quant_case(M, K, seed):
     return run
 
 
-def _midgroup_case(M, N, K, G, seed):
+def _midgroup_case(M, N, K, G, seed, partials=False):
     def run(pkg, dev):
         import torch
         from oracle import w4a8 as ow
@@ -92,6 +93,8 @@ def _midgroup_case(M, N, K, G, seed):
         a = torch.ops.npu.midgroup_quant_a(_bf16(xb).to(dev), G)
         args = (torch.from_numpy(ow.pack_grouped(codes, G)).to(dev), _bf16(sc).to(dev),
                 torch.from_numpy(ks).to(dev), _bf16(zr).to(dev))
+        if partials:
+            return _digest(*a, *torch.ops.npu.midgroup_w4a8_gemm_partials(*a, *args, K, G))
         y = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G)
         return _digest(*a, y)
     return run
@@ -115,7 +118,10 @@ CASES = {
     "gemm_m512_prefill_g128": ("gemm_prefill_kernel, 64-row tiles", _gemm_case(512, 1024, 1024, 128, 12)),
     "gemm_m2048_prefill_g256": ("gemm_prefill_kernel, group 256", _gemm_case(2048, 2048, 1024, 256, 13)),
     "midgroup_m16_g1024": ("compat quant_a + mid-group GEMM", _midgroup_case(16, 2048, 4096, 1024, 14)),
-    "midgroup_m512_g1024": ("compat mid-group GEMM, 64x64 prefill tiles", _midgroup_case(512, 2048, 4096, 1024, 15)),
+    "midgroup_m512_g1024": ("compat GEMM prefill path: compat_act_kernel + gemm_prefill_kernel (CM = 2)",
+                            _midgroup_case(512, 2048, 4096, 1024, 15)),
+    "midgroup_m512_g1024_partials": ("compat mid-group GEMM, 64x64 tiles with the partial dump",
+                                     _midgroup_case(512, 2048, 4096, 1024, 15, partials=True)),
     "midgroup_m16_wide_n": ("compat mid-group GEMM, shared-activation decode", _midgroup_case(16, 16384, 2048, 1024, 16)),
 }
 

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported(pkg, lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.w4a8_abi_version() == 8
+    assert lib.w4a8_abi_version() == 9
     # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
     assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024
@@ -221,3 +221,38 @@ def test_attention_rope_rejects_bad_arguments(lib):
     assert call(cos=18) == 4
     assert call(ws=None, wsb=0) == 6                # 7 splits: the combine needs its workspace
     assert call(D=96, ldq=96 * 56) == 5
+
+
+def test_midgroup_workspace_sizes_and_rejects(lib):
+    """The compat GEMM's prefill path: its workspace query (rebuilt activation rows
+    [Ma, k_tiles * 128] and fp32 activation scales [G, Ma], then from 2048 rows the
+    repacked weight tiles, each 256-byte aligned; 0 where the mid-group kernel runs) and
+    the host checks of w4a8_midgroup_gemm_ws, before any launch.  Without a GPU the
+    library takes 256 CUs."""
+    q = lib.w4a8_midgroup_gemm_workspace_bytes
+    c256 = lambda n: -(-n // 256) * 256
+    tiled = c256(c256(4096 * 5120) + 5 * 4096 * 4) + 448 * 40 * 1024
+    assert q(4096, 7168, 5120, 1024) == tiled
+    assert q(4096, 7168, 5000, 1000) == tiled                    # stride 1024, ragged K
+    assert q(100, 8192, 1057, 1024) == c256(100 * 1152) + 2 * 100 * 4
+    assert q(65, 8200, 3456, 256) == c256(65 * 3456) + 14 * 65 * 4
+    assert q(1024, 7168, 5120, 1024) == c256(1024 * 5120) + 5 * 1024 * 4
+    # the mid-group kernel keeps: up to 64 rows, 64-row tiles for fewer than half
+    # the CUs, group stride 128 or not a multiple of 128, offsets past 2^31
+    assert q(64, 7168, 5120, 1024) == 0
+    assert q(128, 7168, 5120, 1024) == 0 and q(256, 7168, 5120, 1024) > 0
+    assert q(4096, 7168, 5120, 128) == 0
+    assert q(4096, 7168, 5120, 64) == 0
+    assert q(80000, 5120, 27648, 1024) == 0
+    assert q(0, 512, 1024, 1024) == 0 and q(100, 0, 1024, 1024) == 0 and q(100, 512, 1024, 0) == 0
+
+    def call(ws, wsb, Ma=128, ld_as=128):
+        return lib.w4a8_midgroup_gemm_ws(16, 16, 16, 16, Ma, ld_as, 16, 16, 16, 16, 16384, None, 16384, 2048, 1024,
+                                         ws, wsb, None)
+    need = q(128, 16384, 2048, 1024)
+    assert need > 0
+    assert call(None, need) == 6 and b"workspace" in lib.w4a8_last_error()
+    assert call(4096, need - 1) == 6
+    assert call(4096 + 16, need) == 6                 # not 256-byte aligned
+    assert call(4096, -1) == 6
+    assert call(4096, need, ld_as=64) == 2            # ld_as < rows

@@ -1168,6 +1168,110 @@ def test_midgroup_qwq_decode_shapes(pkg, dev, proj, M):
     check_output(tensor_bf16_bits(y)[:M], y32[:M], f"midgroup {proj} M{M}", exact_mid(qp, tensor_bf16_bits(a[2]), codes, sc, zr, 1024))
 
 
+MIDGROUP_PREFILL_CASES = [
+    # (M, N, K, G, asym): past 64 rows with 64-row output tiles for at least half
+    # of 256 CUs (no partial dump), the compat GEMM runs the LDS-tiled prefill
+    # waves on the activation rows rebuilt into a workspace; from 2048 rows on
+    # weight tiles repacked there too
+    (65, 8200, 5120, 1024, True),      # the first row count on it; last column tile partial
+    (100, 8192, 1057, 1024, True),     # ragged K: the last step's upper half is padding
+    (300, 3000, 5120, 1024, False),    # symmetric: zero point all 0
+    (512, 2100, 3072, 1024, True),     # N not a multiple of 16
+    (200, 4200, 3456, 256, True),      # stride 256 (two steps per group)
+    (129, 4000, 1152, 384, True),      # stride 384 (three steps per group)
+    (700, 2064, 2048, 1024, True),     # 64-row tiles
+    (2048, 2064, 2048, 1024, True),    # repacked weight tiles, 128-row tiles
+    (2048, 1000, 1057, 1024, False),   # repacked tiles, ragged K, N not a multiple of 16
+]
+
+
+def _midgroup_inputs(pkg, dev, M, N, K, G, asym, seed):
+    xb = pkg.synth.activations(M, K, seed=seed)
+    w = np.random.default_rng(seed).standard_normal((N, K)).astype(np.float32) * 0.05
+    codes, sc, zr, ks = ow.quantize_weight_asym(w, G)
+    if not asym:
+        zr = np.zeros_like(zr)
+    a = torch.ops.npu.midgroup_quant_a(bf16_bits_tensor(xb).to(dev), G)
+    args = (torch.from_numpy(ow.pack_grouped(codes, G)).to(dev), bits_tensor(sc, torch.bfloat16).to(dev),
+            torch.from_numpy(ks).to(dev), bits_tensor(zr, torch.bfloat16).to(dev))
+    return xb, codes, sc, zr, a, args
+
+
+@pytest.mark.parametrize("M,N,K,G,asym", MIDGROUP_PREFILL_CASES)
+def test_midgroup_prefill_path_equals_reference_order(pkg, dev, M, N, K, G, asym):
+    """One wave walks each output's groups in order, with the reference's roundings, so
+    the bf16 output equals bf16(ReferenceMidGroupGemm's fp32 result) bit for bit
+    (int4_cube_lab/host/gemm_ref.cpp:199-240, restated by the oracle)."""
+    say(f"midgroup prefill path M={M} N={N} K={K} G={G} asym={asym}")
+    xb, codes, sc, zr, a, args = _midgroup_inputs(pkg, dev, M, N, K, G, asym, seed=3 * M + N + K)
+    Mp = a[0].shape[0]
+    assert pkg._abi.lib().w4a8_midgroup_gemm_workspace_bytes(Mp, N, K, G) > 0, "case not on the prefill path"
+    y = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G)
+    torch.cuda.synchronize()
+    q, _ = ow.quant_act_midgroup(xb, G)
+    qp = np.zeros((Mp, K), np.int8)
+    qp[:M] = q
+    y32 = ow.gemm_midgroup_fp32(qp, tensor_bf16_bits(a[2]), codes, sc, zr, G)
+    got = tensor_bf16_bits(y)
+    want = ow.f32_to_bf16_bits(y32)
+    assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} outputs differ from bf16(oracle fp32)"
+    assert np.abs(y32).max() > 0
+
+
+@pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
+@pytest.mark.parametrize("M", [1024, 4096])
+def test_midgroup_prefill_qwq_shapes(pkg, dev, proj, M):
+    """The reference's group 1024 at QwQ-32B shapes (stored weights at 1024 rows, repacked
+    tiles at 4096), on 40 sampled rows (every column) against the oracle's fp32 order, bit
+    for bit."""
+    K, N = pkg.synth.QWQ_SHAPES[proj]
+    say(f"midgroup prefill qwq {proj} M={M}")
+    xb, codes, sc, zr, a, args = _midgroup_inputs(pkg, dev, M, N, K, 1024, True, seed=11)
+    y = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, 1024)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(5).choice(M, 40, replace=False))
+    q, _ = ow.quant_act_midgroup(xb[rows], 1024)
+    y32 = ow.gemm_midgroup_fp32(q, tensor_bf16_bits(a[2])[:, rows], codes, sc, zr, 1024)
+    got = tensor_bf16_bits(y)[rows]
+    want = ow.f32_to_bf16_bits(y32)
+    assert np.array_equal(got, want), f"{proj}: {int((got != want).sum())} of {got.size} sampled outputs differ"
+
+
+def test_midgroup_prefill_path_without_zero_points(pkg, dev):
+    """The C ABI's symmetric call (w_zero NULL: the variant without the zero-point term)
+    equals the call with an all-zero w_zero, through w4a8_midgroup_gemm_ws."""
+    say("midgroup prefill path, w_zero NULL")
+    M, N, K, G = 300, 3000, 3072, 1024
+    _, _, _, _, a, args = _midgroup_inputs(pkg, dev, M, N, K, G, False, seed=9)
+    y0 = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G)
+    a_hi, a_lo, a_scale, a_ksum = a
+    w_q, w_scale = args[0], args[1]
+    Mp = a_hi.shape[0]
+    lib = pkg._abi.lib()
+    need = lib.w4a8_midgroup_gemm_workspace_bytes(Mp, N, K, G)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    y1 = torch.empty((Mp, N), dtype=torch.bfloat16, device=dev)
+    rc = lib.w4a8_midgroup_gemm_ws(a_hi.data_ptr(), a_lo.data_ptr(), a_scale.data_ptr(), a_ksum.data_ptr(), Mp,
+                                   a_scale.stride(0), w_q.data_ptr(), w_scale.data_ptr(), None, y1.data_ptr(), N,
+                                   None, N, K, G, ws.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.w4a8_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+
+
+def test_midgroup_prefill_path_relaunch_deterministic(pkg, dev):
+    """Repeated calls of the prefill path (pre-pass, then the GEMM on a fresh workspace)
+    return the same bytes (the reference's --stress relaunch check, mg_harness.h:307-334)."""
+    for M in (600, 2048):   # stored weights, then weight tiles repacked per call
+        say(f"midgroup prefill relaunch M={M}")
+        _, _, _, _, a, args = _midgroup_inputs(pkg, dev, M, 3000, 5120, 1024, True, seed=7)
+        ys = [torch.ops.npu.midgroup_w4a8_gemm(*a, *args, 5120, 1024) for _ in range(6)]
+        torch.cuda.synchronize()
+        for y in ys[1:]:
+            assert torch.equal(y.view(torch.int16), ys[0].view(torch.int16))
+
+
 def test_midgroup_linear_module(pkg, dev):
     """The reference's MidGroupW4A8LinearMethod.apply semantics: [N, G] checkpoint tensors,
     quant_a, GEMM, slice to the real rows, bias, reshape."""

@@ -209,7 +209,7 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 8; }
+int w4a8_abi_version(void) { return 9; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
@@ -394,9 +394,10 @@ int w4a8_midgroup_quant_a(const void* x, int64_t ldx, void* a_hi, void* a_lo, vo
                       "w4a8_midgroup_quant_a launch");
 }
 
-int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
-                       int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y, int64_t ldy,
-                       void* partials, int64_t N, int64_t K, int64_t group, void* stream) {
+static int midgroup_gemm_impl(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum,
+                              int64_t Ma, int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero,
+                              void* y, int64_t ldy, void* partials, int64_t N, int64_t K, int64_t group,
+                              void* workspace, int64_t workspace_bytes, void* stream) {
     if (int rc = check_problem(Ma, N, K, group)) return rc;
     if (geom::group_stride(group) % 128 != 0)
         return fail(W4A8_ERR_UNSUPPORTED, "group=%lld: the mid-group path needs ceil_to(group, 64) %% 128 == 0",
@@ -413,9 +414,20 @@ int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, 
     if ((Ma + 16) * kb >= (1ll << 31) || (N + 16) * kb >= (1ll << 31))
         return fail(W4A8_ERR_UNSUPPORTED, "operands too large for 32-bit offsets (%lld rows, N=%lld, %lld B/row)", Ma,
                     N, kb);
-    if (midgroup_lds_bytes(Ma, K, group) > 64 * 1024)
+    // Prefill sizes with a workspace: the LDS-tiled prefill waves (no partial
+    // dump there; dumps and calls without a workspace take the mid-group kernel)
+    const int64_t need = partials ? 0 : midgroup_prefill_workspace_bytes(Ma, N, K, group);
+    const bool prefill = need > 0 && workspace_bytes > 0;
+    if (prefill) {
+        if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+            return fail(W4A8_ERR_WORKSPACE, "workspace of %lld bytes (256-byte aligned) needed, got %lld", need,
+                        workspace_bytes);
+        if (geom::num_groups(K, group) * ld_as * 4 >= (1ll << 31))
+            return fail(W4A8_ERR_UNSUPPORTED, "ld_as=%lld: activation ksums too large for 32-bit offsets", ld_as);
+    } else if (midgroup_lds_bytes(Ma, K, group) > 64 * 1024) {
         return fail(W4A8_ERR_UNSUPPORTED, "K=%lld group=%lld: too many groups for the staged scales (%lld B LDS)", K,
                     group, midgroup_lds_bytes(Ma, K, group));
+    }
     MidgroupArgs a{};
     a.a_hi = a_hi;
     a.a_lo = a_lo;
@@ -432,7 +444,31 @@ int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, 
     a.N = N;
     a.K = K;
     a.group = group;
+    if (prefill)
+        return hip_status(launch_gemm_midgroup_prefill(a, workspace, workspace_bytes, static_cast<hipStream_t>(stream)),
+                          "w4a8_midgroup_gemm_ws launch");
     return hip_status(launch_gemm_midgroup(a, static_cast<hipStream_t>(stream)), "w4a8_midgroup_gemm launch");
+}
+
+int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
+                       int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y, int64_t ldy,
+                       void* partials, int64_t N, int64_t K, int64_t group, void* stream) {
+    return midgroup_gemm_impl(a_hi, a_lo, a_scale, a_ksum, Ma, ld_as, w_q, w_scale, w_zero, y, ldy, partials, N, K,
+                              group, nullptr, 0, stream);
+}
+
+int64_t w4a8_midgroup_gemm_workspace_bytes(int64_t Ma, int64_t N, int64_t K, int64_t group) {
+    if (Ma < 0 || N <= 0 || K <= 0 || group <= 0) return 0;
+    return midgroup_prefill_workspace_bytes(Ma, N, K, group);
+}
+
+int w4a8_midgroup_gemm_ws(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
+                          int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y,
+                          int64_t ldy, void* partials, int64_t N, int64_t K, int64_t group, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
+    if (workspace_bytes < 0) return fail(W4A8_ERR_WORKSPACE, "workspace_bytes=%lld < 0", workspace_bytes);
+    return midgroup_gemm_impl(a_hi, a_lo, a_scale, a_ksum, Ma, ld_as, w_q, w_scale, w_zero, y, ldy, partials, N, K,
+                              group, workspace, workspace_bytes, stream);
 }
 
 int w4a8_rmsnorm_quant(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight, float eps,

@@ -189,6 +189,18 @@ __device__ __forceinline__ uint32_t quant2(uint32_t u, const RowScale& q) {
 __device__ __forceinline__ int unpack_lo4(uint32_t w) { return static_cast<int>((w << 4) & 0xf0f0f0f0u); }
 __device__ __forceinline__ int unpack_hi4(uint32_t w) { return static_cast<int>(w & 0xf0f0f0f0u); }
 
+// The reference's mid-group activation planes (one int4 code per nibble,
+// even K in the low nibble): q = 16*hi + lo + 8, stored as hi and lo ^ 8.
+// Even and odd activation bytes of one dword of each plane: byte j of `ev` is
+// (hi nibble 2j << 4) | (lo nibble 2j ^ 8), of `od` the same for nibble 2j+1
+// -- the order unpack_lo4 / unpack_hi4 give the weight codes of the same K.
+// The lo plane's offset flip (every nibble ^ 8) is one xor for both.
+__device__ __forceinline__ void act_pair(uint32_t h, uint32_t l, int& ev, int& od) {
+    const uint32_t lx = l ^ 0x88888888u;
+    ev = static_cast<int>(((h << 4) & 0xf0f0f0f0u) | (lx & 0x0f0f0f0fu));
+    od = static_cast<int>((h & 0xf0f0f0f0u) | ((lx >> 4) & 0x0f0f0f0fu));
+}
+
 // 16 packed bytes (32 codes, two 64-K slabs of 16 codes each for one lane) ->
 // the two MFMA B operands.
 __device__ __forceinline__ void unpack_tile_lane(const uint4 w, v4i& slab0, v4i& slab1) {

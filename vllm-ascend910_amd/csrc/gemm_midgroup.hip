@@ -61,15 +61,6 @@ struct MidParams {
     uint32_t a_bytes, w_bytes;
 };
 
-// Even and odd activation bytes of one dword of each plane: byte j of `ev` is
-// (hi nibble 2j << 4) | (lo nibble 2j ^ 8), of `od` the same for nibble 2j+1.
-// The lo plane's offset flip (every nibble ^ 8) is one xor for both.
-__device__ __forceinline__ void act_pair(uint32_t h, uint32_t l, int& ev, int& od) {
-    const uint32_t lx = l ^ 0x88888888u;
-    ev = static_cast<int>(((h << 4) & 0xf0f0f0f0u) | (lx & 0x0f0f0f0fu));
-    od = static_cast<int>((h & 0xf0f0f0f0u) | ((lx >> 4) & 0x0f0f0f0fu));
-}
-
 template <int MT, int CPW, int KWMAX, int D, bool ASYM, bool DUMP>
 __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidParams p) {
     constexpr int R = 16 * MT;
@@ -157,6 +148,8 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
     __syncthreads();   // LDS scales staged
 
     auto fold = [&](int g, bool own) __attribute__((always_inline)) {
+        // the reference's separate roundings: no multiply-add contraction
+#pragma clang fp contract(off)
 #pragma unroll
         for (int c = 0; c < CPW; ++c) {
             const float ws = s_ws[g * C + c * 16 + colq];
@@ -172,8 +165,8 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
                         if (own && row < p.Ma && col < p.N && g < p.NG)
                             p.P[(static_cast<int64_t>(g) * p.Ma + row) * p.N + col] = I;
                     }
-                    const float t1 = __fmul_rn(static_cast<float>(I), ws);
-                    acc[mt][c][i] = __fadd_rn(acc[mt][c][i], __fmul_rn(t1, s_as[g * R + r]));
+                    const float t1 = static_cast<float>(I) * ws;
+                    acc[mt][c][i] = acc[mt][c][i] + t1 * s_as[g * R + r];
                 }
                 P[mt][c] = v4i{0, 0, 0, 0};
             }
@@ -335,6 +328,8 @@ __global__ __launch_bounds__(64 * kShWaves) void gemm_midgroup_shared_kernel(con
         for (int i = 0; i < 4; ++i) acc[c][i] = 0.0f;
     }
     auto fold = [&](int g) __attribute__((always_inline)) {
+        // the reference's separate roundings: no multiply-add contraction
+#pragma clang fp contract(off)
 #pragma unroll
         for (int c = 0; c < CPW; ++c) {
             const int cw = (wave * CPW + c) * 16 + colq;
@@ -348,8 +343,8 @@ __global__ __launch_bounds__(64 * kShWaves) void gemm_midgroup_shared_kernel(con
                     const int col = nbw * 16 + cw;
                     if (r < p.Ma && col < p.N) p.P[(static_cast<int64_t>(g) * p.Ma + r) * p.N + col] = I;
                 }
-                const float t1 = __fmul_rn(static_cast<float>(I), ws);
-                acc[c][i] = __fadd_rn(acc[c][i], __fmul_rn(t1, s_as[g * R + r]));
+                const float t1 = static_cast<float>(I) * ws;
+                acc[c][i] = acc[c][i] + t1 * s_as[g * R + r];
             }
             Pm[c] = v4i{0, 0, 0, 0};
         }

@@ -94,7 +94,19 @@ struct PrefillParams {
     int splits;        // gemm_prefill_cols_kernel: workgroups along K (blockIdx.y); > 1 writes fp32 sums to R
     float* R;          // splits > 1: fp32 sums before the token scale [splits, M, ldr]
     int64_t ldr;       // NB * 16
+    // The reference's mid-group tensors (gemm_prefill_kernel with CM > 0): A
+    // holds the activation bytes compat_act_kernel rebuilt from the two
+    // planes, W the packed codes [N, kb] and S the weight scales [G, N] as
+    // stored, c_as the activation scales as fp32 [G, M] (rebuilt), c_ak the
+    // ksums [G, ld_as] and c_wz the zero points [G, N] (CM == 2) as stored.
+    const float* c_as;
+    const int32_t* c_ak;
+    const uint16_t* c_wz;
+    int ld_as, kb;
+    uint32_t as_bytes, ak_bytes;
 };
+
+constexpr uint32_t kOOB = 0x80000000u;   // an offset past every buffer here (all below 2^31 bytes)
 
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
 // L2.  Renumber them so that every XCD walks one contiguous run of tiles, and
@@ -151,14 +163,33 @@ __device__ __forceinline__ void store_tile(const PrefillParams& p, const uint16_
 // up columns, so each lane holds both operands of its outputs
 // silu(y[:, n]) * y[:, n + N/2] (a tile covers 64 outputs); every column
 // accumulates exactly as in the plain GEMM.
-template <int GMODE, int DW, bool SBF16, bool DUMP, bool SWIGLU, int BM>
+// CM: the reference's mid-group compat GEMM (1 symmetric, 2 with zero
+// points; group stride 128*t, t >= 2), y = bf16(sum_g (float(I_g) * ws) * as)
+// with I_g = P_g + wz * a_ksum, the fold order of ReferenceMidGroupGemm
+// (int4_cube_lab/host/gemm_ref.cpp:199-240).  WT: the weights repacked into
+// tiles per call (as the per-token path's, natural K order; the activation
+// rows rebuilt in natural order).  Otherwise they are read as stored: lane
+// (column c, half hh) takes bytes 32 hh .. 32 hh + 31 of its column's 64-byte
+// step, so slab s holds codes 64 hh + 16 s + [0, 16) in unpack order (even
+// codes, then odd, per dword), and compat_act_kernel writes each activation
+// row's bytes in that same K order at the positions the operand reads below
+// take (logical chunk 2 s + hh).  The per-row activation
+// scales and ksums of a group reach LDS through a four-step register ring (one
+// dword load per lane and step: rows 0..BM-1 of the scales by the first BM
+// threads, of the ksums by the others), written a step before the group's
+// fold reads them.
+template <int GMODE, int DW, bool SBF16, bool DUMP, bool SWIGLU, int BM, int CM = 0, bool WT = false>
 __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(const PrefillParams p) {
     constexpr int kThreads = threads_for<BM>();
     constexpr int kBM = BM;
     constexpr int kABuf = BM * 128;              // one step's A tile in LDS (unpadded 128-byte rows)
     constexpr int kABuf01 = abuf01_bytes<BM, SWIGLU>();
+    constexpr bool COMPAT = CM > 0;
+    constexpr bool RAWW = COMPAT && !WT;   // compat weights read as stored (else repacked tiles)
     static_assert(kNA == BM * 8 / kThreads, "four 16-byte A chunks per lane per step");
     static_assert(!(SWIGLU && DUMP), "the SwiGLU variant dumps nothing");
+    static_assert(!COMPAT || (GMODE == 3 && !DUMP && !SWIGLU && SBF16 && kThreads == 2 * BM),
+                  "the compat variant: group stride 128*t (t >= 2), bf16 scales, no dump, no SwiGLU");
     // Four separate A buffers (separate objects, so the compiler's tracking of
     // loads into LDS keeps reads of one buffer from waiting on loads into
     // another).
@@ -189,10 +220,14 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
     // epilogue (a load issued there would add a memory round trip per row).
     __shared__ uint32_t tsl[kBM];
     uint32_t ts_bits = 0;
-    if (tid < kBM && m0 + tid < p.M) ts_bits = p.a_scale[m0 + tid];
+    if constexpr (!COMPAT) {
+        if (tid < kBM && m0 + tid < p.M) ts_bits = p.a_scale[m0 + tid];
+    }
 
     // ---- weights: byte offsets of this lane's two 16-byte chunks per step,
     // for the wave's 32-column blocks j = 0, 1 (column blocks past N read 0).
+    // Compat: chunk 0 holds slabs 0-1 and chunk 1 slabs 2-3 of the stored
+    // row; columns past N read zero.
     uint32_t woff[2][2];
     uint32_t soff[2];
     int colj[2];
@@ -200,10 +235,17 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
     for (int j = 0; j < 2; ++j) {
         const int col = SWIGLU ? n0 + wn * 32 + c32 + j * p.half_n : n0 + wn * 64 + j * 32 + c32;
         colj[j] = col;
-        const uint32_t tile0 = static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u;
-        woff[j][0] = tile0 + static_cast<uint32_t>((col & 15) + 16 * hh) * 16u;        // slabs 0, 2
-        woff[j][1] = tile0 + static_cast<uint32_t>((col & 15) + 16 * (2 + hh)) * 16u;  // slabs 1, 3
-        soff[j] = (static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.NG) * 16u + (col & 15)) * 2u;
+        if constexpr (RAWW) {
+            const bool in = col < p.N;
+            woff[j][0] = in ? static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 32u * hh : kOOB;
+            woff[j][1] = woff[j][0] + 16u;
+        } else {
+            const uint32_t tile0 = static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u;
+            woff[j][0] = tile0 + static_cast<uint32_t>((col & 15) + 16 * hh) * 16u;        // slabs 0, 2
+            woff[j][1] = tile0 + static_cast<uint32_t>((col & 15) + 16 * (2 + hh)) * 16u;  // slabs 1, 3
+        }
+        if constexpr (COMPAT) soff[j] = col < p.N ? static_cast<uint32_t>(col) * 2u : kOOB;
+        else soff[j] = (static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.NG) * 16u + (col & 15)) * 2u;
     }
 
     // ---- activations: each step's A[128 rows][128 K] goes straight from
@@ -230,7 +272,7 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 
     uint4 wr[DW][2][2];
     auto load_w = [&](int slot, int kt) {
-        const uint32_t t = static_cast<uint32_t>(min(kt, p.KT - 1)) * 1024u;
+        const uint32_t t = static_cast<uint32_t>(min(kt, p.KT - 1)) * (RAWW ? 64u : 1024u);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             wr[slot][j][0] = buf_load16(rw_rsrc, woff[j][0] + t);
@@ -249,10 +291,51 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 #pragma unroll
         for (int h = 0; h < NSC; ++h) {
             const int g = min((ktc * 128 + (ONE_END ? 127 : h * 64 + 63)) / p.gs, p.NG - 1);
+            const uint32_t go = static_cast<uint32_t>(g) * (COMPAT ? static_cast<uint32_t>(p.N) * 2u : 32u);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) sv[j][h] = buf_load_u16(rs_rsrc, soff[j] + static_cast<uint32_t>(g) * 32u);
+            for (int j = 0; j < 2; ++j) sv[j][h] = buf_load_u16(rs_rsrc, soff[j] + go);
         }
     };
+    // Compat: the zero points of the same groups (CM == 2), and the row ring.
+    // Vector memory operations per step: kNA A chunks, four weight chunks,
+    // the scales (and zero points), the ring's dword.
+    constexpr int kStepVm = kNA + 4 + 2 * NSC * (CM == 2 ? 2 : 1) + (COMPAT ? 1 : 0);
+    const auto rz_rsrc = make_rsrc(p.c_wz, CM == 2 ? static_cast<uint32_t>(p.NG) * static_cast<uint32_t>(p.N) * 2u : 0u);
+    auto load_z = [&](int kt, uint32_t (&zv)[2][NSC]) {
+        if constexpr (CM == 2) {
+            const int ktc = min(kt, p.KT - 1);
+#pragma unroll
+            for (int h = 0; h < NSC; ++h) {
+                const int g = min((ktc * 128 + (ONE_END ? 127 : h * 64 + 63)) / p.gs, p.NG - 1);
+                const uint32_t go = static_cast<uint32_t>(g) * static_cast<uint32_t>(p.N) * 2u;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) zv[j][h] = buf_load_u16(rz_rsrc, soff[j] + go);
+            }
+        }
+    };
+    // Row values of group g(kt) = min(kt / tpg, NG - 1): thread t < BM loads
+    // the fp32 activation scale of tile row t, thread BM + t its ksum (a
+    // wave-uniform choice); rows past M read zero.  Two LDS slots by group
+    // parity: the value of g(kt + 1) is written during step kt, after the
+    // barrier that ended the fold of group g(kt) - 1 (the same slot), and before
+    // the barrier ahead of g(kt + 1)'s fold.
+    // One LDS object for both (slot b: scales at cfv[2 b BM + r], ksums at
+    // cfv[2 b BM + BM + r]): a store that picks between two objects is not
+    // told apart from the A buffers' loads to LDS, and the compiler then
+    // waits for those loads before it.
+    __shared__ __attribute__((aligned(16))) uint32_t cfv[COMPAT ? 4 * kBM : 1];
+    const bool as_wave = wave < kBM / 64;
+    const int rvr = as_wave ? tid : tid - kBM;
+    const uint32_t rvo = (m0 + rvr < p.M) ? static_cast<uint32_t>(m0 + rvr) * 4u : kOOB;
+    const auto ras_rsrc = make_rsrc(p.c_as, COMPAT ? p.as_bytes : 0u);
+    const auto rak_rsrc = make_rsrc(p.c_ak, COMPAT ? p.ak_bytes : 0u);
+    auto group_of = [&](int kt) { return min(kt / p.tpg, p.NG - 1); };
+    auto load_rv = [&](int kt) -> uint32_t {
+        const uint32_t g = static_cast<uint32_t>(group_of(kt));
+        if (as_wave) return buf_load_u32(ras_rsrc, rvo + g * static_cast<uint32_t>(p.M) * 4u);
+        return buf_load_u32(rak_rsrc, rvo + g * static_cast<uint32_t>(p.ld_as) * 4u);
+    };
+    auto store_rv = [&](int kt, uint32_t v) { cfv[(group_of(kt) & 1) * 2 * kBM + (as_wave ? 0 : kBM) + rvr] = v; };
 
     v16i P[2][2];
     float acc[2][2][16];
@@ -270,6 +353,40 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 
     // acc[rb] += float(P[rb]) * w_scale for row block rb of group g;
     // ws2[j] are the scale bits of the wave's column blocks j = 0, 1.
+    // Compat: acc[rb] += (float(P/16 + wz * a_ksum) * ws) * as, rounded at
+    // each operation (zs2: the zero-point bits; the rows' values from LDS).
+    auto fold_cm = [&](int rb, int g, const uint32_t (&ws2)[2], const uint32_t (&zs2)[2])
+        __attribute__((always_inline)) {
+        // the reference's separate roundings: no multiply-add contraction
+#pragma clang fp contract(off)
+        const int b = (g & 1) * 2 * kBM;
+        float ws[2];
+        int wz[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            ws[j] = bf16_bits_to_f32(ws2[j]);
+            wz[j] = CM == 2 ? static_cast<int>(bf16_bits_to_f32(zs2[j])) : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r0 = wm * 64 + rb * 32 + q * 8 + hh * 4;   // rows r0..r0+3: i = 4 q .. 4 q + 3
+            const uint4 as4 = *reinterpret_cast<const uint4*>(&cfv[b + r0]);
+            const uint4 ak4 = *reinterpret_cast<const uint4*>(&cfv[b + kBM + r0]);
+            const float as[4] = {__uint_as_float(as4.x), __uint_as_float(as4.y), __uint_as_float(as4.z),
+                                 __uint_as_float(as4.w)};
+            const int ak[4] = {static_cast<int>(ak4.x), static_cast<int>(ak4.y), static_cast<int>(ak4.z),
+                               static_cast<int>(ak4.w)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int i = q * 4 + e;
+                    const int I = (P[rb][j][i] >> 4) + (CM == 2 ? wz[j] * ak[e] : 0);
+                    const float t1 = static_cast<float>(I) * ws[j];
+                    acc[rb][j][i] = acc[rb][j][i] + t1 * as[e];
+                }
+        }
+    };
     auto fold_rb = [&](int rb, int g, const uint32_t (&ws2)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -293,6 +410,11 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
     // ---- prologue: A(0..2) to their LDS buffers, then W(0..DW-1) and the
     // first scales (the empty asm statements keep this issue order, which the
     // wait below counts on)
+    // Compat: group 0's row values first (written to LDS below), the ring's
+    // next three entries after the scales.
+    uint32_t rv[4] = {0u, 0u, 0u, 0u};
+    uint32_t rv0 = 0u;
+    if constexpr (COMPAT) rv0 = load_rv(0);
     load_a(0, 0);
     load_a(1, 1);
     load_a(2, 2);
@@ -301,14 +423,23 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
     for (int s = 0; s < DW; ++s) load_w(s, s);
     uint32_t sc[2][NSC];
     load_s(0, sc);
+    uint32_t zc[2][NSC] = {};
+    load_z(0, zc);
+    if constexpr (COMPAT) {
+        rv[1] = load_rv(1);
+        rv[2] = load_rv(2);
+        rv[3] = load_rv(3);
+    }
     asm volatile("" ::: "memory");
     // STAG: the scale bits of the previous step's groups (zero before step 0,
     // whose fold of row block 1 adds zero partials times zero)
     uint32_t scp[2] = {0u, 0u};
     if (tid < kBM) tsl[tid] = ts_bits;
-    // A(0) has landed once at most the 2 * kNA + DW * 4 + 2 * NSC newer
-    // loads are outstanding; then every wave's part of it is in LDS
-    wait_vm_barrier<2 * kNA + DW * 4 + 2 * NSC>();
+    if constexpr (COMPAT) store_rv(0, rv0);
+    // A(0) has landed once at most the loads issued after it are outstanding
+    // (A(1), A(2), the weight ring, the scales, the row ring); then every
+    // wave's part of it is in LDS
+    wait_vm_barrier<2 * kNA + DW * 4 + (kStepVm - kNA - 4) + (COMPAT ? 2 : 0)>();
 
     // This lane's A operand offsets for slab s of row block 0 (row block 1 is
     // 32 rows = 4096 bytes further): row wm * 64 + c32, logical chunk 2 s + hh.
@@ -325,6 +456,14 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
         load_a(kt + 3, (buf + 3) % kNB);
         uint32_t scn[2][NSC];
         load_s(kt + 1, scn);
+        uint32_t zcn[2][NSC] = {};
+        load_z(kt + 1, zcn);
+        if constexpr (COMPAT) {
+            // ring entry of step kt - 3 (landed: the barrier ending step kt - 1
+            // waited for it) -> LDS; this step's entry is group g(kt + 4)'s
+            store_rv(kt + 1, rv[(buf + 1) & 3]);
+            rv[buf] = load_rv(kt + 4);
+        }
         // A operands from LDS two slabs at a time: slabs 0-1 now (their
         // latency hides behind the weight unpack), slabs 2-3 before slab 1's
         // MFMAs.  The scheduling barrier keeps the first reads ahead of the
@@ -355,9 +494,12 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const uint4 w = wr[u][j][s & 1];
-                const uint32_t d0 = (s >> 1) ? w.z : w.x;
-                const uint32_t d1 = (s >> 1) ? w.w : w.y;
+                // repacked: chunk s % 2, half s / 2; stored compat rows:
+                // chunk s / 2, half s % 2
+                const uint4 w = wr[u][j][RAWW ? (s >> 1) : (s & 1)];
+                const bool upper = RAWW ? (s & 1) : (s >> 1);
+                const uint32_t d0 = upper ? w.z : w.x;
+                const uint32_t d1 = upper ? w.w : w.y;
                 bvs[s][j] = v4i{unpack_lo4(d0), unpack_hi4(d0), unpack_lo4(d1), unpack_hi4(d1)};
             }
         load_w(u, kt + DW);
@@ -439,8 +581,14 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
                 if (ends) {
                     const int h = ONE_END ? 0 : (s >> 1);
                     const uint32_t ws2[2] = {sc[0][h], sc[1][h]};
-                    fold_rb(0, g, ws2);
-                    fold_rb(1, g, ws2);
+                    if constexpr (COMPAT) {
+                        const uint32_t zs2[2] = {zc[0][h], zc[1][h]};
+                        fold_cm(0, g, ws2, zs2);
+                        fold_cm(1, g, ws2, zs2);
+                    } else {
+                        fold_rb(0, g, ws2);
+                        fold_rb(1, g, ws2);
+                    }
                     if constexpr (GMODE >= 2) {
 #pragma unroll
                         for (int rb = 0; rb < 2; ++rb)
@@ -453,12 +601,15 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int h = 0; h < NSC; ++h) sc[j][h] = scn[j][h];
+            for (int h = 0; h < NSC; ++h) {
+                sc[j][h] = scn[j][h];
+                zc[j][h] = zcn[j][h];
+            }
     };
 
     // Steps are unrolled by kNB (a multiple of DW), so the A buffer and the
     // weight ring slot of each step are compile-time indices.  A step issues
-    // exactly kNA + 4 + 2 * NSC vector memory operations (the partial dump
+    // exactly kStepVm vector memory operations (the partial dump
     // only adds stores, which make the wait below stricter); A(kt + 1), loaded
     // during step kt - 2, has landed once at most the two newest steps'
     // operations are outstanding, and after the barrier every wave's part of
@@ -467,7 +618,7 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
     static_assert(kNB % DW == 0, "an unrolled group covers whole weight rings");
     auto one = [&](int kt, int u) __attribute__((always_inline)) {
         step(kt, u % DW, u % kNB);
-        wait_vm_barrier<2 * (kNA + 4 + 2 * NSC)>();
+        wait_vm_barrier<2 * kStepVm>();
     };
     // Whole groups of kNB steps, then the remaining steps after the loop: an
     // early exit inside the unrolled group would give the loop header a path
@@ -502,7 +653,7 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int r = wm * 64 + rb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);   // row in the tile
-            const float ts = bf16_bits_to_f32(tsl[r]) * 0.0625f;
+            const float ts = COMPAT ? 1.0f : bf16_bits_to_f32(tsl[r]) * 0.0625f;
             if constexpr (SWIGLU) {
                 orow(r)[wn * 32 + c32] =
                     static_cast<uint16_t>(swiglu_bf16_bits(acc[rb][0][i] * ts, acc[rb][1][i] * ts));
@@ -735,6 +886,49 @@ __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_prefill_cols_kerne
                                       m0, n0, p.N, tid);
 }
 
+// The reference's mid-group activation planes rebuilt for the compat variant
+// of gemm_prefill_kernel: row `blockIdx.x` of A [Ma, KT * 128], whose 16-byte
+// chunk L = 2 s + hh of step kt holds the codes kt * 128 + 64 hh + 16 s +
+// [0, 16) (even codes of each dword first, as act_pair builds them; codes past
+// kpad are zero), and the row's activation scales as fp32 into as32 [G, Ma].
+// NAT: natural K order instead (chunk L of step kt: codes kt * 128 + 16 L +
+// [0, 16), byte i = code i), for the repacked weight tiles.
+template <bool NAT>
+__global__ __launch_bounds__(256) void compat_act_kernel(const uint8_t* __restrict__ hi,
+                                                         const uint8_t* __restrict__ lo,
+                                                         const uint16_t* __restrict__ a_scale, int ld_as, int kb,
+                                                         int kpad, int Ma, int KT, int NG, int8_t* __restrict__ A,
+                                                         float* __restrict__ as32) {
+    const int64_t row = blockIdx.x;
+    const int ci = static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x);
+    if (ci < KT * 8) {
+        const int L = ci & 7, kt = ci >> 3;
+        const int k0 = NAT ? kt * 128 + 16 * L : kt * 128 + 64 * (L & 1) + 16 * (L >> 1);
+        uint4 out = make_uint4(0u, 0u, 0u, 0u);
+        if (k0 < kpad) {   // k0 and kpad are multiples of 16: the chunk is whole
+            const int64_t src = row * kb + k0 / 2;
+            const uint2 h = *reinterpret_cast<const uint2*>(hi + src);
+            const uint2 l = *reinterpret_cast<const uint2*>(lo + src);
+            int e0, o0, e1, o1;
+            act_pair(h.x, l.x, e0, o0);
+            act_pair(h.y, l.y, e1, o1);
+            if (NAT) {
+                // bytes [e.b0, o.b0, e.b1, o.b1], [e.b2, o.b2, e.b3, o.b3]
+                const uint32_t ue0 = e0, uo0 = o0, ue1 = e1, uo1 = o1;
+                out = make_uint4(__builtin_amdgcn_perm(uo0, ue0, 0x05010400u), __builtin_amdgcn_perm(uo0, ue0, 0x07030602u),
+                                 __builtin_amdgcn_perm(uo1, ue1, 0x05010400u), __builtin_amdgcn_perm(uo1, ue1, 0x07030602u));
+            } else {
+                out = make_uint4(static_cast<uint32_t>(e0), static_cast<uint32_t>(o0), static_cast<uint32_t>(e1),
+                                 static_cast<uint32_t>(o1));
+            }
+        }
+        *reinterpret_cast<uint4*>(A + row * (static_cast<int64_t>(KT) * 128) + 16 * ci) = out;
+    }
+    if (blockIdx.y == 0)
+        for (int g = static_cast<int>(threadIdx.x); g < NG; g += 256)
+            as32[static_cast<int64_t>(g) * Ma + row] = bf16_bits_to_f32(a_scale[static_cast<int64_t>(g) * ld_as + row]);
+}
+
 template <int GMODE, bool SBF16, bool DUMP, bool SWIGLU>
 hipError_t launch_g(const PrefillParams& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
@@ -772,6 +966,136 @@ hipError_t launch(const PrefillParams& p, hipStream_t stream) {
 #endif
 
 int64_t prefill_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
+
+// The compat GEMM on gemm_prefill_kernel (group stride 128 * t, t >= 2, more
+// than kMidPrefillMinRows rows, and 64-row output tiles for at least half the
+// CUs: with fewer, the mid-group kernel's K split over waves is faster -- on
+// MI355X at 128 rows, qkv / o / down_proj 25.9 / 24.0 / 124 against 35.6 /
+// 33.0 / 149 us, gate_up 145 against 86 us; from 256 rows this path wins on
+// all four, 1.1-1.8x).  Workspace: the rebuilt activation rows,
+// then the fp32 activation scales, then (from W4A8_MID_TILED_MIN_ROWS rows)
+// the weight tiles repacked from w_q for this call, each 256-byte aligned.
+// Reading w_q as stored, a wave's 16-byte loads cover 32 columns' half lines
+// each, against one 1 KB tile for the repacked layout; the repack streams the
+// weights once more (2 N kpad / 2 bytes), which the larger calls repay.  0
+// where the shape takes the mid-group kernel (gemm_midgroup.hip) instead.
+// Tiled against stored weights, us (qkv / o / gate_up / down, repack
+// included): 1024 rows 69 / 61 / 472 / 277 against 72 / 58 / 455 / 277, 2048
+// rows 125 / 97 / 811 / 448 against 147 / 110 / 837 / 477, 4096 rows 216 /
+// 156 / 1441 / 729 against 248 / 175 / 1646 / 805.
+constexpr int64_t kMidPrefillMinRows = 64;
+#ifndef W4A8_MID_TILED_MIN_ROWS
+#define W4A8_MID_TILED_MIN_ROWS 2048
+#endif
+
+namespace {
+
+struct MidPrefillLayout {
+    int64_t a_off, as_off, wt_off, bytes;
+    bool tiled;
+};
+
+MidPrefillLayout mid_prefill_layout(int64_t Ma, int64_t N, int64_t K, int64_t group) {
+    MidPrefillLayout l{0, 0, 0, 0, false};
+    const int64_t gs = geom::group_stride(group);
+    if (Ma <= kMidPrefillMinRows || gs % 128 != 0 || gs < 256 || N <= 0 || K <= 0) return l;
+    if (geom::ceil_div(Ma, int64_t{64}) * geom::ceil_div(N, int64_t{kBN}) * 2 < device_cu_count()) return l;
+    const int64_t KT = geom::k_tiles(K, group), lda = KT * 128, kb = geom::kpad(K, group) / 2;
+    const int64_t ng = geom::num_groups(K, group);
+    const int64_t wt = geom::col_blocks(N) * KT * geom::kTileBytes;
+    const int64_t lim = int64_t{1} << 31;
+    // every buffer offset of the kernel, tile overhang included, below 2^31
+    if ((Ma + 128) * lda >= lim || (N + 128) * kb >= lim || ng * (N + 128) * 2 >= lim || ng * Ma * 4 >= lim ||
+        wt + 8 * geom::kTileBytes * KT >= lim)
+        return l;
+    l.tiled = Ma >= W4A8_MID_TILED_MIN_ROWS;
+    l.a_off = 0;
+    l.as_off = geom::ceil_to(Ma * lda, int64_t{256});
+    l.wt_off = geom::ceil_to(l.as_off + ng * Ma * 4, int64_t{256});
+    l.bytes = l.tiled ? l.wt_off + wt : l.as_off + ng * Ma * 4;
+    return l;
+}
+
+template <bool WT>
+void launch_mid_prefill(const PrefillParams& p, bool asym, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+    if (p.bm == 64) {
+        if (asym) gemm_prefill_kernel<3, kDW, true, false, false, 64, 2, WT><<<grid, dim3(threads_for<64>()), 0, stream>>>(p);
+        else gemm_prefill_kernel<3, kDW, true, false, false, 64, 1, WT><<<grid, dim3(threads_for<64>()), 0, stream>>>(p);
+    } else {
+        if (asym) gemm_prefill_kernel<3, kDW, true, false, false, 128, 2, WT><<<grid, dim3(threads_for<128>()), 0, stream>>>(p);
+        else gemm_prefill_kernel<3, kDW, true, false, false, 128, 1, WT><<<grid, dim3(threads_for<128>()), 0, stream>>>(p);
+    }
+}
+
+}  // namespace
+
+int64_t midgroup_prefill_workspace_bytes(int64_t Ma, int64_t N, int64_t K, int64_t group) {
+    return mid_prefill_layout(Ma, N, K, group).bytes;
+}
+
+hipError_t launch_gemm_midgroup_prefill(const MidgroupArgs& a, void* ws, int64_t ws_bytes, hipStream_t stream) {
+    const MidPrefillLayout l = mid_prefill_layout(a.Ma, a.N, a.K, a.group);
+    const int64_t ng = geom::num_groups(a.K, a.group);
+    if (l.bytes == 0 || ws == nullptr || ws_bytes < l.bytes || a.partials != nullptr ||
+        ng * a.ld_as * 4 >= (int64_t{1} << 31))
+        return hipErrorInvalidValue;
+    char* const w = static_cast<char*>(ws);
+    const int64_t KT = geom::k_tiles(a.K, a.group), lda = KT * 128;
+    PrefillParams p{};
+    p.A = reinterpret_cast<const int8_t*>(w + l.a_off);
+    p.lda = lda;
+    p.c_as = reinterpret_cast<const float*>(w + l.as_off);
+    p.c_ak = static_cast<const int32_t*>(a.a_ksum);
+    p.c_wz = static_cast<const uint16_t*>(a.w_zero);
+    p.ld_as = static_cast<int>(a.ld_as);
+    p.kb = static_cast<int>(geom::kpad(a.K, a.group) / 2);
+    p.W = l.tiled ? reinterpret_cast<const uint4*>(w + l.wt_off) : static_cast<const uint4*>(a.w_q);
+    p.S = static_cast<const uint16_t*>(a.w_scale);
+    p.Y = static_cast<uint16_t*>(a.y);
+    p.ldy = a.ldy;
+    p.M = static_cast<int>(a.Ma);
+    p.N = static_cast<int>(a.N);
+    p.K = static_cast<int>(a.K);
+    p.KT = static_cast<int>(KT);
+    p.NG = static_cast<int>(ng);
+    p.NB = static_cast<int>(geom::col_blocks(a.N));
+    p.gs = static_cast<int>(geom::group_stride(a.group));
+    p.kpad = static_cast<int>(geom::kpad(a.K, a.group));
+    p.tpg = p.gs / 128;
+    p.bm = prefill_tile_rows(a.Ma, a.N, a.group, false);
+    p.tiles_m = static_cast<int>(geom::ceil_div(a.Ma, int64_t{p.bm}));
+    p.tiles_n = static_cast<int>(geom::ceil_div(a.N, int64_t{kBN}));
+    p.band = 4;
+    p.a_bytes = static_cast<uint32_t>(a.Ma * lda);
+    p.w_bytes = static_cast<uint32_t>(l.tiled ? p.NB * KT * geom::kTileBytes : a.N * p.kb);
+    p.s_bytes = static_cast<uint32_t>(ng * a.N * 2);
+    p.as_bytes = static_cast<uint32_t>(ng * a.Ma * 4);
+    p.ak_bytes = static_cast<uint32_t>(ng * a.ld_as * 4);
+    p.vec_out = (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (a.ldy % 8 == 0);
+    p.splits = 1;
+    const dim3 agrid(static_cast<unsigned>(a.Ma), static_cast<unsigned>(geom::ceil_div(KT * 8, int64_t{256})));
+    const auto* hi = static_cast<const uint8_t*>(a.a_hi);
+    const auto* lo = static_cast<const uint8_t*>(a.a_lo);
+    const auto* as = static_cast<const uint16_t*>(a.a_scale);
+    auto* A = reinterpret_cast<int8_t*>(w + l.a_off);
+    auto* as32 = reinterpret_cast<float*>(w + l.as_off);
+    if (l.tiled) {
+        hipError_t e = launch_repack_weights(static_cast<const uint8_t*>(a.w_q), reinterpret_cast<uint8_t*>(w + l.wt_off),
+                                             a.N, a.K, a.group, stream);
+        if (e != hipSuccess) return e;
+        compat_act_kernel<true><<<agrid, dim3(256), 0, stream>>>(hi, lo, as, p.ld_as, p.kb, p.kpad, p.M, p.KT, p.NG, A,
+                                                                  as32);
+    } else {
+        compat_act_kernel<false><<<agrid, dim3(256), 0, stream>>>(hi, lo, as, p.ld_as, p.kb, p.kpad, p.M, p.KT, p.NG, A,
+                                                                   as32);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (l.tiled) launch_mid_prefill<true>(p, a.w_zero != nullptr, stream);
+    else launch_mid_prefill<false>(p, a.w_zero != nullptr, stream);
+    return hipGetLastError();
+}
 
 int prefill_tile_rows(int64_t M, int64_t N, int64_t group, bool swiglu) {
     const int64_t tn = swiglu ? geom::ceil_div(N / 2, kBN / 2) : geom::ceil_div(N, kBN);

@@ -15,6 +15,9 @@ hipError_t launch_quant_act(const uint16_t* x, int64_t ldx, int8_t* a_q, int64_t
 hipError_t launch_repack(const uint8_t* w_q, const uint16_t* w_scale, uint8_t* w_tiles,
                          uint16_t* s_tiles, int64_t N, int64_t K, int64_t group,
                          hipStream_t stream);
+// The weight tiles alone (the compat GEMM's prefill path repacks w_q per call).
+hipError_t launch_repack_weights(const uint8_t* w_q, uint8_t* w_tiles, int64_t N, int64_t K, int64_t group,
+                                 hipStream_t stream);
 
 // Problem description shared by the GEMM paths.
 struct GemmArgs {
@@ -127,6 +130,13 @@ struct MidgroupArgs {
 // shapes above 64 KiB).
 int64_t midgroup_lds_bytes(int64_t Ma, int64_t K, int64_t group);
 hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream);
+// The same GEMM at prefill sizes on gemm_prefill_kernel's LDS-tiled waves
+// (gemm_prefill.hip): the activation planes rebuilt into a workspace of
+// midgroup_prefill_workspace_bytes (0: the shape takes launch_gemm_midgroup;
+// no partial dump).  Outputs equal a one-wave-per-column-tile walk of
+// ReferenceMidGroupGemm's fold order.
+int64_t midgroup_prefill_workspace_bytes(int64_t Ma, int64_t N, int64_t K, int64_t group);
+hipError_t launch_gemm_midgroup_prefill(const MidgroupArgs& a, void* ws, int64_t ws_bytes, hipStream_t stream);
 
 // RMSNorm (+ optional residual add) fused with the per-token quant.
 struct RmsNormArgs {

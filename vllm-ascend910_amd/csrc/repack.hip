@@ -66,6 +66,17 @@ __global__ __launch_bounds__(256) void repack_scale_kernel(const uint16_t* __res
 
 }  // namespace
 
+hipError_t launch_repack_weights(const uint8_t* w_q, uint8_t* w_tiles, int64_t N, int64_t K, int64_t group,
+                                 hipStream_t stream) {
+    const int64_t kp = geom::kpad(K, group);
+    const int64_t KT = geom::k_tiles(K, group);
+    const int64_t wd = geom::col_blocks(N) * KT * 256;  // dwords
+    if (wd > 0)
+        repack_weight_kernel<<<dim3(static_cast<unsigned>((wd + 255) / 256)), dim3(256), 0, stream>>>(
+            w_q, reinterpret_cast<uint32_t*>(w_tiles), N, kp, KT, wd);
+    return hipGetLastError();
+}
+
 hipError_t launch_repack(const uint8_t* w_q, const uint16_t* w_scale, uint8_t* w_tiles,
                          uint16_t* s_tiles, int64_t N, int64_t K, int64_t group,
                          hipStream_t stream) {

@@ -579,12 +579,18 @@ def _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, 
     P = torch.empty((G, M, N), dtype=torch.int32, device=dev) if partials else None
     if M:
         # w_ksum is validated but not read: the activation bytes are rebuilt
-        # exactly from the two planes, so the kernel needs no +8 correction
-        _abi.check(_abi.lib().w4a8_midgroup_gemm(a_hi.data_ptr(), a_lo.data_ptr(), a_scale.data_ptr(),
-                                                 a_ksum.data_ptr(), M, a_scale.stride(0), w_q.data_ptr(),
-                                                 w_scale.data_ptr(), w_zero.data_ptr(), y.data_ptr(), N,
-                                                 P.data_ptr() if P is not None else None, N, K, group,
-                                                 _stream(dev)), "midgroup_w4a8_gemm")
+        # exactly from the two planes, so the kernel needs no +8 correction.
+        # Prefill sizes get a workspace for the rebuilt rows, allocated per
+        # call as the reference host allocates its GEMM workspace
+        # (npu_ops/host/midgroup_w4a8_gemm.cpp:116-118).
+        need = 0 if partials else _abi.lib().w4a8_midgroup_gemm_workspace_bytes(M, N, K, group)
+        ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+        _abi.check(_abi.lib().w4a8_midgroup_gemm_ws(a_hi.data_ptr(), a_lo.data_ptr(), a_scale.data_ptr(),
+                                                    a_ksum.data_ptr(), M, a_scale.stride(0), w_q.data_ptr(),
+                                                    w_scale.data_ptr(), w_zero.data_ptr(), y.data_ptr(), N,
+                                                    P.data_ptr() if P is not None else None, N, K, group,
+                                                    ws.data_ptr() if ws is not None else None, need,
+                                                    _stream(dev)), "midgroup_w4a8_gemm")
     return (y, P) if partials else y
 
 
