@@ -895,6 +895,12 @@ def compat(pkg, dev, synth, time_graph, T, cold_bytes):
     return rows
 
 
+def kernel_short_name(name):
+    """A kernel's unqualified name without template arguments ("(anonymous
+    namespace)" would otherwise end the name at its parenthesis)."""
+    return name.replace("(anonymous namespace)", "~").split("(")[0].split("<")[0].split("::")[-1].split()[-1]
+
+
 def trace_summary(db):
     """Per-kernel and per-dispatch-shape duration table of a rocprofv3
     --kernel-trace database (the rocpd ``kernels`` view)."""
@@ -905,7 +911,7 @@ def trace_summary(db):
     by_name, by_shape = collections.defaultdict(list), collections.defaultdict(list)
     by_stream = collections.defaultdict(list)
     for name, dur, gx, gy, wx, stream in rows:
-        short = name.split("(")[0].split("<")[0].split("::")[-1]
+        short = kernel_short_name(name)
         by_name[short].append(dur)
         by_shape[(short, gx, gy, wx)].append(dur)
         by_stream[(short, stream)].append(dur)
@@ -925,7 +931,7 @@ def trace_summary(db):
     # pmc_summary counts them).
     calls, total = collections.Counter(), collections.Counter()
     for name, dur, gx, gy, wx, stream in rows:
-        k = name.split("(")[0].split("<")[0].split("::")[-1]
+        k = kernel_short_name(name)
         is_call = k in ("gemm_decode_kernel", "gemm_wide_kernel") or (k == "gemm_prefill_cols_kernel" and gy > 1)
         if is_call:
             calls[stream] += 1
@@ -936,7 +942,7 @@ def trace_summary(db):
               f"wide_reduce_kernel) | {st} | {calls[st]} | {total[st] / calls[st] / 1e3:.3f} |")
     print("\n| kernel | grid x (threads) | grid y | workgroup | calls | avg us |\n|---|---:|---:|---:|---:|---:|")
     for (k, gx, gy, wx), d in sorted(by_shape.items()):
-        if k.startswith(("gemm_", "linear_", "quant_", "wide_")):
+        if k.startswith(("gemm_", "linear_", "quant_", "wide_", "compat_", "repack_")):
             print(f"| {k} | {gx} | {gy} | {wx} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} |")
 
 

@@ -225,7 +225,7 @@ def test_attention_rope_rejects_bad_arguments(lib):
 
 def test_midgroup_workspace_sizes_and_rejects(lib):
     """The compat GEMM's prefill path: its workspace query (rebuilt activation rows
-    [Ma, k_tiles * 128] and fp32 activation scales [G, Ma], then from 2048 rows the
+    [Ma, k_tiles * 128] and fp32 activation scales [G, Ma], then from 1024 rows the
     repacked weight tiles, each 256-byte aligned; 0 where the mid-group kernel runs) and
     the host checks of w4a8_midgroup_gemm_ws, before any launch.  Without a GPU the
     library takes 256 CUs."""
@@ -236,7 +236,8 @@ def test_midgroup_workspace_sizes_and_rejects(lib):
     assert q(4096, 7168, 5000, 1000) == tiled                    # stride 1024, ragged K
     assert q(100, 8192, 1057, 1024) == c256(100 * 1152) + 2 * 100 * 4
     assert q(65, 8200, 3456, 256) == c256(65 * 3456) + 14 * 65 * 4
-    assert q(1024, 7168, 5120, 1024) == c256(1024 * 5120) + 5 * 1024 * 4
+    assert q(1000, 7168, 5120, 1024) == c256(1000 * 5120) + 5 * 1000 * 4
+    assert q(1024, 7168, 5120, 1024) == c256(c256(1024 * 5120) + 5 * 1024 * 4) + 448 * 40 * 1024
     # the mid-group kernel keeps: up to 64 rows, 64-row tiles for fewer than half
     # the CUs, group stride 128 or not a multiple of 128, offsets past 2^31
     assert q(64, 7168, 5120, 1024) == 0

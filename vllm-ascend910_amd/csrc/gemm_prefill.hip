@@ -979,13 +979,13 @@ int64_t prefill_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; 
 // each, against one 1 KB tile for the repacked layout; the repack streams the
 // weights once more (2 N kpad / 2 bytes), which the larger calls repay.  0
 // where the shape takes the mid-group kernel (gemm_midgroup.hip) instead.
-// Tiled against stored weights, us (qkv / o / gate_up / down, repack
-// included): 1024 rows 69 / 61 / 472 / 277 against 72 / 58 / 455 / 277, 2048
-// rows 125 / 97 / 811 / 448 against 147 / 110 / 837 / 477, 4096 rows 216 /
-// 156 / 1441 / 729 against 248 / 175 / 1646 / 805.
+// Tiled against stored weights on MI355X, us (qkv / o / gate_up / down,
+// repack included; bench graph replays): 1024 rows 67 / 62 / 450 / 288
+// against 74 / 60 / 504 / 302; 4096 rows 218 / 158 / 1423 / 746 against 248 /
+// 175 / 1646 / 805 (at 512 rows the stored weights were ahead).
 constexpr int64_t kMidPrefillMinRows = 64;
 #ifndef W4A8_MID_TILED_MIN_ROWS
-#define W4A8_MID_TILED_MIN_ROWS 2048
+#define W4A8_MID_TILED_MIN_ROWS 1024
 #endif
 
 namespace {

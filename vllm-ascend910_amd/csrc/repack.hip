@@ -24,31 +24,45 @@
 namespace w4a8 {
 namespace {
 
-__global__ __launch_bounds__(256) void repack_weight_kernel(const uint8_t* __restrict__ wq,
-                                                             uint32_t* __restrict__ out,
-                                                             int64_t N, int64_t kpadv,
-                                                             int64_t KT, int64_t total_dwords) {
-    const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (o >= total_dwords) return;
-    const int64_t tile = o >> 8;
-    const int lane = static_cast<int>((o >> 2) & 63);
-    const int d = static_cast<int>(o & 3);
-    const int64_t nb = tile / KT;
-    const int64_t kt = tile - nb * KT;
-    const int64_t n = nb * 16 + (lane & 15);
-    const int64_t k0 = kt * 128 + (d >> 1) * 64 + (lane >> 4) * 16 + (d & 1) * 8;
-    uint32_t in = 0u;
-    if (n < N && k0 < kpadv) {
-        in = *reinterpret_cast<const uint32_t*>(wq + n * (kpadv / 2) + k0 / 2);
-    }
-    // in nibble i = code k0+i; out nibble 2j = code k0+j, out nibble 2j+1 = code k0+4+j.
+// One output nibble order per input dword: in nibble i = code k0+i; out
+// nibble 2j = code k0+j, out nibble 2j+1 = code k0+4+j.
+__device__ __forceinline__ uint32_t tile_dword(uint32_t in) {
     uint32_t r = 0u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         r |= ((in >> (4 * j)) & 0xfu) << (8 * j);
         r |= ((in >> (4 * (j + 4))) & 0xfu) << (8 * j + 4);
     }
-    out[o] = r;
+    return r;
+}
+
+// One thread per 16-byte lane chunk of a tile: its dwords d = 0, 1 are the
+// 8 bytes at K byte kt*64 + (l/16)*8 of column n's row, d = 2, 3 the 8 bytes
+// 32 further (16 codes each, inside or past kpad as a whole).
+__global__ __launch_bounds__(256) void repack_weight_kernel(const uint8_t* __restrict__ wq,
+                                                             uint4* __restrict__ out,
+                                                             int64_t N, int64_t kpadv,
+                                                             int64_t KT, int64_t total_chunks) {
+    const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= total_chunks) return;
+    const int64_t tile = o >> 6;
+    const int lane = static_cast<int>(o & 63);
+    const int64_t nb = tile / KT;
+    const int64_t kt = tile - nb * KT;
+    const int64_t n = nb * 16 + (lane & 15);
+    uint32_t in[4] = {0u, 0u, 0u, 0u};
+    if (n < N) {
+        const uint8_t* row = wq + n * (kpadv / 2);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t b = kt * 64 + h * 32 + (lane >> 4) * 8;
+            if (2 * b < kpadv) {   // dword loads: w_q is only required 4-byte aligned
+                in[2 * h] = *reinterpret_cast<const uint32_t*>(row + b);
+                in[2 * h + 1] = *reinterpret_cast<const uint32_t*>(row + b + 4);
+            }
+        }
+    }
+    out[o] = make_uint4(tile_dword(in[0]), tile_dword(in[1]), tile_dword(in[2]), tile_dword(in[3]));
 }
 
 __global__ __launch_bounds__(256) void repack_scale_kernel(const uint16_t* __restrict__ ws,
@@ -70,10 +84,10 @@ hipError_t launch_repack_weights(const uint8_t* w_q, uint8_t* w_tiles, int64_t N
                                  hipStream_t stream) {
     const int64_t kp = geom::kpad(K, group);
     const int64_t KT = geom::k_tiles(K, group);
-    const int64_t wd = geom::col_blocks(N) * KT * 256;  // dwords
-    if (wd > 0)
-        repack_weight_kernel<<<dim3(static_cast<unsigned>((wd + 255) / 256)), dim3(256), 0, stream>>>(
-            w_q, reinterpret_cast<uint32_t*>(w_tiles), N, kp, KT, wd);
+    const int64_t wc = geom::col_blocks(N) * KT * 64;  // 16-byte lane chunks
+    if (wc > 0)
+        repack_weight_kernel<<<dim3(static_cast<unsigned>((wc + 255) / 256)), dim3(256), 0, stream>>>(
+            w_q, reinterpret_cast<uint4*>(w_tiles), N, kp, KT, wc);
     return hipGetLastError();
 }
 
@@ -84,11 +98,11 @@ hipError_t launch_repack(const uint8_t* w_q, const uint16_t* w_scale, uint8_t* w
     const int64_t NB = geom::col_blocks(N);
     const int64_t KT = geom::k_tiles(K, group);
     const int64_t G = geom::num_groups(K, group);
-    const int64_t wd = NB * KT * 256;  // dwords
-    if (wd > 0) {
-        const int64_t blocks = (wd + 255) / 256;
+    const int64_t wc = NB * KT * 64;  // 16-byte lane chunks
+    if (wc > 0) {
+        const int64_t blocks = (wc + 255) / 256;
         repack_weight_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
-            w_q, reinterpret_cast<uint32_t*>(w_tiles), N, kp, KT, wd);
+            w_q, reinterpret_cast<uint4*>(w_tiles), N, kp, KT, wc);
     }
     const int64_t sn = NB * G * 16;
     if (sn > 0) {
