@@ -1237,6 +1237,22 @@ def test_midgroup_prefill_qwq_shapes(pkg, dev, proj, M):
     assert np.array_equal(got, want), f"{proj}: {int((got != want).sum())} of {got.size} sampled outputs differ"
 
 
+@pytest.mark.parametrize("M", [1, 5, 16, 40])
+def test_midgroup_gemm_real_rows_equal_padded_rows(pkg, dev, M):
+    """rows=M computes only the real rows of quant_a's padded planes: the same bits as the
+    padded product's first M rows (the plan does not depend on the row count up to 64)."""
+    say(f"midgroup rows={M}")
+    K, N, G = 5120, 7168, 1024
+    _, _, _, _, a, args = _midgroup_inputs(pkg, dev, M, N, K, G, True, seed=21 + M)
+    y_pad = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G)
+    y = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G, M)
+    torch.cuda.synchronize()
+    assert y.shape == (M, N) and y_pad.shape[0] >= M
+    assert torch.equal(y.view(torch.int16), y_pad[:M].view(torch.int16))
+    with pytest.raises(RuntimeError, match="exceeds"):
+        torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G, y_pad.shape[0] + 1)
+
+
 def test_midgroup_prefill_path_without_zero_points(pkg, dev):
     """The C ABI's symmetric call (w_zero NULL: the variant without the zero-point term)
     equals the call with an all-zero w_zero, through w4a8_midgroup_gemm_ws."""

@@ -115,8 +115,9 @@ def midgroup_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wk: tor
     lead, K = x.shape[:-1], x.shape[-1]
     x2 = x.reshape(-1, K).to(torch.bfloat16).contiguous()
     a_hi, a_lo, a_scale, a_ksum = torch.ops.npu.midgroup_quant_a(x2, group)
-    y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, wq, ws, wk, wz, K, group)
-    return y[:x2.shape[0]].reshape(*lead, y.shape[-1])
+    # only the real rows (the reference slices them from the padded product)
+    y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, wq, ws, wk, wz, K, group, x2.shape[0])
+    return y.reshape(*lead, y.shape[-1])
 
 
 class MidGroupW4A8Linear(nn.Module):
@@ -171,8 +172,7 @@ class MidGroupW4A8Linear(nn.Module):
         rows = x2.shape[0]
         a_hi, a_lo, a_scale, a_ksum = torch.ops.npu.midgroup_quant_a(x2, self.group)
         y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, self.weight_packed, ws, wk, wz, k,
-                                             self.group)
-        y = y[:rows]
+                                             self.group, rows)
         if self.bias is not None:
             y = y + self.bias
         return y.reshape(*lead, self.out_features)

@@ -26,7 +26,7 @@ reference's fixed value as default), its mid-group compat pair:
 
     torch.ops.npu.midgroup_quant_a(x, group=1024) -> [a_hi, a_lo, a_scale, a_ksum]
     torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero,
-                                     K, group=1024) -> y
+                                     K, group=1024, rows=-1) -> y   (rows >= 0: only the first rows)
     torch.ops.npu.midgroup_w4a8_gemm_partials(...) -> (y, partials)   (parity hook)
 
 Only the CUDA (= HIP on ROCm) dispatch key and fake (meta) kernels are
@@ -66,7 +66,7 @@ _LIB.define("w4a8_attention_rope(Tensor qkv, Tensor cos, Tensor sin, Tensor pos,
             "float? scale=None) -> Tensor")
 _LIB.define("midgroup_quant_a(Tensor x, int group=1024) -> Tensor[]")
 _LIB.define("midgroup_w4a8_gemm(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
-            "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> Tensor")
+            "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024, int rows=-1) -> Tensor")
 _LIB.define("midgroup_w4a8_gemm_partials(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
             "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> (Tensor, Tensor)")
 
@@ -569,8 +569,14 @@ def _check_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K
     return M, N, G
 
 
-def _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, partials: bool):
+def _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, partials: bool,
+                  rows: int = -1):
     M, N, G = _check_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group)
+    if rows >= 0:
+        # the first `rows` rows only (the real rows before quant_a's padding):
+        # the padding rows' activation planes are then never read
+        _require(rows <= M, f"midgroup_w4a8_gemm: rows={rows} exceeds the {M} activation rows")
+        M = rows
     a_hi, a_lo, w_q = a_hi.contiguous(), a_lo.contiguous(), w_q.contiguous()
     a_scale, a_ksum = a_scale.contiguous(), a_ksum.contiguous()
     w_scale, w_zero = w_scale.contiguous(), w_zero.contiguous()
@@ -595,15 +601,18 @@ def _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, 
 
 
 @torch.library.impl(_LIB, "midgroup_w4a8_gemm", "CUDA")
-def _midgroup_gemm_cuda(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K: int, group: int = 1024):
+def _midgroup_gemm_cuda(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K: int, group: int = 1024,
+                        rows: int = -1):
     """The reference's run_midgroup_w4a8_gemm (npu_ops/host/midgroup_w4a8_gemm.cpp:45-140): y bf16
-    [a_hi rows, N]; callers slice back to their real rows, as with the reference."""
-    return _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, False)
+    [a_hi rows, N]; callers slice back to their real rows, as with the reference.  ``rows`` >= 0
+    computes and returns only the first ``rows`` rows (the same values): callers that know their
+    real row count (``midgroup_linear``, ``MidGroupW4A8Linear``, the vLLM method) skip the padding."""
+    return _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, False, rows)
 
 
 @torch.library.register_fake("npu::midgroup_w4a8_gemm")
-def _midgroup_gemm_fake(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group=1024):
-    return a_scale.new_empty((a_hi.shape[0], w_q.shape[0]), dtype=torch.bfloat16)
+def _midgroup_gemm_fake(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group=1024, rows=-1):
+    return a_scale.new_empty((a_hi.shape[0] if rows < 0 else rows, w_q.shape[0]), dtype=torch.bfloat16)
 
 
 @torch.library.impl(_LIB, "midgroup_w4a8_gemm_partials", "CUDA")

@@ -187,8 +187,7 @@ class MidGroupW4A8LinearMethod(LinearMethodBase):
         rows = x2.shape[0]
         a_hi, a_lo, a_scale, a_ksum = torch.ops.npu.midgroup_quant_a(x2, layer.w4a8_group)
         y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, layer.weight_packed, layer.weight_scale,
-                                             layer.weight_ksum, layer.weight_zero, k, layer.w4a8_group)
-        y = y[:rows]
+                                             layer.weight_ksum, layer.weight_zero, k, layer.w4a8_group, rows)
         if bias is not None:
             y = y + bias
         return y.reshape(*lead, layer.w4a8_n)
