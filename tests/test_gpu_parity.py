@@ -1237,6 +1237,29 @@ def test_midgroup_prefill_qwq_shapes(pkg, dev, proj, M):
     assert np.array_equal(got, want), f"{proj}: {int((got != want).sum())} of {got.size} sampled outputs differ"
 
 
+@pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_midgroup_decode_reference_order(pkg, dev, proj, M):
+    """Decode rows at group 1024: the K split over waves adds exact int32 group sums and folds
+    once in group order (or one wave walks every group), so the output is bf16 of the
+    reference's fp32 result bit for bit -- except where 64-row tiles' sums of many groups
+    exceed LDS (down_proj past 16 rows: the waves' fp32 sums are added, within the bar)."""
+    K, N = pkg.synth.QWQ_SHAPES[proj]
+    say(f"midgroup decode order {proj} M={M}")
+    xb, codes, sc, zr, a, args = _midgroup_inputs(pkg, dev, M, N, K, 1024, True, seed=31 + M)
+    y = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, 1024, M)
+    torch.cuda.synchronize()
+    q, _ = ow.quant_act_midgroup(xb, 1024)
+    y32 = ow.gemm_midgroup_fp32(q, tensor_bf16_bits(a[2])[:, :M], codes, sc, zr, 1024)
+    got = tensor_bf16_bits(y)
+    if proj == "down_proj" and M > 16:
+        check_output(got, y32, f"midgroup decode {proj} M{M}",
+                     exact_mid(q, tensor_bf16_bits(a[2]), codes, sc, zr, 1024))
+    else:
+        want = ow.f32_to_bf16_bits(y32)
+        assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} outputs differ"
+
+
 @pytest.mark.parametrize("M", [1, 5, 16, 40])
 def test_midgroup_gemm_real_rows_equal_padded_rows(pkg, dev, M):
     """rows=M computes only the real rows of quant_a's padded planes: the same bits as the

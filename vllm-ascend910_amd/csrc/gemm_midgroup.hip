@@ -42,6 +42,11 @@ namespace {
 
 constexpr uint32_t kOOBm = 0x80000000u;
 constexpr size_t kMidLdsLimit = 64 * 1024;
+// The int32 group sums of the tile-granular K split may take the workgroup's
+// LDS past the 64 KiB a launch gets by default (down_proj at one 16-row tile:
+// 27 groups of 16 x 32 sums), up to this much (the attribute is set once per
+// kernel).
+constexpr size_t kMidLdsIsum = 128 * 1024;
 
 struct MidParams {
     const uint8_t* a_hi;
@@ -59,6 +64,7 @@ struct MidParams {
     int kpad, KT, NG, NB;
     int tpg;                   // 128-K tiles per group stride
     uint32_t a_bytes, w_bytes;
+    bool isum;                 // K split over waves at tile granularity, int32 group sums in LDS
 };
 
 template <int MT, int CPW, int KWMAX, int D, bool ASYM, bool DUMP>
@@ -67,7 +73,8 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
     constexpr int C = 16 * CPW;
     extern __shared__ float smem[];
     // [NG][R] activation scales (fp32), [NG][R] ksums, [NG][C] weight scales,
-    // [NG][C] zero points, then the K-split reduction buffer [kw][R][C].
+    // [NG][C] zero points, then the K-split reduction buffer: [kw][R][C] fp32
+    // wave sums, or with p.isum the int32 group sums [NG][R][C].
     float* s_as = smem;
     int* s_ak = reinterpret_cast<int*>(s_as + p.NG * R);
     float* s_ws = reinterpret_cast<float*>(s_ak + p.NG * R);
@@ -99,10 +106,15 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
     }
 
     // This wave's tile range, in whole groups.
+    // p.isum: an even share of the K tiles, groups split between waves
+    // meeting in the int32 sums; otherwise whole groups.
     const int ua = (wave * p.NG) / kw;
     const int ub = ((wave + 1) * p.NG) / kw;
-    const int ta = ua * p.tpg;
-    const int tb = min(p.KT, ub * p.tpg);
+    const int ta = p.isum ? (wave * p.KT) / kw : ua * p.tpg;
+    const int tb = p.isum ? ((wave + 1) * p.KT) / kw : min(p.KT, ub * p.tpg);
+    int* const isum = reinterpret_cast<int*>(red);
+    if (p.isum)
+        for (int e = threadIdx.x; e < p.NG * R * C; e += blockDim.x) isum[e] = 0;
 
     uint32_t wo[CPW], ao[MT];
 #pragma unroll
@@ -147,6 +159,19 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
         }
     __syncthreads();   // LDS scales staged
 
+    // p.isum: this wave's int32 sum of group g (sum A*W, exact) into the
+    // group's LDS sums; the fold happens once every wave has added its share.
+    auto flush = [&](int g) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < CPW; ++c)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    atomicAdd(&isum[(g * R + mt * 16 + rowq + i) * C + c * 16 + colq], P[mt][c][i] >> 4);
+                P[mt][c] = v4i{0, 0, 0, 0};
+            }
+    };
     auto fold = [&](int g, bool own) __attribute__((always_inline)) {
         // the reference's separate roundings: no multiply-add contraction
 #pragma clang fp contract(off)
@@ -207,9 +232,35 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                         for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(av[mt][h], bw[c][h], P[mt][c]);
-                if ((t + 1) % p.tpg == 0 || t == p.KT - 1) fold(t / p.tpg, true);
+                if (p.isum) {
+                    if ((t + 1) % p.tpg == 0 || t == p.KT - 1 || t == tb - 1) flush(t / p.tpg);
+                } else if ((t + 1) % p.tpg == 0 || t == p.KT - 1) {
+                    fold(t / p.tpg, true);
+                }
             }
         }
+    }
+
+    if (p.isum) {
+        // every group's int32 sum complete: the fold in group order, one
+        // output element per thread and step
+#pragma clang fp contract(off)
+        __syncthreads();
+        for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
+            const int r = e / C, cc = e - r * C;
+            const int row = m0 + r;
+            const int col = nb0 * 16 + cc;
+            if (row >= p.Ma || col >= p.N) continue;
+            float a = 0.0f;
+            for (int g = 0; g < p.NG; ++g) {
+                const int I = isum[(g * R + r) * C + cc] + (ASYM ? static_cast<int>(s_wz[g * C + cc]) * s_ak[g * R + r] : 0);
+                if constexpr (DUMP) p.P[(static_cast<int64_t>(g) * p.Ma + row) * p.N + col] = I;
+                const float t1 = static_cast<float>(I) * s_ws[g * C + cc];
+                a = a + t1 * s_as[g * R + r];
+            }
+            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(a));
+        }
+        return;
     }
 
     // Fixed-order reduction of the kw wave partials.
@@ -423,18 +474,46 @@ constexpr int mid_depth(int mt) { return mt == 1 ? 4 : 2; }
 constexpr int kwmax_mid(int mt, int cpw) { return mt == 1 ? 12 : cpw > 2 ? 4 : 8; }
 
 template <int MT, int CPW, bool ASYM, bool DUMP>
-hipError_t launch_mid(const MidParams& p, int kw, hipStream_t stream) {
+hipError_t launch_mid(const MidParams& p0, int kw, hipStream_t stream) {
     constexpr int D = mid_depth(MT), KWM = kwmax_mid(MT, CPW);
+    MidParams p = p0;
+    p.isum = false;
     // dynamic LDS stays within the 64 KiB a launch gets without a function
     // attribute: the staged scales, then as many reduction slices as fit
     const size_t staged = static_cast<size_t>(p.NG) * (2 * 16 * MT + 2 * 16 * CPW) * sizeof(float);
     const size_t slice = static_cast<size_t>(16 * MT) * 16 * CPW * sizeof(float);
+    const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW), static_cast<unsigned>((p.Ma + 16 * MT - 1) / (16 * MT)));
+    const int64_t wgs = static_cast<int64_t>(grid.x) * grid.y;
+    // Few workgroups: K split over waves, every wave adding its exact int32
+    // group sums in LDS, then one fold in group order -- the reference's fp32
+    // order, bit for bit, whatever the split (the fp32 sums of whole-group
+    // waves, added across waves, had put two down_proj outputs at 64 rows
+    // outside 1 bf16 ulp of the float64 value).  Tile granularity (about four
+    // tiles a wave) except on 9-16-row tiles, where whole groups per wave are
+    // faster (MI355X, qkv / o us, tiles against groups: 1 row 8.8 / 8.5 against
+    // 9.7 / 9.5, 16 rows 11.9 / 11.6 against 11.4 / 11.1, 64 rows 21.5 / 20.8
+    // against 22.5 / 21.9).
+    if (wgs < 512 && staged + p.NG * slice <= kMidLdsIsum) {
+        int w = MT == 1 && p.Ma > 8 ? std::min(p.NG, (p.NG + 1) / 2) : std::max(1, (p.KT + 3) / 4);
+        w = std::min(KWM, w);
+        if (CPW > 2) w = std::min(w, wgs >= 256 ? 2 : 4);
+        if (w > 1) {
+            p.isum = true;
+            const size_t lds = staged + p.NG * slice;
+            if (lds > kMidLdsLimit) {
+                static const hipError_t attr = hipFuncSetAttribute(
+                    reinterpret_cast<const void*>(&gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP>),
+                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMidLdsIsum));
+                if (attr != hipSuccess) return attr;
+            }
+            gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP><<<grid, dim3(64 * w), lds, stream>>>(p);
+            return hipGetLastError();
+        }
+    }
     if (staged + slice > kMidLdsLimit) return hipErrorInvalidValue;
     const int wfit = static_cast<int>((kMidLdsLimit - staged) / slice);
-    const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW), static_cast<unsigned>((p.Ma + 16 * MT - 1) / (16 * MT)));
     if (CPW > 2) {
         // prefill: split K over waves only while the grid is small
-        const int64_t wgs = static_cast<int64_t>(grid.x) * grid.y;
         kw = std::min(kw, wgs >= 1024 ? 1 : wgs >= 256 ? 2 : 4);
     }
     const int w = std::max(1, std::min({kw, KWM, p.NG, wfit}));
@@ -465,11 +544,25 @@ hipError_t launch_shared(const MidParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// The int32 group sums of an MT x CPW tile fit the LDS beside the staged scales.
+bool mid_isum_fits(const MidParams& p, int mt, int cpw) {
+    return static_cast<size_t>(p.NG) * (2 * 16 * mt + 2 * 16 * cpw + 16 * mt * 16 * cpw) * sizeof(float) <= kMidLdsIsum;
+}
+
 template <bool ASYM, bool DUMP>
 hipError_t launch_mt(const MidParams& p, int kw, hipStream_t stream) {
     if (mid_shared_fits(p)) return launch_shared<ASYM, DUMP>(p, stream);
     if (p.Ma <= 16) return launch_mid<1, 2, ASYM, DUMP>(p, kw, stream);
-    if (p.Ma <= 64 || !mid_wide_fits(p)) return launch_mid<4, 2, ASYM, DUMP>(p, kw, stream);
+    if (p.Ma <= 64 || !mid_wide_fits(p)) {
+        // 64-row tiles whose group sums exceed the LDS (many groups: down_proj's
+        // 27 at group 1024) take 32-row tiles, whose sums fit, where the K
+        // split over waves applies (few workgroups): the exact fold order at
+        // the cost of reading the weights once per 32 rows
+        const int64_t nb2 = (p.NB + 1) / 2;
+        if (!mid_isum_fits(p, 4, 2) && mid_isum_fits(p, 2, 2) && nb2 * ((p.Ma + 31) / 32) < 512)
+            return launch_mid<2, 2, ASYM, DUMP>(p, kw, stream);
+        return launch_mid<4, 2, ASYM, DUMP>(p, kw, stream);
+    }
     return launch_mid<4, 4, ASYM, DUMP>(p, kw, stream);
 }
 
