@@ -861,6 +861,7 @@ def compat(pkg, dev, synth, time_graph, T, cold_bytes):
             wz = torch.randint(-8, 8, (ng, N), device=dev, generator=gen).to(torch.bfloat16)
             wk = torch.zeros((ng, N), dtype=torch.int32, device=dev)
             pool.append((w_q, ws, wk, wz))
+        tiles = [torch.ops.npu.midgroup_tile_weights(w[0], K, G) for w in pool]
         for M in (1, 16, 64, 1024, 4096):
             x = torch.from_numpy(synth.activations(M, K, seed=M).view(np.int16)).view(torch.bfloat16).to(dev)
             a = torch.ops.npu.midgroup_quant_a(x, G)
@@ -878,16 +879,23 @@ def compat(pkg, dev, synth, time_graph, T, cold_bytes):
                 for i in range(n):
                     torch.ops.npu.midgroup_w4a8_gemm(*a, *pool[i % len(pool)], K, G, M)
 
+            def gemms_tiled(a=a, K=K, N=N, n=n, M=M):
+                for i in range(n):
+                    w_q, ws, wk, wz = pool[i % len(pool)]
+                    torch.ops.npu.midgroup_w4a8_gemm_tiled(*a, tiles[i % len(pool)], ws, wk, wz, N, K, G, M)
+
             us, qus = time_graph(gemms) / n, time_graph(quants) / n
             Mp = a[0].shape[0]
             # the real rows only (midgroup_linear / the vLLM method), where quant_a padded them
             rus = time_graph(gemms_rows) / n if Mp > M else us
+            # the weight as 1 KB tiles made once at load (the vLLM method's and MidGroupW4A8Linear's layout)
+            tus = time_graph(gemms_tiled) / n
             b = N * kb + ng * N * 6 + Mp * kb * 2 + ng * Mp * 6 + 2 * Mp * N
             tops = 2 * M * N * K / us / 1e6
             row = {"proj": p, "M": M, "gemm_us": round(us, 2), "GBs": round(b / us / 1e3, 1),
                    "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "TOPS": round(tops, 1),
                    "mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "quant_a_us": round(qus, 2),
-                   "gemm_real_rows_us": round(rus, 2)}
+                   "gemm_real_rows_us": round(rus, 2), "gemm_tiled_rows_us": round(tus, 2)}
             if (p, M) in REF_MIDGROUP_US:
                 ref_us, line = REF_MIDGROUP_US[(p, M)]
                 row.update(reference_910b4_us=ref_us,
@@ -896,9 +904,9 @@ def compat(pkg, dev, synth, time_graph, T, cold_bytes):
             rows.append(row)
             log(f"  compat {p:13s} M={M:5d}: gemm {us:9.2f} us {b / us / 1e3:7.1f} GB/s "
                 f"({b / us / 1e3 / HBM_PEAK_GBS:.1%}) {tops:7.1f} TOPS  quant_a {qus:7.2f} us"
-                f"  real rows {rus:9.2f} us")
+                f"  real rows {rus:9.2f} us  tiled {tus:9.2f} us")
             del x, a
-        del pool
+        del pool, tiles
         torch.cuda.empty_cache()
     return rows
 

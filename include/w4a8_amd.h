@@ -48,7 +48,9 @@ enum w4a8_dtype { W4A8_DT_F16 = 0, W4A8_DT_BF16 = 1 };
  * first build whose GEMM asks a workspace of some decode shapes; 5 adds
  * w4a8_rope_kv; 6 adds w4a8_stream_capture_id and requires 4-byte aligned
  * s_tiles; 7 adds w4a8_attention and its two size queries; 8 adds
- * w4a8_attention_rope; 9 adds w4a8_midgroup_gemm_ws and its size query). */
+ * w4a8_attention_rope; 9 adds w4a8_midgroup_gemm_ws and its size query; 10
+ * adds w4a8_midgroup_tile_weights, w4a8_midgroup_tiles_bytes and
+ * w4a8_midgroup_gemm_tiled). */
 int w4a8_abi_version(void);
 
 /* Message for the calling thread's last failed call ("" if none). */
@@ -393,6 +395,26 @@ int w4a8_midgroup_gemm_ws(const void* a_hi, const void* a_lo, const void* a_scal
                           int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero, void* y,
                           int64_t ldy, void* partials, int64_t N, int64_t K, int64_t group, void* workspace,
                           int64_t workspace_bytes, void* stream);
+
+/*
+ * The compat GEMM on a weight reordered once at load time.  The reference
+ * reads w_q [N, kpad/2] as stored on every call (its op takes it so,
+ * npu_ops/host/midgroup_w4a8_gemm.cpp:45-140); its vLLM method converts
+ * checkpoint tensors once after loading (npu_ops/python/midgroup_quant.py:148-161),
+ * and at that point w4a8_midgroup_tile_weights writes the same bytes into
+ * 1 KB tiles of w4a8_midgroup_tiles_bytes(N, K, group) bytes,
+ *   w_tiles[nb][kt][q][c][0..15] = w_q[16 nb + c][64 kt + 16 q .. +15]
+ * (zero past N and past kpad/2), which every compat kernel reads in whole
+ * tiles.  w4a8_midgroup_gemm_tiled takes w_tiles in place of w_q, otherwise
+ * as w4a8_midgroup_gemm_ws (the same workspace query, an upper bound here:
+ * no per-call repack), with the same outputs bit for bit.
+ */
+int64_t w4a8_midgroup_tiles_bytes(int64_t N, int64_t K, int64_t group);
+int w4a8_midgroup_tile_weights(const void* w_q, void* w_tiles, int64_t N, int64_t K, int64_t group, void* stream);
+int w4a8_midgroup_gemm_tiled(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
+                             int64_t ld_as, const void* w_tiles, const void* w_scale, const void* w_zero, void* y,
+                             int64_t ldy, void* partials, int64_t N, int64_t K, int64_t group, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported(pkg, lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.w4a8_abi_version() == 9
+    assert lib.w4a8_abi_version() == 10
     # 16-column x 128-K tiles of 1 KB; scales [ceil(N/16), G, 16] x 2 bytes
     assert lib.w4a8_repacked_weight_bytes(5120, 5120, 128) == 320 * 40 * 1024
     assert lib.w4a8_repacked_weight_bytes(100, 512, 64) == 7 * 4 * 1024

@@ -1260,6 +1260,40 @@ def test_midgroup_decode_reference_order(pkg, dev, proj, M):
         assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} outputs differ"
 
 
+def _tiles_ref(w_q: np.ndarray, KT: int) -> np.ndarray:
+    """midgroup_tile_weights' layout built on the CPU: tiles[nb][kt][q][c][16 bytes] =
+    w_q[16 nb + c][64 kt + 16 q .. +15], zero past N and past the row."""
+    N, kb = w_q.shape
+    NB = -(-N // 16)
+    pad = np.zeros((NB * 16, KT * 64), np.int8)
+    pad[:N, :kb] = w_q
+    return pad.reshape(NB, 16, KT, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+@pytest.mark.parametrize("M,N,K,G", [
+    (1, 7168, 5120, 1024),      # per-wave kernel, int32 group sums
+    (16, 1000, 1057, 1024),     # ragged K (a half-padding last tile), N not a multiple of 16
+    (1, 16400, 1057, 1024),     # shared-activation kernel on wide N
+    (64, 5120, 27648, 1024),    # 32-row tiles (27 groups of sums)
+    (48, 2064, 3456, 256),      # 64-row tiles, stride 256
+    (300, 8200, 5120, 1024),    # prefill path on the tiles
+    (2048, 1000, 1057, 1024),   # prefill path (the stored rows would be repacked per call)
+])
+def test_midgroup_tiled_weights_equal_stored_rows(pkg, dev, M, N, K, G):
+    """midgroup_tile_weights equals its CPU construction byte for byte, and the GEMM on the
+    tiles returns the bits of the GEMM on the rows as stored, on every compat path."""
+    say(f"midgroup tiles M={M} N={N} K={K} G={G}")
+    _, _, _, _, a, args = _midgroup_inputs(pkg, dev, M, N, K, G, True, seed=41 + M)
+    w_q = args[0]
+    tiles = torch.ops.npu.midgroup_tile_weights(w_q, K, G)
+    KT = -(-pkg.geometry.kpad(K, G) // 128)
+    assert np.array_equal(tiles.cpu().numpy(), _tiles_ref(w_q.cpu().numpy(), KT))
+    y = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G, M)
+    yt = torch.ops.npu.midgroup_w4a8_gemm_tiled(*a, tiles, *args[1:], N, K, G, M)
+    torch.cuda.synchronize()
+    assert torch.equal(yt.view(torch.int16), y.view(torch.int16))
+
+
 @pytest.mark.parametrize("M", [1, 5, 16, 40])
 def test_midgroup_gemm_real_rows_equal_padded_rows(pkg, dev, M):
     """rows=M computes only the real rows of quant_a's padded planes: the same bits as the

@@ -15,7 +15,7 @@ from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "_lib" / "libw4a8_amd.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 W4A8_DT_F16 = 0
 W4A8_DT_BF16 = 1
@@ -43,6 +43,10 @@ SIGNATURES = {
     "w4a8_midgroup_gemm": (_I, [_VP, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
                                 _VP]),
     "w4a8_midgroup_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "w4a8_midgroup_tiles_bytes": (_I64, [_I64, _I64, _I64]),
+    "w4a8_midgroup_tile_weights": (_I, [_VP, _VP, _I64, _I64, _I64, _VP]),
+    "w4a8_midgroup_gemm_tiled": (_I, [_VP, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
+                                      _VP, _I64, _VP]),
     "w4a8_midgroup_gemm_ws": (_I, [_VP, _VP, _VP, _VP, _I64, _I64, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
                                    _VP, _I64, _VP]),
     "w4a8_rmsnorm_quant": (_I, [_VP, _I64, _VP, _I64, _VP, ctypes.c_float, _VP, _I64, _VP, _I64, _VP, _I64, _VP,

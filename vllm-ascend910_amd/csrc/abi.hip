@@ -209,7 +209,7 @@ using namespace w4a8;
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 9; }
+int w4a8_abi_version(void) { return 10; }
 
 const char* w4a8_last_error(void) { return g_last_error.c_str(); }
 
@@ -397,7 +397,7 @@ int w4a8_midgroup_quant_a(const void* x, int64_t ldx, void* a_hi, void* a_lo, vo
 static int midgroup_gemm_impl(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum,
                               int64_t Ma, int64_t ld_as, const void* w_q, const void* w_scale, const void* w_zero,
                               void* y, int64_t ldy, void* partials, int64_t N, int64_t K, int64_t group,
-                              void* workspace, int64_t workspace_bytes, void* stream) {
+                              void* workspace, int64_t workspace_bytes, void* stream, bool w_tiles = false) {
     if (int rc = check_problem(Ma, N, K, group)) return rc;
     if (geom::group_stride(group) % 128 != 0)
         return fail(W4A8_ERR_UNSUPPORTED, "group=%lld: the mid-group path needs ceil_to(group, 64) %% 128 == 0",
@@ -411,7 +411,8 @@ static int midgroup_gemm_impl(const void* a_hi, const void* a_lo, const void* a_
         (partials && !aligned(partials, 4)))
         return fail(W4A8_ERR_ALIGN, "planes and w_q 16-byte aligned; scales 2-, ksum and partials 4-byte aligned");
     const int64_t kb = geom::kpad(K, group) / 2;
-    if ((Ma + 16) * kb >= (1ll << 31) || (N + 16) * kb >= (1ll << 31))
+    if ((Ma + 16) * kb >= (1ll << 31) || (N + 16) * kb >= (1ll << 31) ||
+        (w_tiles && midgroup_tiles_bytes(N + 128, K, group) >= (1ll << 31)))
         return fail(W4A8_ERR_UNSUPPORTED, "operands too large for 32-bit offsets (%lld rows, N=%lld, %lld B/row)", Ma,
                     N, kb);
     // Prefill sizes with a workspace: the LDS-tiled prefill waves (no partial
@@ -444,6 +445,7 @@ static int midgroup_gemm_impl(const void* a_hi, const void* a_lo, const void* a_
     a.N = N;
     a.K = K;
     a.group = group;
+    a.w_tiles = w_tiles;
     if (prefill)
         return hip_status(launch_gemm_midgroup_prefill(a, workspace, workspace_bytes, static_cast<hipStream_t>(stream)),
                           "w4a8_midgroup_gemm_ws launch");
@@ -460,6 +462,28 @@ int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, 
 int64_t w4a8_midgroup_gemm_workspace_bytes(int64_t Ma, int64_t N, int64_t K, int64_t group) {
     if (Ma < 0 || N <= 0 || K <= 0 || group <= 0) return 0;
     return midgroup_prefill_workspace_bytes(Ma, N, K, group);
+}
+
+int64_t w4a8_midgroup_tiles_bytes(int64_t N, int64_t K, int64_t group) {
+    if (N <= 0 || K <= 0 || group <= 0) return -1;
+    return midgroup_tiles_bytes(N, K, group);
+}
+
+int w4a8_midgroup_tile_weights(const void* w_q, void* w_tiles, int64_t N, int64_t K, int64_t group, void* stream) {
+    if (int rc = check_problem(1, N, K, group)) return rc;
+    if (!w_q || !w_tiles) return fail(W4A8_ERR_NULL, "w_q and w_tiles must not be NULL");
+    if (!aligned(w_q, 16) || !aligned(w_tiles, 16)) return fail(W4A8_ERR_ALIGN, "w_q and w_tiles 16-byte aligned");
+    return hip_status(launch_midgroup_tile(w_q, w_tiles, N, K, group, static_cast<hipStream_t>(stream)),
+                      "w4a8_midgroup_tile_weights launch");
+}
+
+int w4a8_midgroup_gemm_tiled(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,
+                             int64_t ld_as, const void* w_tiles, const void* w_scale, const void* w_zero, void* y,
+                             int64_t ldy, void* partials, int64_t N, int64_t K, int64_t group, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+    if (workspace_bytes < 0) return fail(W4A8_ERR_WORKSPACE, "workspace_bytes=%lld < 0", workspace_bytes);
+    return midgroup_gemm_impl(a_hi, a_lo, a_scale, a_ksum, Ma, ld_as, w_tiles, w_scale, w_zero, y, ldy, partials, N,
+                              K, group, workspace, workspace_bytes, stream, true);
 }
 
 int w4a8_midgroup_gemm_ws(const void* a_hi, const void* a_lo, const void* a_scale, const void* a_ksum, int64_t Ma,

@@ -65,7 +65,22 @@ struct MidParams {
     int tpg;                   // 128-K tiles per group stride
     uint32_t a_bytes, w_bytes;
     bool isum;                 // K split over waves at tile granularity, int32 group sums in LDS
+    bool wtiles;               // w_q is w4a8_midgroup_tile_weights' layout (1 KB tiles), not [N, kpad/2]
 };
+
+// The weight's byte offset of lane (column col, quad q) in K tile 0, and the
+// stride of one K tile: rows as stored ([N, kpad/2], 64 bytes a tile), or the
+// tile layout ([col block][K tile][quad][column in block][16 bytes]: a
+// block's tile is 1 KB contiguous -- the same bytes, one 16-byte load per lane
+// either way).
+__device__ __forceinline__ uint32_t mid_woff(const MidParams& p, int col, int q) {
+    if (col >= p.N) return kOOBm;
+    if (p.wtiles)
+        return static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u +
+               (16u * static_cast<uint32_t>(q) + static_cast<uint32_t>(col & 15)) * 16u;
+    return static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 16u * static_cast<uint32_t>(q);
+}
+__device__ __forceinline__ uint32_t mid_wstep(const MidParams& p) { return p.wtiles ? 1024u : 64u; }
 
 template <int MT, int CPW, int KWMAX, int D, bool ASYM, bool DUMP>
 __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidParams p) {
@@ -120,7 +135,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
         const int col = (nb0 + c) * 16 + colq;
-        wo[c] = col < p.N ? static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 16u * q : kOOBm;
+        wo[c] = mid_woff(p, col, q);
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -135,7 +150,7 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
         // is half padding, the upper quads read zero weights
         const uint32_t base = static_cast<uint32_t>(min(t, p.KT - 1)) * 64u;
         const bool half = q >= 2 && (p.kpad - t * 128) < 128;
-        const auto rw = make_rsrc_at(p.w_q, base, t < tb ? p.w_bytes : 0u);
+        const auto rw = make_rsrc_at(p.w_q, static_cast<uint32_t>(min(t, p.KT - 1)) * mid_wstep(p), t < tb ? p.w_bytes : 0u);
         const auto rh = make_rsrc_at(p.a_hi, base, p.a_bytes);
         const auto rl = make_rsrc_at(p.a_lo, base, p.a_bytes);
 #pragma unroll
@@ -347,13 +362,12 @@ __global__ __launch_bounds__(64 * kShWaves) void gemm_midgroup_shared_kernel(con
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
         const int col = (nbw + wave * CPW + c) * 16 + colq;
-        wo[c] = col < p.N ? static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 16u * q : kOOBm;
+        wo[c] = mid_woff(p, col, q);
     }
     uint4 wb[D][CPW];
     auto load_w = [&](int s, int t) {
-        const uint32_t base = static_cast<uint32_t>(min(t, p.KT - 1)) * 64u;
         const bool half = q >= 2 && (p.kpad - t * 128) < 128;
-        const auto rw = make_rsrc_at(p.w_q, base, t < p.KT ? p.w_bytes : 0u);
+        const auto rw = make_rsrc_at(p.w_q, static_cast<uint32_t>(min(t, p.KT - 1)) * mid_wstep(p), t < p.KT ? p.w_bytes : 0u);
 #pragma unroll
         for (int c = 0; c < CPW; ++c) wb[s][c] = buf_load16(rw, half ? kOOBm : wo[c]);
     };
@@ -566,7 +580,36 @@ hipError_t launch_mt(const MidParams& p, int kw, hipStream_t stream) {
     return launch_mid<4, 4, ASYM, DUMP>(p, kw, stream);
 }
 
+// w_q [N, kpad/2] as stored -> the tile layout (one thread per 16 bytes of a
+// tile; columns past N and bytes past kpad/2 -- a last tile's padding half --
+// are zero).
+__global__ __launch_bounds__(256) void mid_tile_kernel(const uint8_t* __restrict__ wq, uint4* __restrict__ out, int64_t N,
+                                                      int64_t kb, int64_t KT, int64_t chunks) {
+    const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= chunks) return;
+    const int64_t tile = o >> 6;
+    const int l = static_cast<int>(o & 63);
+    const int64_t nb = tile / KT, kt = tile - nb * KT;
+    const int64_t col = nb * 16 + (l & 15);
+    const int64_t b = kt * 64 + 16 * (l >> 4);
+    out[o] = (col < N && b < kb) ? *reinterpret_cast<const uint4*>(wq + col * kb + b) : make_uint4(0u, 0u, 0u, 0u);
+}
+
 }  // namespace
+
+int64_t midgroup_tiles_bytes(int64_t N, int64_t K, int64_t group) {
+    return geom::col_blocks(N) * geom::k_tiles(K, group) * 1024;
+}
+
+hipError_t launch_midgroup_tile(const void* w_q, void* w_tiles, int64_t N, int64_t K, int64_t group,
+                                hipStream_t stream) {
+    const int64_t chunks = midgroup_tiles_bytes(N, K, group) / 16;
+    if (chunks > 0)
+        mid_tile_kernel<<<dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, stream>>>(
+            static_cast<const uint8_t*>(w_q), static_cast<uint4*>(w_tiles), N, geom::kpad(K, group) / 2,
+            geom::k_tiles(K, group), chunks);
+    return hipGetLastError();
+}
 
 int64_t midgroup_lds_bytes(int64_t Ma, int64_t K, int64_t group) {
     const int64_t mt = Ma <= 16 ? 1 : 4;
@@ -597,7 +640,9 @@ hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream) {
     p.NB = static_cast<int>(geom::col_blocks(a.N));
     p.tpg = static_cast<int>(geom::group_stride(a.group) / 128);
     p.a_bytes = static_cast<uint32_t>(a.Ma * static_cast<int64_t>(p.kb));
-    p.w_bytes = static_cast<uint32_t>(a.N * static_cast<int64_t>(p.kb));
+    p.wtiles = a.w_tiles;
+    p.w_bytes = static_cast<uint32_t>(a.w_tiles ? midgroup_tiles_bytes(a.N, a.K, a.group)
+                                                : a.N * static_cast<int64_t>(p.kb));
     // waves per workgroup: about two groups each, more for few column blocks
     const int64_t wgs = (p.NB + 1) / 2;
     const int kw = wgs >= 512 ? 1 : std::max(1, std::min(p.NG, static_cast<int>((p.NG + 1) / 2)));

@@ -104,6 +104,7 @@ struct PrefillParams {
     const uint16_t* c_wz;
     int ld_as, kb;
     uint32_t as_bytes, ak_bytes;
+    bool cwt;          // compat W in launch_midgroup_tile's 1 KB tiles instead of rows as stored
 };
 
 constexpr uint32_t kOOB = 0x80000000u;   // an offset past every buffer here (all below 2^31 bytes)
@@ -236,9 +237,18 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
         const int col = SWIGLU ? n0 + wn * 32 + c32 + j * p.half_n : n0 + wn * 64 + j * 32 + c32;
         colj[j] = col;
         if constexpr (RAWW) {
+            // the column's step bytes 32 hh .. +31: quads 2 hh and 2 hh + 1 of a
+            // compat tile (256 bytes apart), or 32 contiguous bytes of its row
             const bool in = col < p.N;
-            woff[j][0] = in ? static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 32u * hh : kOOB;
-            woff[j][1] = woff[j][0] + 16u;
+            if (p.cwt) {
+                woff[j][0] = in ? static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u +
+                                      (32u * hh + static_cast<uint32_t>(col & 15)) * 16u
+                                : kOOB;
+                woff[j][1] = woff[j][0] + 256u;
+            } else {
+                woff[j][0] = in ? static_cast<uint32_t>(col) * static_cast<uint32_t>(p.kb) + 32u * hh : kOOB;
+                woff[j][1] = woff[j][0] + 16u;
+            }
         } else {
             const uint32_t tile0 = static_cast<uint32_t>(col >> 4) * static_cast<uint32_t>(p.KT) * 1024u;
             woff[j][0] = tile0 + static_cast<uint32_t>((col & 15) + 16 * hh) * 16u;        // slabs 0, 2
@@ -272,7 +282,7 @@ __global__ __launch_bounds__(threads_for<BM>(), 2) void gemm_prefill_kernel(cons
 
     uint4 wr[DW][2][2];
     auto load_w = [&](int slot, int kt) {
-        const uint32_t t = static_cast<uint32_t>(min(kt, p.KT - 1)) * (RAWW ? 64u : 1024u);
+        const uint32_t t = static_cast<uint32_t>(min(kt, p.KT - 1)) * (RAWW && !p.cwt ? 64u : 1024u);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             wr[slot][j][0] = buf_load16(rw_rsrc, woff[j][0] + t);
@@ -995,7 +1005,7 @@ struct MidPrefillLayout {
     bool tiled;
 };
 
-MidPrefillLayout mid_prefill_layout(int64_t Ma, int64_t N, int64_t K, int64_t group) {
+MidPrefillLayout mid_prefill_layout(int64_t Ma, int64_t N, int64_t K, int64_t group, bool w_tiles = false) {
     MidPrefillLayout l{0, 0, 0, 0, false};
     const int64_t gs = geom::group_stride(group);
     if (Ma <= kMidPrefillMinRows || gs % 128 != 0 || gs < 256 || N <= 0 || K <= 0) return l;
@@ -1008,7 +1018,7 @@ MidPrefillLayout mid_prefill_layout(int64_t Ma, int64_t N, int64_t K, int64_t gr
     if ((Ma + 128) * lda >= lim || (N + 128) * kb >= lim || ng * (N + 128) * 2 >= lim || ng * Ma * 4 >= lim ||
         wt + 8 * geom::kTileBytes * KT >= lim)
         return l;
-    l.tiled = Ma >= W4A8_MID_TILED_MIN_ROWS;
+    l.tiled = !w_tiles && Ma >= W4A8_MID_TILED_MIN_ROWS;   // tiles given: read them, no repack
     l.a_off = 0;
     l.as_off = geom::ceil_to(Ma * lda, int64_t{256});
     l.wt_off = geom::ceil_to(l.as_off + ng * Ma * 4, int64_t{256});
@@ -1035,7 +1045,7 @@ int64_t midgroup_prefill_workspace_bytes(int64_t Ma, int64_t N, int64_t K, int64
 }
 
 hipError_t launch_gemm_midgroup_prefill(const MidgroupArgs& a, void* ws, int64_t ws_bytes, hipStream_t stream) {
-    const MidPrefillLayout l = mid_prefill_layout(a.Ma, a.N, a.K, a.group);
+    const MidPrefillLayout l = mid_prefill_layout(a.Ma, a.N, a.K, a.group, a.w_tiles);
     const int64_t ng = geom::num_groups(a.K, a.group);
     if (l.bytes == 0 || ws == nullptr || ws_bytes < l.bytes || a.partials != nullptr ||
         ng * a.ld_as * 4 >= (int64_t{1} << 31))
@@ -1051,6 +1061,7 @@ hipError_t launch_gemm_midgroup_prefill(const MidgroupArgs& a, void* ws, int64_t
     p.ld_as = static_cast<int>(a.ld_as);
     p.kb = static_cast<int>(geom::kpad(a.K, a.group) / 2);
     p.W = l.tiled ? reinterpret_cast<const uint4*>(w + l.wt_off) : static_cast<const uint4*>(a.w_q);
+    p.cwt = a.w_tiles;
     p.S = static_cast<const uint16_t*>(a.w_scale);
     p.Y = static_cast<uint16_t*>(a.y);
     p.ldy = a.ldy;
@@ -1068,7 +1079,7 @@ hipError_t launch_gemm_midgroup_prefill(const MidgroupArgs& a, void* ws, int64_t
     p.tiles_n = static_cast<int>(geom::ceil_div(a.N, int64_t{kBN}));
     p.band = 4;
     p.a_bytes = static_cast<uint32_t>(a.Ma * lda);
-    p.w_bytes = static_cast<uint32_t>(l.tiled ? p.NB * KT * geom::kTileBytes : a.N * p.kb);
+    p.w_bytes = static_cast<uint32_t>(l.tiled || a.w_tiles ? p.NB * KT * geom::kTileBytes : a.N * p.kb);
     p.s_bytes = static_cast<uint32_t>(ng * a.N * 2);
     p.as_bytes = static_cast<uint32_t>(ng * a.Ma * 4);
     p.ak_bytes = static_cast<uint32_t>(ng * a.ld_as * 4);

@@ -125,6 +125,7 @@ struct MidgroupArgs {
     int64_t ldy;
     void* partials;        // optional int32 [G, Ma, N]
     int64_t N, K, group;
+    bool w_tiles;          // w_q in launch_midgroup_tile's layout instead of [N, kpad/2]
 };
 // Bytes of LDS the staged scales need for one workgroup (the launch refuses
 // shapes above 64 KiB).
@@ -136,6 +137,11 @@ hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream);
 // no partial dump).  Outputs equal a one-wave-per-column-tile walk of
 // ReferenceMidGroupGemm's fold order.
 int64_t midgroup_prefill_workspace_bytes(int64_t Ma, int64_t N, int64_t K, int64_t group);
+// w_q [N, kpad/2] -> 1 KB tiles [ceil(N/16)][k_tiles][quad][column][16 bytes]
+// (the same bytes; every compat kernel reads either layout).
+int64_t midgroup_tiles_bytes(int64_t N, int64_t K, int64_t group);
+hipError_t launch_midgroup_tile(const void* w_q, void* w_tiles, int64_t N, int64_t K, int64_t group,
+                                hipStream_t stream);
 hipError_t launch_gemm_midgroup_prefill(const MidgroupArgs& a, void* ws, int64_t ws_bytes, hipStream_t stream);
 
 // RMSNorm (+ optional residual add) fused with the per-token quant.

@@ -29,6 +29,13 @@ reference's fixed value as default), its mid-group compat pair:
                                      K, group=1024, rows=-1) -> y   (rows >= 0: only the first rows)
     torch.ops.npu.midgroup_w4a8_gemm_partials(...) -> (y, partials)   (parity hook)
 
+and the same GEMM on a weight reordered once at load time (1 KB tiles, the
+same bytes; what the compat linear module and vLLM method keep):
+
+    torch.ops.npu.midgroup_tile_weights(w_q, K, group=1024) -> w_tiles
+    torch.ops.npu.midgroup_w4a8_gemm_tiled(a_hi, a_lo, a_scale, a_ksum, w_tiles, w_scale, w_ksum, w_zero,
+                                           N, K, group=1024, rows=-1) -> y
+
 Only the CUDA (= HIP on ROCm) dispatch key and fake (meta) kernels are
 registered: CPU tensors raise, there is no fallback path.  Each impl checks
 dtypes and shapes like the reference's host impls (TORCH_CHECK ->
@@ -69,6 +76,9 @@ _LIB.define("midgroup_w4a8_gemm(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor
             "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024, int rows=-1) -> Tensor")
 _LIB.define("midgroup_w4a8_gemm_partials(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_q, "
             "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int K, int group=1024) -> (Tensor, Tensor)")
+_LIB.define("midgroup_tile_weights(Tensor w_q, int K, int group=1024) -> Tensor")
+_LIB.define("midgroup_w4a8_gemm_tiled(Tensor a_hi, Tensor a_lo, Tensor a_scale, Tensor a_ksum, Tensor w_tiles, "
+            "Tensor w_scale, Tensor w_ksum, Tensor w_zero, int N, int K, int group=1024, int rows=-1) -> Tensor")
 
 _SCALE_DT = {torch.float16: _abi.W4A8_DT_F16, torch.bfloat16: _abi.W4A8_DT_BF16}
 
@@ -570,8 +580,16 @@ def _check_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K
 
 
 def _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, partials: bool,
-                  rows: int = -1):
-    M, N, G = _check_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group)
+                  rows: int = -1, tiles_n: int = -1):
+    if tiles_n >= 0:
+        # w_q holds midgroup_tile_weights' tiles of an [N, kpad/2] weight
+        nbytes = _abi.lib().w4a8_midgroup_tiles_bytes(tiles_n, K, group)
+        _require(w_q.dtype == torch.int8 and w_q.numel() == nbytes and w_q.is_contiguous(),
+                 f"midgroup_w4a8_gemm_tiled: w_tiles must be the {nbytes} int8 bytes of midgroup_tile_weights")
+        shape_ref = torch.empty((tiles_n, geo.kpad(K, group) // 2), dtype=torch.int8, device="meta")
+        M, N, G = _check_midgroup(a_hi, a_lo, a_scale, a_ksum, shape_ref, w_scale, w_ksum, w_zero, K, group)
+    else:
+        M, N, G = _check_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group)
     if rows >= 0:
         # the first `rows` rows only (the real rows before quant_a's padding):
         # the padding rows' activation planes are then never read
@@ -591,7 +609,8 @@ def _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, 
         # (npu_ops/host/midgroup_w4a8_gemm.cpp:116-118).
         need = 0 if partials else _abi.lib().w4a8_midgroup_gemm_workspace_bytes(M, N, K, group)
         ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
-        _abi.check(_abi.lib().w4a8_midgroup_gemm_ws(a_hi.data_ptr(), a_lo.data_ptr(), a_scale.data_ptr(),
+        entry = _abi.lib().w4a8_midgroup_gemm_tiled if tiles_n >= 0 else _abi.lib().w4a8_midgroup_gemm_ws
+        _abi.check(entry(a_hi.data_ptr(), a_lo.data_ptr(), a_scale.data_ptr(),
                                                     a_ksum.data_ptr(), M, a_scale.stride(0), w_q.data_ptr(),
                                                     w_scale.data_ptr(), w_zero.data_ptr(), y.data_ptr(), N,
                                                     P.data_ptr() if P is not None else None, N, K, group,
@@ -619,6 +638,40 @@ def _midgroup_gemm_fake(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zer
 def _midgroup_gemm_partials_cuda(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K: int,
                                  group: int = 1024):
     return _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_q, w_scale, w_ksum, w_zero, K, group, True)
+
+
+@torch.library.impl(_LIB, "midgroup_tile_weights", "CUDA")
+def _midgroup_tile_weights_cuda(w_q, K: int, group: int = 1024):
+    """w_q [N, kpad/2] -> the 1 KB tiles midgroup_w4a8_gemm_tiled reads (the same bytes)."""
+    _require(w_q.dim() == 2 and w_q.dtype == torch.int8, "midgroup_tile_weights: w_q must be int8 [N, kpad/2]")
+    _require(w_q.shape[1] == geo.kpad(K, group) // 2,
+             f"midgroup_tile_weights: packed row length must be Kpad/2 = {geo.kpad(K, group) // 2} for K={K}")
+    w_q = w_q.contiguous()
+    N = w_q.shape[0]
+    out = torch.empty(max(0, _abi.lib().w4a8_midgroup_tiles_bytes(N, K, group)), dtype=torch.int8, device=w_q.device)
+    if N:
+        _abi.check(_abi.lib().w4a8_midgroup_tile_weights(w_q.data_ptr(), out.data_ptr(), N, K, group,
+                                                         _stream(w_q.device)), "midgroup_tile_weights")
+    return out
+
+
+@torch.library.register_fake("npu::midgroup_tile_weights")
+def _midgroup_tile_weights_fake(w_q, K, group=1024):
+    N, KT = w_q.shape[0], -(-geo.kpad(K, group) // 128)
+    return w_q.new_empty(((N + 15) // 16 * KT * 1024,), dtype=torch.int8)
+
+
+@torch.library.impl(_LIB, "midgroup_w4a8_gemm_tiled", "CUDA")
+def _midgroup_gemm_tiled_cuda(a_hi, a_lo, a_scale, a_ksum, w_tiles, w_scale, w_ksum, w_zero, N: int, K: int,
+                              group: int = 1024, rows: int = -1):
+    """midgroup_w4a8_gemm on midgroup_tile_weights' tiles of the [N, kpad/2] weight: the same output bits."""
+    return _run_midgroup(a_hi, a_lo, a_scale, a_ksum, w_tiles, w_scale, w_ksum, w_zero, K, group, False, rows, N)
+
+
+@torch.library.register_fake("npu::midgroup_w4a8_gemm_tiled")
+def _midgroup_gemm_tiled_fake(a_hi, a_lo, a_scale, a_ksum, w_tiles, w_scale, w_ksum, w_zero, N, K, group=1024,
+                              rows=-1):
+    return a_scale.new_empty((a_hi.shape[0] if rows < 0 else rows, N), dtype=torch.bfloat16)
 
 
 @torch.library.register_fake("npu::midgroup_w4a8_gemm_partials")

@@ -174,20 +174,30 @@ class MidGroupW4A8LinearMethod(LinearMethodBase):
         layer.w4a8_k, layer.w4a8_n, layer.w4a8_group = k, n, group
 
     def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
-        """The per-group tensors [N, G] -> [G, N], the layout the GEMM reads (once)."""
+        """The per-group tensors [N, G] -> [G, N], the layout the GEMM reads, and the packed
+        weight -> midgroup_tile_weights' 1 KB tiles (the same bytes, read in whole tiles; the
+        rows as stored are released), once."""
         for name in ("weight_scale", "weight_zero", "weight_ksum"):
             t = getattr(layer, name).data.t().contiguous()
             delattr(layer, name)
             layer.register_parameter(name, torch.nn.Parameter(t, requires_grad=False))
-        layer.weight_packed = torch.nn.Parameter(layer.weight_packed.data.contiguous(), requires_grad=False)
+        if layer.weight_packed.is_cuda:
+            w_tiles = torch.ops.npu.midgroup_tile_weights(layer.weight_packed.data, layer.w4a8_k, layer.w4a8_group)
+            del layer.weight_packed
+            layer.register_parameter("w_tiles", torch.nn.Parameter(w_tiles, requires_grad=False))
 
     def apply(self, layer: torch.nn.Module, x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
         lead, k = x.shape[:-1], x.shape[-1]
         x2 = x.reshape(-1, k).to(torch.bfloat16).contiguous()
         rows = x2.shape[0]
         a_hi, a_lo, a_scale, a_ksum = torch.ops.npu.midgroup_quant_a(x2, layer.w4a8_group)
-        y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, layer.weight_packed, layer.weight_scale,
-                                             layer.weight_ksum, layer.weight_zero, k, layer.w4a8_group, rows)
+        if hasattr(layer, "w_tiles"):
+            y = torch.ops.npu.midgroup_w4a8_gemm_tiled(a_hi, a_lo, a_scale, a_ksum, layer.w_tiles, layer.weight_scale,
+                                                       layer.weight_ksum, layer.weight_zero, layer.w4a8_n, k,
+                                                       layer.w4a8_group, rows)
+        else:   # loaded off the GPU: the rows as stored (the same output bits)
+            y = torch.ops.npu.midgroup_w4a8_gemm(a_hi, a_lo, a_scale, a_ksum, layer.weight_packed, layer.weight_scale,
+                                                 layer.weight_ksum, layer.weight_zero, k, layer.w4a8_group, rows)
         if bias is not None:
             y = y + bias
         return y.reshape(*lead, layer.w4a8_n)
