@@ -1136,8 +1136,8 @@ def run_midgroup(pkg, dev, M, N, K, G, asym, seed):
 
 @pytest.mark.parametrize("M,N,K,G,asym", MIDGROUP_CASES)
 def test_midgroup_gemm_partials_bit_exact_and_output(pkg, dev, M, N, K, G, asym):
-    """int32 I_g = sum A*(W - wz) bit-exact; bf16 output against ReferenceMidGroupGemm's
-    fp32 order (the oracle restates it bit for bit), to the same bars as the main path."""
+    """int32 I_g = sum A*(W - wz) bit-exact; bf16 output equal to bf16 of ReferenceMidGroupGemm's
+    fp32 result (the oracle restates its order bit for bit), and within the main path's bars."""
     say(f"midgroup gemm M={M} N={N} K={K} G={G} asym={asym}")
     xb, codes, sc, zr, a, args, y, P = run_midgroup(pkg, dev, M, N, K, G, asym, seed=M + N + K)
     Mp = a[0].shape[0]
@@ -1150,13 +1150,15 @@ def test_midgroup_gemm_partials_bit_exact_and_output(pkg, dev, M, N, K, G, asym)
     y32 = ow.gemm_midgroup_fp32(qp, a_scale, codes, sc, zr, G, partials=P_ref)
     assert y.shape == (Mp, N)
     check_output(tensor_bf16_bits(y)[:M], y32[:M], f"midgroup M{M} N{N} K{K}", exact_mid(qp, a_scale, codes, sc, zr, G))
+    assert np.array_equal(tensor_bf16_bits(y)[:M], ow.f32_to_bf16_bits(y32[:M])), "not bf16 of the oracle's fp32 result"
     assert not tensor_bf16_bits(y)[M:].any() or np.all(ow.bf16_bits_to_f32(tensor_bf16_bits(y)[M:]) == 0)
 
 
 @pytest.mark.parametrize("proj", ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"])
 @pytest.mark.parametrize("M", [1, 16])
 def test_midgroup_qwq_decode_shapes(pkg, dev, proj, M):
-    """The reference's own decode configuration: group 1024 at QwQ-32B shapes."""
+    """The reference's own decode configuration: group 1024 at QwQ-32B shapes (partial dump
+    on: int32 partials and bf16 of the oracle's fp32 result, bit for bit)."""
     K, N = pkg.synth.QWQ_SHAPES[proj]
     say(f"midgroup qwq {proj} M={M}")
     xb, codes, sc, zr, a, args, y, P = run_midgroup(pkg, dev, M, N, K, 1024, True, seed=M)
@@ -1166,6 +1168,7 @@ def test_midgroup_qwq_decode_shapes(pkg, dev, proj, M):
     qp[:M] = q
     y32 = ow.gemm_midgroup_fp32(qp, tensor_bf16_bits(a[2]), codes, sc, zr, 1024)
     check_output(tensor_bf16_bits(y)[:M], y32[:M], f"midgroup {proj} M{M}", exact_mid(qp, tensor_bf16_bits(a[2]), codes, sc, zr, 1024))
+    assert np.array_equal(tensor_bf16_bits(y)[:M], ow.f32_to_bf16_bits(y32[:M])), "not bf16 of the oracle's fp32 result"
 
 
 MIDGROUP_PREFILL_CASES = [
@@ -1242,8 +1245,8 @@ def test_midgroup_prefill_qwq_shapes(pkg, dev, proj, M):
 def test_midgroup_decode_reference_order(pkg, dev, proj, M):
     """Decode rows at group 1024: the K split over waves adds exact int32 group sums and folds
     once in group order (or one wave walks every group), so the output is bf16 of the
-    reference's fp32 result bit for bit -- except where 64-row tiles' sums of many groups
-    exceed LDS (down_proj past 16 rows: the waves' fp32 sums are added, within the bar)."""
+    reference's fp32 result bit for bit -- down_proj past 16 rows included, whose 27 groups
+    of 64-row sums exceed the LDS and which takes 32-row tiles."""
     K, N = pkg.synth.QWQ_SHAPES[proj]
     say(f"midgroup decode order {proj} M={M}")
     xb, codes, sc, zr, a, args = _midgroup_inputs(pkg, dev, M, N, K, 1024, True, seed=31 + M)
@@ -1252,12 +1255,8 @@ def test_midgroup_decode_reference_order(pkg, dev, proj, M):
     q, _ = ow.quant_act_midgroup(xb, 1024)
     y32 = ow.gemm_midgroup_fp32(q, tensor_bf16_bits(a[2])[:, :M], codes, sc, zr, 1024)
     got = tensor_bf16_bits(y)
-    if proj == "down_proj" and M > 16:
-        check_output(got, y32, f"midgroup decode {proj} M{M}",
-                     exact_mid(q, tensor_bf16_bits(a[2]), codes, sc, zr, 1024))
-    else:
-        want = ow.f32_to_bf16_bits(y32)
-        assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} outputs differ"
+    want = ow.f32_to_bf16_bits(y32)
+    assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} outputs differ"
 
 
 def _tiles_ref(w_q: np.ndarray, KT: int) -> np.ndarray:
@@ -1308,6 +1307,86 @@ def test_midgroup_gemm_real_rows_equal_padded_rows(pkg, dev, M):
     assert torch.equal(y.view(torch.int16), y_pad[:M].view(torch.int16))
     with pytest.raises(RuntimeError, match="exceeds"):
         torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G, y_pad.shape[0] + 1)
+
+
+@pytest.mark.parametrize("M,N,K,G", [
+    (1, 5120, 27648, 128),     # 216 groups: one 16-row tile's staged values past 64 KiB
+    (16, 2048, 27648, 128),
+    (40, 1296, 12730, 128),    # 100 groups: 64-row tiles within 128 KiB
+    (64, 2048, 27648, 128),    # 216 groups: 16-row tiles (64 rows' values past 128 KiB)
+    (100, 700, 27648, 128),    # past 64 rows, off the prefill path: 16-row tiles
+    (33, 2000, 40000, 256),    # 157 groups
+])
+def test_midgroup_many_groups(pkg, dev, M, N, K, G):
+    """More groups than 64 KiB of staged row and column values hold (group 128 on down_proj's
+    K): int32 partials bit-exact, the output bf16 of the oracle's fp32 result bit for bit, and
+    the call without the dump returns the dump call's bits."""
+    say(f"midgroup many groups M={M} N={N} K={K} G={G}")
+    xb, codes, sc, zr, a, args, y, P = run_midgroup(pkg, dev, M, N, K, G, True, seed=M + N + K + G)
+    Mp = a[0].shape[0]
+    q, _ = ow.quant_act_midgroup(xb, G)
+    qp = np.zeros((Mp, K), np.int8)
+    qp[:M] = q
+    P_ref = ow.group_partials_asym(qp, codes, zr, G)
+    assert np.array_equal(P.cpu().numpy().astype(np.int64), P_ref), "int32 partials differ"
+    a_scale = tensor_bf16_bits(a[2])
+    y32 = ow.gemm_midgroup_fp32(qp, a_scale, codes, sc, zr, G, partials=P_ref)
+    got, want = tensor_bf16_bits(y)[:M], ow.f32_to_bf16_bits(y32[:M])
+    assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} outputs differ"
+    y_plain = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G)
+    torch.cuda.synchronize()
+    assert torch.equal(y_plain.view(torch.int16), y.view(torch.int16))
+
+
+def random_midgroup_shapes(seed: int, n: int, max_mnk: float = 2e9, max_gmn: float = 3e7):
+    """n seeded random (M, N, K, group, asym) draws for the compat GEMM: any N, K not a
+    multiple of the group, groups whose padded stride is a multiple of 128 (the path's
+    contract, 250 and 1000 among them), rows from one token to past the prefill path's
+    tile rule (the last third of the draws sized for it), up to 125 groups at decode rows
+    (past what the exact LDS group sums hold).  Capped so the oracle takes seconds."""
+    rng = np.random.default_rng(seed)
+    groups = [128, 250, 256, 384, 512, 640, 1000, 1024, 2048]
+    out = []
+    while len(out) < n:
+        G = int(rng.choice(groups))
+        u = rng.random()
+        if u < 0.4:
+            M, N, K = int(rng.integers(1, 65)), int(rng.integers(1, 9001)), int(rng.integers(1, 16001))
+        elif u < 0.67:
+            M, N, K = int(rng.integers(65, 700)), int(rng.integers(1, 3001)), int(rng.integers(1, 4001))
+        else:
+            M = int(rng.integers(256, 2600))
+            N = int(rng.integers((1 << 20) // M + 1, 5001))
+            K = int(rng.integers(1, 2001))
+        if M * N * K > max_mnk or ow.num_groups(K, G) * M * N > max_gmn or N * K > 4e7:
+            continue
+        out.append((M, N, K, G, bool(rng.random() < 0.75)))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,G,asym", random_midgroup_shapes(20261203, 12 * RANDOM_SCALE))
+def test_midgroup_random_shapes(pkg, dev, M, N, K, G, asym):
+    """Seeded random compat shapes through every plan the row count, width and group count
+    select.  On each: bf16 of the oracle's ReferenceMidGroupGemm fp32 result
+    (int4_cube_lab/host/gemm_ref.cpp:199-240) bit for bit -- every plan folds each output's
+    groups in order (one wave, or exact int32 group sums met in LDS, in chunks past what LDS
+    holds at once) -- and the GEMM on weight tiles equal to the GEMM on the stored rows."""
+    say(f"midgroup random M={M} N={N} K={K} G={G} asym={asym}")
+    xb, codes, sc, zr, a, args = _midgroup_inputs(pkg, dev, M, N, K, G, asym, seed=7 * M + N + K + G)
+    y = torch.ops.npu.midgroup_w4a8_gemm(*a, *args, K, G, M)
+    tiles = torch.ops.npu.midgroup_tile_weights(args[0], K, G)
+    yt = torch.ops.npu.midgroup_w4a8_gemm_tiled(*a, tiles, *args[1:], N, K, G, M)
+    torch.cuda.synchronize()
+    assert y.shape == (M, N)
+    assert torch.equal(yt.view(torch.int16), y.view(torch.int16)), "tiled weights differ from stored rows"
+    q, _ = ow.quant_act_midgroup(xb, G)
+    as_bits = tensor_bf16_bits(a[2])[:, :M]
+    y32 = ow.gemm_midgroup_fp32(q, as_bits, codes, sc, zr, G)
+    got = tensor_bf16_bits(y)
+    want = ow.f32_to_bf16_bits(y32)
+    path = "prefill" if pkg._abi.lib().w4a8_midgroup_gemm_workspace_bytes(M, N, K, G) > 0 else "mid-group"
+    assert np.array_equal(got, want), f"{path} path: {int((got != want).sum())} of {got.size} outputs differ"
+    assert np.abs(y32).max() > 0
 
 
 def test_midgroup_prefill_path_without_zero_points(pkg, dev):

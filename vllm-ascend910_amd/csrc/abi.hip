@@ -425,7 +425,7 @@ static int midgroup_gemm_impl(const void* a_hi, const void* a_lo, const void* a_
                         workspace_bytes);
         if (geom::num_groups(K, group) * ld_as * 4 >= (1ll << 31))
             return fail(W4A8_ERR_UNSUPPORTED, "ld_as=%lld: activation ksums too large for 32-bit offsets", ld_as);
-    } else if (midgroup_lds_bytes(Ma, K, group) > 64 * 1024) {
+    } else if (midgroup_lds_bytes(Ma, K, group) > midgroup_lds_max()) {
         return fail(W4A8_ERR_UNSUPPORTED, "K=%lld group=%lld: too many groups for the staged scales (%lld B LDS)", K,
                     group, midgroup_lds_bytes(Ma, K, group));
     }

@@ -65,6 +65,7 @@ struct MidParams {
     int tpg;                   // 128-K tiles per group stride
     uint32_t a_bytes, w_bytes;
     bool isum;                 // K split over waves at tile granularity, int32 group sums in LDS
+    int gchunk;                // isum: groups whose sums LDS holds at once (chunks of them, folded in turn)
     bool wtiles;               // w_q is w4a8_midgroup_tile_weights' layout (1 KB tiles), not [N, kpad/2]
 };
 
@@ -120,16 +121,23 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
         s_wz[e] = (ASYM && ok) ? bf16_bits_to_f32(p.w_zero[static_cast<int64_t>(g) * p.N + col]) : 0.0f;
     }
 
-    // This wave's tile range, in whole groups.
-    // p.isum: an even share of the K tiles, groups split between waves
-    // meeting in the int32 sums; otherwise whole groups.
-    const int ua = (wave * p.NG) / kw;
-    const int ub = ((wave + 1) * p.NG) / kw;
-    const int ta = p.isum ? (wave * p.KT) / kw : ua * p.tpg;
-    const int tb = p.isum ? ((wave + 1) * p.KT) / kw : min(p.KT, ub * p.tpg);
+    // This wave's tile range [ta, tb).  p.isum: an even share of the tiles of
+    // the current chunk of p.gchunk groups, groups split between waves meeting
+    // in the int32 sums; otherwise one wave walks every group (the host
+    // launches a single wave then).
+    int ta = 0, tb = 0;
+    auto share = [&](int T0, int T1) {
+        ta = T0 + (wave * (T1 - T0)) / kw;
+        tb = T0 + ((wave + 1) * (T1 - T0)) / kw;
+    };
+    const int gch = p.isum ? p.gchunk : p.NG;
+    share(0, min(p.KT, gch * p.tpg));
+    // [gch][R][C] int32 group sums, then (more than one chunk) the running
+    // fp32 fold [R][C] of each output, carried from chunk to chunk
     int* const isum = reinterpret_cast<int*>(red);
+    float* const accl = reinterpret_cast<float*>(isum + gch * R * C);
     if (p.isum)
-        for (int e = threadIdx.x; e < p.NG * R * C; e += blockDim.x) isum[e] = 0;
+        for (int e = threadIdx.x; e < gch * R * C; e += blockDim.x) isum[e] = 0;
 
     uint32_t wo[CPW], ao[MT];
 #pragma unroll
@@ -213,7 +221,9 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
         }
     };
 
-    if (tb > ta) {
+    // The wave's range [ta, tb); group g's sums go to chunk slot g - gbase.
+    auto run = [&](int gbase) __attribute__((always_inline)) {
+        if (tb <= ta) return;
 #pragma unroll
         for (int s = 0; s < D; ++s) load_slot(s, ta + s);
         for (int t0 = ta; t0 < tb; t0 += D) {
@@ -248,66 +258,63 @@ __global__ __launch_bounds__(64 * KWMAX) void gemm_midgroup_kernel(const MidPara
 #pragma unroll
                         for (int c = 0; c < CPW; ++c) P[mt][c] = mfma16(av[mt][h], bw[c][h], P[mt][c]);
                 if (p.isum) {
-                    if ((t + 1) % p.tpg == 0 || t == p.KT - 1 || t == tb - 1) flush(t / p.tpg);
+                    if ((t + 1) % p.tpg == 0 || t == p.KT - 1 || t == tb - 1) flush(t / p.tpg - gbase);
                 } else if ((t + 1) % p.tpg == 0 || t == p.KT - 1) {
                     fold(t / p.tpg, true);
                 }
             }
         }
-    }
+    };
 
     if (p.isum) {
-        // every group's int32 sum complete: the fold in group order, one
-        // output element per thread and step
+        // Chunk by chunk: every wave adds its share of the chunk's int32 group
+        // sums, then the fold in group order, one output element per thread
+        // and step (each element stays with one thread, so its running fold
+        // needs no barrier of its own)
 #pragma clang fp contract(off)
-        __syncthreads();
-        for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
-            const int r = e / C, cc = e - r * C;
-            const int row = m0 + r;
-            const int col = nb0 * 16 + cc;
-            if (row >= p.Ma || col >= p.N) continue;
-            float a = 0.0f;
-            for (int g = 0; g < p.NG; ++g) {
-                const int I = isum[(g * R + r) * C + cc] + (ASYM ? static_cast<int>(s_wz[g * C + cc]) * s_ak[g * R + r] : 0);
-                if constexpr (DUMP) p.P[(static_cast<int64_t>(g) * p.Ma + row) * p.N + col] = I;
-                const float t1 = static_cast<float>(I) * s_ws[g * C + cc];
-                a = a + t1 * s_as[g * R + r];
+        for (int g0 = 0; g0 < p.NG; g0 += gch) {
+            const int g1 = min(p.NG, g0 + gch);
+            if (g0 > 0) {
+                share(g0 * p.tpg, min(p.KT, g1 * p.tpg));
+                for (int e = threadIdx.x; e < (g1 - g0) * R * C; e += blockDim.x) isum[e] = 0;
+                __syncthreads();
             }
-            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(a));
+            run(g0);
+            __syncthreads();
+            const bool last = g1 == p.NG;
+            for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
+                const int r = e / C, cc = e - r * C;
+                const int row = m0 + r;
+                const int col = nb0 * 16 + cc;
+                if (row >= p.Ma || col >= p.N) continue;
+                float a = g0 == 0 ? 0.0f : accl[e];
+                for (int g = g0; g < g1; ++g) {
+                    const int I = isum[((g - g0) * R + r) * C + cc] +
+                                  (ASYM ? static_cast<int>(s_wz[g * C + cc]) * s_ak[g * R + r] : 0);
+                    if constexpr (DUMP) p.P[(static_cast<int64_t>(g) * p.Ma + row) * p.N + col] = I;
+                    const float t1 = static_cast<float>(I) * s_ws[g * C + cc];
+                    a = a + t1 * s_as[g * R + r];
+                }
+                if (last) p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(a));
+                else accl[e] = a;
+            }
+            if (!last) __syncthreads();   // the chunk's sums are read before the next chunk clears them
         }
         return;
     }
 
-    // Fixed-order reduction of the kw wave partials.
-    if (kw > 1) {
+    // one wave: every group folded in order in its registers
+    run(0);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int c = 0; c < CPW; ++c)
+        for (int c = 0; c < CPW; ++c)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) red[wave * R * C + (mt * 16 + rowq + i) * C + c * 16 + colq] = acc[mt][c][i];
-        __syncthreads();
-        for (int e = threadIdx.x; e < R * C; e += blockDim.x) {
-            const int r = e / C;
-            const int row = m0 + r;
-            const int col = nb0 * 16 + (e - r * C);
-            if (row >= p.Ma || col >= p.N) continue;
-            float sum = red[e];
-            for (int w = 1; w < kw; ++w) sum += red[w * R * C + e];
-            p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(sum));
-        }
-    } else {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int c = 0; c < CPW; ++c)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = m0 + mt * 16 + rowq + i, col = (nb0 + c) * 16 + colq;
-                    if (row < p.Ma && col < p.N)
-                        p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][c][i]));
-                }
-    }
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + mt * 16 + rowq + i, col = (nb0 + c) * 16 + colq;
+                if (row < p.Ma && col < p.N)
+                    p.Y[static_cast<int64_t>(row) * p.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][c][i]));
+            }
 }
 
 // Decode rows (Ma <= 16) on wide N: four waves of two column blocks each
@@ -492,47 +499,59 @@ hipError_t launch_mid(const MidParams& p0, int kw, hipStream_t stream) {
     constexpr int D = mid_depth(MT), KWM = kwmax_mid(MT, CPW);
     MidParams p = p0;
     p.isum = false;
-    // dynamic LDS stays within the 64 KiB a launch gets without a function
-    // attribute: the staged scales, then as many reduction slices as fit
+    p.gchunk = p.NG;
+    // dynamic LDS: the staged scales, then the int32 group sums of as many
+    // groups as fit (a slice each) and, past one chunk, the running fold
     const size_t staged = static_cast<size_t>(p.NG) * (2 * 16 * MT + 2 * 16 * CPW) * sizeof(float);
     const size_t slice = static_cast<size_t>(16 * MT) * 16 * CPW * sizeof(float);
     const dim3 grid(static_cast<unsigned>((p.NB + CPW - 1) / CPW), static_cast<unsigned>((p.Ma + 16 * MT - 1) / (16 * MT)));
     const int64_t wgs = static_cast<int64_t>(grid.x) * grid.y;
-    // Few workgroups: K split over waves, every wave adding its exact int32
-    // group sums in LDS, then one fold in group order -- the reference's fp32
-    // order, bit for bit, whatever the split (the fp32 sums of whole-group
-    // waves, added across waves, had put two down_proj outputs at 64 rows
-    // outside 1 bf16 ulp of the float64 value).  Tile granularity (about four
-    // tiles a wave) except on 9-16-row tiles, where whole groups per wave are
-    // faster (MI355X, qkv / o us, tiles against groups: 1 row 8.8 / 8.5 against
-    // 9.7 / 9.5, 16 rows 11.9 / 11.6 against 11.4 / 11.1, 64 rows 21.5 / 20.8
-    // against 22.5 / 21.9).
-    if (wgs < 512 && staged + p.NG * slice <= kMidLdsIsum) {
-        int w = MT == 1 && p.Ma > 8 ? std::min(p.NG, (p.NG + 1) / 2) : std::max(1, (p.KT + 3) / 4);
-        w = std::min(KWM, w);
+    // more than the default 64 KiB of dynamic LDS: the attribute, set once
+    auto allow_lds = [](size_t lds) -> hipError_t {
+        if (lds <= kMidLdsLimit) return hipSuccess;
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMidLdsIsum));
+        return attr;
+    };
+    if (staged + slice > kMidLdsIsum) return hipErrorInvalidValue;
+    // Waves per workgroup.  Few workgroups: K split at tile granularity
+    // (about four tiles a wave) except on 9-16-row tiles, where whole groups
+    // per wave are faster (MI355X, qkv / o us, tiles against groups: 1 row
+    // 8.8 / 8.5 against 9.7 / 9.5, 16 rows 11.9 / 11.6 against 11.4 / 11.1, 64
+    // rows 21.5 / 20.8 against 22.5 / 21.9); many workgroups: the caller's
+    // count (one from 512 column pairs), at most two on prefill tiles.
+    int w;
+    if (wgs < 512) {
+        w = MT == 1 && p.Ma > 8 ? std::min(p.NG, (p.NG + 1) / 2) : std::max(1, (p.KT + 3) / 4);
         if (CPW > 2) w = std::min(w, wgs >= 256 ? 2 : 4);
-        if (w > 1) {
+    } else {
+        w = std::min(kw, p.NG);
+        if (CPW > 2) w = std::min(w, wgs >= 1024 ? 1 : 2);
+    }
+    w = std::max(1, std::min(KWM, w));
+    if (w > 1) {
+        // Every wave adds its exact int32 group sums into LDS, after which the
+        // workgroup folds the groups once in order -- the reference's fp32
+        // order, bit for bit, whatever the split (the fp32 sums of whole-group
+        // waves, added across waves, had put outputs outside 1 bf16 ulp of the
+        // float64 value).  Groups whose sums do not fit at once go in chunks,
+        // each output's fold carried between them.
+        const size_t room = kMidLdsIsum - staged;
+        int gch = static_cast<int>(std::min<size_t>(p.NG, room / slice));
+        if (gch < p.NG) gch = static_cast<int>((room - slice) / slice);
+        if (gch >= 1) {
             p.isum = true;
-            const size_t lds = staged + p.NG * slice;
-            if (lds > kMidLdsLimit) {
-                static const hipError_t attr = hipFuncSetAttribute(
-                    reinterpret_cast<const void*>(&gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP>),
-                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMidLdsIsum));
-                if (attr != hipSuccess) return attr;
-            }
+            p.gchunk = gch;
+            const size_t lds = staged + static_cast<size_t>(gch + (gch < p.NG ? 1 : 0)) * slice;
+            if (const hipError_t e = allow_lds(lds); e != hipSuccess) return e;
             gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP><<<grid, dim3(64 * w), lds, stream>>>(p);
             return hipGetLastError();
         }
     }
-    if (staged + slice > kMidLdsLimit) return hipErrorInvalidValue;
-    const int wfit = static_cast<int>((kMidLdsLimit - staged) / slice);
-    if (CPW > 2) {
-        // prefill: split K over waves only while the grid is small
-        kw = std::min(kw, wgs >= 1024 ? 1 : wgs >= 256 ? 2 : 4);
-    }
-    const int w = std::max(1, std::min({kw, KWM, p.NG, wfit}));
-    const size_t lds = staged + static_cast<size_t>(w) * slice;
-    gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP><<<grid, dim3(64 * w), lds, stream>>>(p);
+    // one wave walks every group in order
+    if (const hipError_t e = allow_lds(staged); e != hipSuccess) return e;
+    gemm_midgroup_kernel<MT, CPW, KWM, D, ASYM, DUMP><<<grid, dim3(64), staged, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -558,6 +577,13 @@ hipError_t launch_shared(const MidParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// The staged values of an MT x 2 tile (16 MT rows, 32 columns) and one
+// wave's fp32 sums within the LDS a launch can get.
+bool mid_staged_fits(int64_t ng, int mt) {
+    return static_cast<size_t>(ng) * (2 * 16 * mt + 2 * 32) * sizeof(float) + 16 * mt * 32 * sizeof(float) <=
+           kMidLdsIsum;
+}
+
 // The int32 group sums of an MT x CPW tile fit the LDS beside the staged scales.
 bool mid_isum_fits(const MidParams& p, int mt, int cpw) {
     return static_cast<size_t>(p.NG) * (2 * 16 * mt + 2 * 16 * cpw + 16 * mt * 16 * cpw) * sizeof(float) <= kMidLdsIsum;
@@ -575,6 +601,8 @@ hipError_t launch_mt(const MidParams& p, int kw, hipStream_t stream) {
         const int64_t nb2 = (p.NB + 1) / 2;
         if (!mid_isum_fits(p, 4, 2) && mid_isum_fits(p, 2, 2) && nb2 * ((p.Ma + 31) / 32) < 512)
             return launch_mid<2, 2, ASYM, DUMP>(p, kw, stream);
+        // more groups than 64 rows' staged values leave room for: 16-row tiles
+        if (!mid_staged_fits(p.NG, 4)) return launch_mid<1, 2, ASYM, DUMP>(p, kw, stream);
         return launch_mid<4, 2, ASYM, DUMP>(p, kw, stream);
     }
     return launch_mid<4, 4, ASYM, DUMP>(p, kw, stream);
@@ -612,10 +640,12 @@ hipError_t launch_midgroup_tile(const void* w_q, void* w_tiles, int64_t N, int64
 }
 
 int64_t midgroup_lds_bytes(int64_t Ma, int64_t K, int64_t group) {
-    const int64_t mt = Ma <= 16 ? 1 : 4;
     const int64_t ng = geom::num_groups(K, group);
+    const int64_t mt = Ma <= 16 || !mid_staged_fits(ng, 4) ? 1 : 4;
     return (ng * (2 * 16 * mt + 2 * 32) + 16 * mt * 32) * 4;
 }
+
+int64_t midgroup_lds_max() { return static_cast<int64_t>(kMidLdsIsum); }
 
 hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream) {
     MidParams p{};

@@ -127,9 +127,11 @@ struct MidgroupArgs {
     int64_t N, K, group;
     bool w_tiles;          // w_q in launch_midgroup_tile's layout instead of [N, kpad/2]
 };
-// Bytes of LDS the staged scales need for one workgroup (the launch refuses
-// shapes above 64 KiB).
+// Bytes of LDS the staged scales need for one workgroup of the smallest tile
+// the rows take (16 rows up to 16 rows or where 64 rows' values do not fit),
+// and the most a launch gets (shapes above it are refused).
 int64_t midgroup_lds_bytes(int64_t Ma, int64_t K, int64_t group);
+int64_t midgroup_lds_max();
 hipError_t launch_gemm_midgroup(const MidgroupArgs& a, hipStream_t stream);
 // The same GEMM at prefill sizes on gemm_prefill_kernel's LDS-tiled waves
 // (gemm_prefill.hip): the activation planes rebuilt into a workspace of
