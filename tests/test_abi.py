@@ -238,8 +238,12 @@ def test_midgroup_workspace_sizes_and_rejects(lib):
     assert q(65, 8200, 3456, 256) == c256(65 * 3456) + 14 * 65 * 4
     assert q(1000, 7168, 5120, 1024) == c256(1000 * 5120) + 5 * 1000 * 4
     assert q(1024, 7168, 5120, 1024) == c256(c256(1024 * 5120) + 5 * 1024 * 4) + 448 * 40 * 1024
-    # the mid-group kernel keeps: up to 64 rows, 64-row tiles for fewer than half
+    # wide N from 17 rows (one row tile of 432 column tiles)
+    assert q(17, 55296, 5120, 1024) == c256(17 * 5120) + 5 * 17 * 4
+    assert q(64, 55296, 5120, 1024) == c256(64 * 5120) + 5 * 64 * 4
+    # the mid-group kernel keeps: up to 16 rows, 64-row tiles for fewer than half
     # the CUs, group stride 128 or not a multiple of 128, offsets past 2^31
+    assert q(16, 55296, 5120, 1024) == 0
     assert q(64, 7168, 5120, 1024) == 0
     assert q(128, 7168, 5120, 1024) == 0 and q(256, 7168, 5120, 1024) > 0
     assert q(4096, 7168, 5120, 128) == 0

@@ -1172,11 +1172,13 @@ def test_midgroup_qwq_decode_shapes(pkg, dev, proj, M):
 
 
 MIDGROUP_PREFILL_CASES = [
-    # (M, N, K, G, asym): past 64 rows with 64-row output tiles for at least half
+    # (M, N, K, G, asym): past 16 rows with 64-row output tiles for at least half
     # of 256 CUs (no partial dump), the compat GEMM runs the LDS-tiled prefill
     # waves on the activation rows rebuilt into a workspace; from 1024 rows on
     # weight tiles repacked there too
-    (65, 8200, 5120, 1024, True),      # the first row count on it; last column tile partial
+    (17, 16400, 1057, 1024, False),    # the first row count on it (wide N), ragged K
+    (40, 16400, 2048, 1024, True),     # one partial row tile
+    (65, 8200, 5120, 1024, True),      # last column tile partial
     (100, 8192, 1057, 1024, True),     # ragged K: the last step's upper half is padding
     (300, 3000, 5120, 1024, False),    # symmetric: zero point all 0
     (512, 2100, 3072, 1024, True),     # N not a multiple of 16

@@ -982,7 +982,10 @@ int64_t prefill_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; 
 // CUs: with fewer, the mid-group kernel's K split over waves is faster -- on
 // MI355X at 128 rows, qkv / o / down_proj 25.9 / 24.0 / 124 against 35.6 /
 // 33.0 / 149 us, gate_up 145 against 86 us; from 256 rows this path wins on
-// all four, 1.1-1.8x).  Workspace: the rebuilt activation rows,
+// all four, 1.1-1.8x).  Wide N meets the tile rule from one row tile on:
+// gate_up on weight tiles at 24 / 32 / 48 / 64 rows 43.6 / 43.8 / 45.3 / 46.6
+// against 54.2 / 64.7 / 76.8 / 97.7 us on the mid-group kernel, at 16 rows
+// 43.8 against 29.6 for its shared-activation kernel.  Workspace: the rebuilt activation rows,
 // then the fp32 activation scales, then (from W4A8_MID_TILED_MIN_ROWS rows)
 // the weight tiles repacked from w_q for this call, each 256-byte aligned.
 // Reading w_q as stored, a wave's 16-byte loads cover 32 columns' half lines
@@ -993,7 +996,10 @@ int64_t prefill_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; 
 // repack included; bench graph replays): 1024 rows 67 / 62 / 450 / 288
 // against 74 / 60 / 504 / 302; 4096 rows 218 / 158 / 1423 / 746 against 248 /
 // 175 / 1646 / 805 (at 512 rows the stored weights were ahead).
-constexpr int64_t kMidPrefillMinRows = 64;
+#ifndef W4A8_MID_PREFILL_MIN_ROWS
+#define W4A8_MID_PREFILL_MIN_ROWS 16
+#endif
+constexpr int64_t kMidPrefillMinRows = W4A8_MID_PREFILL_MIN_ROWS;
 #ifndef W4A8_MID_TILED_MIN_ROWS
 #define W4A8_MID_TILED_MIN_ROWS 1024
 #endif
