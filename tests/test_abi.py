@@ -261,3 +261,12 @@ def test_midgroup_workspace_sizes_and_rejects(lib):
     assert call(4096 + 16, need) == 6                 # not 256-byte aligned
     assert call(4096, -1) == 6
     assert call(4096, need, ld_as=64) == 2            # ld_as < rows
+
+
+def test_midgroup_group_count_limit(lib):
+    """The compat kernel stages every group's row and column values in at most 128 KiB of
+    LDS (16-row tiles where 64 rows' values do not fit: about 330 groups): 782 groups at
+    K=100000, group 128 are refused before any launch, at one row and at 64."""
+    for Ma in (1, 64):
+        rc = lib.w4a8_midgroup_gemm(16, 16, 16, 16, Ma, Ma, 16, 16, 16, 16, 16, None, 16, 100000, 128, None)
+        assert rc == 5 and b"too many groups" in lib.w4a8_last_error()
