@@ -366,9 +366,13 @@ int w4a8_midgroup_quant_a(const void* x, int64_t ldx, void* a_hi, void* a_lo, vo
  *   y        bf16  [Ma, ldy]
  *   partials int32 [G, Ma, N]     optional: I_g = sum_{k in g} A*(W - wz), exact
  *   y[m,n] = bf16( sum_g (float(I_g[m,n]) * w_scale[g,n]) * a_scale[g,m] )
- * (the reference's CPU definition, int4_cube_lab/host/gemm_ref.cpp:199-240).  The
+ * (the reference's CPU definition, int4_cube_lab/host/gemm_ref.cpp:199-240),
+ * each product and sum rounded in that order and the groups added in order, so
+ * y is bf16 of ReferenceMidGroupGemm's fp32 result bit for bit.  The
  * reference kernel's w_ksum input is not needed: the activation bytes are
- * rebuilt exactly from the two planes.  Needs ceil_to(group, 64) % 128 == 0.
+ * rebuilt exactly from the two planes.  Needs ceil_to(group, 64) % 128 == 0
+ * and at most about 330 groups (every group's row and column values are staged
+ * in LDS; more is W4A8_ERR_UNSUPPORTED).
  * Replaces npu_ops/kernel/midgroup_w4a8_gemm.inc:491-1169 bound by
  * npu_ops/host/midgroup_w4a8_gemm.cpp:45-140 (run_midgroup_w4a8_gemm).
  */
