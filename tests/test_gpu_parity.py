@@ -1099,6 +1099,52 @@ def test_midgroup_quant_a_byte_exact(pkg, dev, M, K, G):
         assert np.array_equal(gn.view(e.dtype) if gn.dtype != e.dtype else gn, e), f"{name} differs"
 
 
+@pytest.mark.parametrize("M,K,G", [(2500, 27648, 1024), (2300, 30000, 1000)])
+def test_midgroup_quant_a_large_calls(pkg, dev, M, K, G):
+    """Past 64k (row, group) workgroups the quant takes four rows per workgroup (the last
+    one holding padded rows past M): all four tensors byte-exact, ragged groups included."""
+    say(f"midgroup quant_a large M={M} K={K} G={G}")
+    xb = pkg.synth.activations(M, K, seed=M + K)
+    got = torch.ops.npu.midgroup_quant_a(bf16_bits_tensor(xb).to(dev), G)
+    torch.cuda.synchronize()
+    assert got[0].shape[0] * ow.num_groups(K, G) > 65536
+    exp = ow.midgroup_quant_a(xb, G)
+    for name, g, e in zip(("a_hi", "a_lo", "a_scale", "a_ksum"), got, exp):
+        gn = tensor_bf16_bits(g) if g.dtype == torch.bfloat16 else g.cpu().numpy()
+        assert gn.shape == e.shape, f"{name} shape {gn.shape} vs {e.shape}"
+        assert np.array_equal(gn.view(e.dtype) if gn.dtype != e.dtype else gn, e), f"{name} differs"
+
+
+@pytest.mark.parametrize("G", [1000, 250])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_midgroup_quant_a_ties_zero_and_tiny_groups(pkg, dev, G, offset):
+    """midgroup_quant_a on a group whose quotients x/s are all exact half-integers (s = 0.5,
+    round half to even), an all-zero row (tiny scale), a row of subnormal-range scales (the
+    divide path) and random rows; group 250 and a source shifted by one element put the
+    16-byte chunks off alignment: all four tensors byte-exact."""
+    say(f"midgroup quant_a ties G={G} offset={offset}")
+    M, K = 6, 3000
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((M, K + 1)).astype(np.float32)
+    odd = rng.choice(np.arange(-253, 254, 2), size=K + 1).astype(np.float32)
+    x[0] = odd * 0.25                      # x / s = odd / 2 with s = bf16(63.5 / 127) = 0.5
+    x[0, ::97] = 63.5                      # every group's absmax
+    x[1] = 0.0
+    x[2] = rng.standard_normal(K + 1).astype(np.float32) * 1e-38
+    xb_all = ow.f32_to_bf16_bits(x)
+    src = bf16_bits_tensor(xb_all).to(dev)[:, offset:offset + K]
+    got = torch.ops.npu.midgroup_quant_a(src, G)
+    torch.cuda.synchronize()
+    exp = ow.midgroup_quant_a(np.ascontiguousarray(xb_all[:, offset:offset + K]), G)
+    names = ("a_hi", "a_lo", "a_scale", "a_ksum")
+    for name, g, e in zip(names, got, exp):
+        gn = tensor_bf16_bits(g) if g.dtype == torch.bfloat16 else g.cpu().numpy()
+        assert gn.shape == e.shape, f"{name} shape {gn.shape} vs {e.shape}"
+        assert np.array_equal(gn.view(e.dtype) if gn.dtype != e.dtype else gn, e), f"{name} differs"
+    s_row0 = ow.bf16_bits_to_f32(exp[2][:, 0])
+    assert np.all(s_row0 == 0.5), "row 0 is not on the half-integer scale"
+
+
 MIDGROUP_CASES = [
     # (M, N, K, G, asym)
     (1, 512, 5120, 1024, True),
