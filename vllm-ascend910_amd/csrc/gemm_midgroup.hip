@@ -24,9 +24,11 @@
 // order: (float(I) * ws) * as, added to the accumulator group by group.
 //
 // Work split as in the decode kernel: a workgroup owns CPW column blocks of 16
-// and a block of 16*MT rows (grid.y walks row blocks), its KW waves split K at
-// group boundaries and are reduced through LDS in a fixed order (prefill
-// shapes: 64 x 64 tiles, K split only while the grid is small).  The
+// and a block of 16*MT rows (grid.y walks row blocks); its KW waves split K
+// and add their exact int32 group sums into LDS, after which the workgroup
+// folds the groups in order (in chunks of groups when their sums exceed the
+// LDS), or a single wave walks all of K (prefill shapes: 64 x 64 tiles, K
+// split only while the grid is small).  The
 // activation scales and ksums of the workgroup's rows, and the weight scales
 // and zero points of its columns, are staged in LDS once.  All global reads are
 // raw buffer loads; rows and columns past the tensors, and the K tail past
