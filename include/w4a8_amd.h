@@ -384,10 +384,9 @@ int w4a8_midgroup_gemm(const void* a_hi, const void* a_lo, const void* a_scale, 
  * The same GEMM with a caller-owned workspace, as the reference host allocates
  * its GEMM workspace per call (npu_ops/host/midgroup_w4a8_gemm.cpp:116-118).
  * Where w4a8_midgroup_gemm_workspace_bytes(Ma, N, K, group) is non-zero (more
- * than 16 rows whose 64-row output tiles, two per 128 columns, number at least
- * the CU count, group stride ceil_to(group, 64) a multiple of 128 and at
- * least 256, offsets below 2^31) and no partials are asked for, a call with
- * workspace_bytes > 0
+ * than 16 rows whose 64 x 128 output tiles number at least half the CU count,
+ * group stride ceil_to(group, 64) a multiple of 128 and at least 256, offsets
+ * below 2^31) and no partials are asked for, a call with workspace_bytes > 0
  * rebuilds the activation bytes from the two planes into the workspace
  * (256-byte aligned, at least that many bytes; W4A8_ERR_WORKSPACE otherwise)
  * and runs the LDS-tiled prefill kernel on w_q as stored.  Every output is the
